@@ -1,0 +1,192 @@
+// C ABI of the EPTQ gfx950 library (declarations and contract: include/eptq_hip.h).
+//
+// Host-side validation mirrors and extends the reference dispatcher's checks
+// (csrc/eptq_kernels.cu:478-494): null pointers, sizes, alignment of every
+// 16-byte vector operand, S_group group size, then a launch and a
+// hipGetLastError check.
+
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "eptq_hip.h"
+#include "kernels.h"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+int check_launch(const char* what) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(EPTQ_EHIP, "%s: %s", what, hipGetErrorString(e));
+  return EPTQ_OK;
+}
+
+int check_common(const char* fn, const void* Q, const void* codes, const void* g,
+                 const void* h, const void* O_vals, const void* O_col,
+                 const void* O_row_ptr, const void* S_group, int n_groups, int M, int N,
+                 int* qb) {
+  if (!Q || !codes || !g || !h || !O_row_ptr)
+    return fail(EPTQ_EINVAL, "%s: null Q/codes/g/h/O_row_ptr", fn);
+  if (M <= 0 || N <= 0) return fail(EPTQ_EINVAL, "%s: M=%d N=%d must be positive", fn, M, N);
+  if ((int64_t)M * 8 > 0x7fffffff) return fail(EPTQ_EINVAL, "%s: M=%d too large", fn, M);
+  if ((!O_vals || !O_col) && (O_vals || O_col))
+    return fail(EPTQ_EINVAL, "%s: O_vals and O_col must both be given or both be null", fn);
+  if (O_vals && !aligned16(O_vals))
+    return fail(EPTQ_EUNSUPPORTED, "%s: O_vals must be 16-byte aligned", fn);
+  *qb = 1;
+  if (S_group) {
+    if (n_groups <= 0 || (8 * M) % n_groups != 0)
+      return fail(EPTQ_EINVAL, "%s: n_groups=%d must divide out_features=%d", fn, n_groups, 8 * M);
+    *qb = (8 * M) / n_groups;
+    if (*qb % 8 != 0)
+      return fail(EPTQ_EUNSUPPORTED, "%s: group size %d is not a multiple of 8", fn, *qb);
+  }
+  return EPTQ_OK;
+}
+
+int linear_common(int kind, const void* Q, const void* codes, int codes_dtype, const void* g,
+                  const void* h, const void* x, int x_dtype, const void* O_vals,
+                  const void* O_col, const void* O_row_ptr, const void* bias,
+                  const void* S_group, int n_groups, int M, int N, int B, void* y,
+                  void* stream) {
+  const char* fn = kind == eptq::KIND_E8D4 ? "eptq_e8d4_forward" : "eptq_e8_forward";
+  int qb = 1;
+  int rc = check_common(fn, Q, codes, g, h, O_vals, O_col, O_row_ptr, S_group, n_groups, M, N, &qb);
+  if (rc) return rc;
+  if (B < 0) return fail(EPTQ_EINVAL, "%s: B=%d", fn, B);
+  if (B == 0) return EPTQ_OK;
+  if (!x || !y) return fail(EPTQ_EINVAL, "%s: null x/y", fn);
+  if (codes_dtype != EPTQ_F16 && codes_dtype != EPTQ_F32)
+    return fail(EPTQ_EINVAL, "%s: codes_dtype must be EPTQ_F16 or EPTQ_F32", fn);
+  if (x_dtype != EPTQ_F16 && x_dtype != EPTQ_BF16)
+    return fail(EPTQ_EINVAL, "%s: x_dtype must be EPTQ_F16 or EPTQ_BF16", fn);
+  if (N % 8 != 0) return fail(EPTQ_EUNSUPPORTED, "%s: in_features=%d not a multiple of 8", fn, N);
+  if (!aligned16(Q) || !aligned16(x) || !aligned16(h) || (S_group && !aligned16(S_group)))
+    return fail(EPTQ_EUNSUPPORTED, "%s: Q, x, h and S_group must be 16-byte aligned", fn);
+  if (kind == eptq::KIND_E8 && !aligned16(codes))
+    return fail(EPTQ_EUNSUPPORTED, "%s: E8 codebook must be 16-byte aligned", fn);
+
+  eptq::LinearArgs a;
+  a.Q = (const int16_t*)Q;
+  a.codes = codes;
+  a.codes_f32 = codes_dtype == EPTQ_F32;
+  a.g = (const eptq::f16*)g;
+  a.h = (const eptq::f16*)h;
+  a.x = (const uint16_t*)x;
+  a.x_bf16 = x_dtype == EPTQ_BF16;
+  a.O = (const eptq::f16*)O_vals;
+  a.O_col = (const int32_t*)O_col;
+  a.O_row_ptr = (const int32_t*)O_row_ptr;
+  a.bias = (const eptq::f16*)bias;
+  a.S = (const eptq::f16*)S_group;
+  a.qb = qb;
+  a.M = M;
+  a.N = N;
+  a.B = B;
+  a.y = (uint16_t*)y;
+  hipStream_t s = (hipStream_t)stream;
+
+  if (B <= eptq::kMatvecMaxBatch) {
+    rc = kind == eptq::KIND_E8D4 ? eptq::launch_matvec<eptq::KIND_E8D4>(a, s)
+                                 : eptq::launch_matvec<eptq::KIND_E8>(a, s);
+  } else if (kind == eptq::KIND_E8D4) {
+    rc = eptq::launch_gemm_e8d4(a, s);
+  } else {
+    // E8 at large batch: batch tiles through the decode matvec.
+    for (int b0 = 0; b0 < B && rc == 0; b0 += eptq::kMatvecMaxBatch) {
+      eptq::LinearArgs t = a;
+      t.B = B - b0 < eptq::kMatvecMaxBatch ? B - b0 : eptq::kMatvecMaxBatch;
+      t.x = a.x + (size_t)b0 * N;
+      t.y = a.y + (size_t)b0 * 8 * M;
+      rc = eptq::launch_matvec<eptq::KIND_E8>(t, s);
+    }
+  }
+  if (rc) return fail(EPTQ_EUNSUPPORTED, "%s: no kernel for M=%d N=%d B=%d", fn, M, N, B);
+  return check_launch(fn);
+}
+
+int dequant_common(int kind, const void* Q, const void* codes_f32, const void* g,
+                   const void* h, const void* O_vals, const void* O_col,
+                   const void* O_row_ptr, const void* S_group, int n_groups, int M, int N,
+                   void* W, void* stream) {
+  const char* fn = kind == eptq::KIND_E8D4 ? "eptq_e8d4_dequant" : "eptq_e8_dequant";
+  int qb = 1;
+  int rc = check_common(fn, Q, codes_f32, g, h, O_vals, O_col, O_row_ptr, S_group, n_groups, M,
+                        N, &qb);
+  if (rc) return rc;
+  if (!W) return fail(EPTQ_EINVAL, "%s: null W", fn);
+  if (!aligned16(codes_f32)) return fail(EPTQ_EUNSUPPORTED, "%s: table must be 16-byte aligned", fn);
+  if ((N & 3) == 0 && ((uintptr_t)W & 7u))
+    return fail(EPTQ_EUNSUPPORTED, "%s: W must be 8-byte aligned", fn);
+  eptq::DequantArgs a;
+  a.Q = (const int16_t*)Q;
+  a.table = (const float*)codes_f32;
+  a.g = (const eptq::f16*)g;
+  a.h = (const eptq::f16*)h;
+  a.O = (const eptq::f16*)O_vals;
+  a.O_col = (const int32_t*)O_col;
+  a.O_row_ptr = (const int32_t*)O_row_ptr;
+  a.S = (const eptq::f16*)S_group;
+  a.qb = qb;
+  a.M = M;
+  a.N = N;
+  a.W = (eptq::f16*)W;
+  hipStream_t s = (hipStream_t)stream;
+  rc = kind == eptq::KIND_E8D4 ? eptq::launch_dequant<eptq::KIND_E8D4>(a, s)
+                               : eptq::launch_dequant<eptq::KIND_E8>(a, s);
+  if (rc) return fail(EPTQ_EUNSUPPORTED, "%s: layer too large (M=%d N=%d)", fn, M, N);
+  return check_launch(fn);
+}
+
+}  // namespace
+
+extern "C" {
+
+int eptq_abi_version(void) { return 1; }
+
+const char* eptq_last_error(void) { return g_err; }
+
+int eptq_e8d4_forward(const void* Q, const void* codes, int codes_dtype, const void* g,
+                      const void* h, const void* x, int x_dtype, const void* O_vals,
+                      const void* O_col, const void* O_row_ptr, const void* bias,
+                      const void* S_group, int n_groups, int M, int N, int B, void* y,
+                      void* stream) {
+  return linear_common(eptq::KIND_E8D4, Q, codes, codes_dtype, g, h, x, x_dtype, O_vals, O_col,
+                       O_row_ptr, bias, S_group, n_groups, M, N, B, y, stream);
+}
+
+int eptq_e8_forward(const void* Q, const void* codes, int codes_dtype, const void* g,
+                    const void* h, const void* x, int x_dtype, const void* O_vals,
+                    const void* O_col, const void* O_row_ptr, const void* bias,
+                    const void* S_group, int n_groups, int M, int N, int B, void* y,
+                    void* stream) {
+  return linear_common(eptq::KIND_E8, Q, codes, codes_dtype, g, h, x, x_dtype, O_vals, O_col,
+                       O_row_ptr, bias, S_group, n_groups, M, N, B, y, stream);
+}
+
+int eptq_e8d4_dequant(const void* Q, const void* codes_f32, const void* g, const void* h,
+                      const void* O_vals, const void* O_col, const void* O_row_ptr,
+                      const void* S_group, int n_groups, int M, int N, void* W, void* stream) {
+  return dequant_common(eptq::KIND_E8D4, Q, codes_f32, g, h, O_vals, O_col, O_row_ptr, S_group,
+                        n_groups, M, N, W, stream);
+}
+
+int eptq_e8_dequant(const void* Q, const void* codes_f32, const void* g, const void* h,
+                    const void* O_vals, const void* O_col, const void* O_row_ptr,
+                    const void* S_group, int n_groups, int M, int N, void* W, void* stream) {
+  return dequant_common(eptq::KIND_E8, Q, codes_f32, g, h, O_vals, O_col, O_row_ptr, S_group,
+                        n_groups, M, N, W, stream);
+}
+
+}  // extern "C"

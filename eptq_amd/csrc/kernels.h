@@ -1,0 +1,52 @@
+// Internal launch interface between the C ABI (abi.hip) and the kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "common.h"
+
+namespace eptq {
+
+enum { KIND_E8D4 = 0, KIND_E8 = 1 };
+
+struct DequantArgs {
+  const int16_t* Q;
+  const float* table;
+  const f16* g;
+  const f16* h;
+  const f16* O;
+  const int32_t* O_col;
+  const int32_t* O_row_ptr;
+  const f16* S;   // nullable
+  int qb;
+  int M, N;
+  f16* W;
+};
+
+struct LinearArgs {
+  const int16_t* Q;
+  const void* codes;
+  int codes_f32;        // table element type: 1 fp32, 0 fp16
+  const f16* g;
+  const f16* h;
+  const uint16_t* x;    // fp16 or bf16 words
+  int x_bf16;
+  const f16* O;
+  const int32_t* O_col;
+  const int32_t* O_row_ptr;
+  const f16* bias;      // nullable
+  const f16* S;         // nullable
+  int qb;
+  int M, N, B;
+  uint16_t* y;          // same element type as x
+};
+
+template <int KIND> int launch_dequant(const DequantArgs& a, hipStream_t s);
+template <int KIND> int launch_matvec(const LinearArgs& a, hipStream_t s);
+int launch_gemm_e8d4(const LinearArgs& a, hipStream_t s);
+
+// Largest batch served by the decode matvec; larger batches take the GEMM.
+constexpr int kMatvecMaxBatch = 16;
+
+}  // namespace eptq

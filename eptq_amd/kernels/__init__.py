@@ -1,0 +1,188 @@
+"""EPTQ HIP kernels as ``torch.library`` custom ops.
+
+Drop-in for the reference's ``kernels/__init__.py:50-91``: the ops
+``eptq::e8_forward`` and ``eptq::e8d4_forward`` keep their names, argument
+order and meaning ``(Q, codebook, g, h, x, O_vals, O_col, O_row_ptr, bias)``
+(an empty ``bias`` means no bias) and have fake implementations for
+``torch.compile``.  They run the gfx950 kernels of ``libeptq_hip.so`` through
+its C ABI on the current HIP stream; there is no CPU or PyTorch fallback.
+
+Additions over the reference: fp32 tables are accepted (the kernels convert),
+bf16 activations give bf16 outputs, ``*_grouped`` variants take ``S_group``
+(the reference materializes an fp16 W instead, ``kernels/linear.py:97-120``),
+and ``eptq::e8d4_dequant`` / ``eptq::e8_dequant`` produce the bit-exact fp16 W of
+``dequantize_layer`` (``algorithms/eptq.py:406-471``) on the GPU.
+"""
+
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+from . import _lib
+from ._lib import EPTQ_BF16, EPTQ_F16, EPTQ_F32, EptqError
+
+__all__ = ["e8_forward", "e8d4_forward", "e8_forward_grouped", "e8d4_forward_grouped",
+           "e8_dequant", "e8d4_dequant", "EptqError", "linear_forward", "dequant"]
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    if t is None or t.numel() == 0:
+        return None
+    return t.data_ptr()
+
+
+def _require(cond: bool, msg: str) -> None:
+    if not cond:
+        raise RuntimeError(msg)
+
+
+def _check_layer(kind, Q, codes, g, h, O_vals, O_col, O_row_ptr, S_group):
+    _require(Q.is_cuda, "Q must be a CUDA (HIP) tensor")
+    dev = Q.device
+    _require(Q.dtype == torch.int16 and Q.dim() == 2 and Q.is_contiguous(),
+             "Q must be a contiguous 2-D int16 tensor")
+    M, N = Q.shape
+    for name, t, dt in (("g", g, torch.float16), ("h", h, torch.float16),
+                        ("O_vals", O_vals, torch.float16), ("O_col", O_col, torch.int32),
+                        ("O_row_ptr", O_row_ptr, torch.int32)):
+        _require(t.device == dev, f"{name} must be on {dev}")
+        _require(t.dtype == dt, f"{name} must be {dt}, got {t.dtype}")
+        _require(t.is_contiguous(), f"{name} must be contiguous")
+    _require(g.numel() == 8 * M, f"g must have {8 * M} elements")
+    _require(h.numel() == N, f"h must have {N} elements")
+    _require(O_row_ptr.numel() == M + 1, f"O_row_ptr must have {M + 1} elements")
+    _require(O_vals.numel() == 8 * O_col.numel(), "O_vals must be (nnz, 8) with nnz = len(O_col)")
+    _require(codes.device == dev and codes.is_contiguous(), "codebook must be contiguous on the layer's device")
+    _require(codes.dtype in (torch.float16, torch.float32), "codebook must be fp16 or fp32")
+    rows = 512 if kind == "e8_d4" else 65535
+    _require(codes.numel() == rows * (4 if kind == "e8_d4" else 8),
+             f"{kind} codebook must have {rows} rows")
+    n_groups = 0
+    if S_group is not None:
+        _require(S_group.device == dev and S_group.dtype == torch.float16 and S_group.is_contiguous(),
+                 "S_group must be a contiguous fp16 tensor on the layer's device")
+        _require(S_group.dim() == 2 and S_group.shape[1] == N, "S_group must be (n_groups, in_features)")
+        n_groups = int(S_group.shape[0])
+    return M, N, n_groups
+
+
+def linear_forward(kind: str, Q, codes, g, h, x, O_vals, O_col, O_row_ptr, bias=None,
+                   S_group=None) -> torch.Tensor:
+    """Run the fused quantized Linear on ``x`` (B, N) -> (B, 8M), dtype of x."""
+    M, N, n_groups = _check_layer(kind, Q, codes, g, h, O_vals, O_col, O_row_ptr, S_group)
+    _require(x.device == Q.device, "x must be on the layer's device")
+    _require(x.dim() == 2 and x.shape[1] == N, f"x must be (B, {N})")
+    _require(x.dtype in (torch.float16, torch.bfloat16), "x must be fp16 or bf16")
+    _require(x.is_contiguous(), "x must be contiguous")
+    if bias is not None and bias.numel() > 0:
+        _require(bias.device == Q.device and bias.dtype == torch.float16 and bias.numel() == 8 * M
+                 and bias.is_contiguous(), "bias must be a contiguous fp16 (out_features,) tensor")
+    B = int(x.shape[0])
+    y = torch.empty((B, 8 * M), dtype=x.dtype, device=x.device)
+    if B == 0:
+        return y
+    lib = _lib.load()
+    fn = lib.eptq_e8d4_forward if kind == "e8_d4" else lib.eptq_e8_forward
+    with torch.cuda.device(x.device):
+        stream = torch.cuda.current_stream().cuda_stream
+        rc = fn(_ptr(Q), _ptr(codes), EPTQ_F32 if codes.dtype == torch.float32 else EPTQ_F16,
+                _ptr(g), _ptr(h), _ptr(x), EPTQ_BF16 if x.dtype == torch.bfloat16 else EPTQ_F16,
+                _ptr(O_vals), _ptr(O_col), _ptr(O_row_ptr), _ptr(bias), _ptr(S_group), n_groups,
+                M, N, B, _ptr(y), stream)
+    _lib.check(rc, fn.__name__)
+    return y
+
+
+def dequant(kind: str, Q, codes, g, h, O_vals, O_col, O_row_ptr, S_group=None) -> torch.Tensor:
+    """Bit-exact fp16 W (8M, N) on the GPU; ``codes`` must be the fp32 table."""
+    M, N, n_groups = _check_layer(kind, Q, codes, g, h, O_vals, O_col, O_row_ptr, S_group)
+    _require(codes.dtype == torch.float32, "dequant needs the fp32 table for bit-exact W")
+    W = torch.empty((8 * M, N), dtype=torch.float16, device=Q.device)
+    lib = _lib.load()
+    fn = lib.eptq_e8d4_dequant if kind == "e8_d4" else lib.eptq_e8_dequant
+    with torch.cuda.device(Q.device):
+        stream = torch.cuda.current_stream().cuda_stream
+        rc = fn(_ptr(Q), _ptr(codes), _ptr(g), _ptr(h), _ptr(O_vals), _ptr(O_col),
+                _ptr(O_row_ptr), _ptr(S_group), n_groups, M, N, _ptr(W), stream)
+    _lib.check(rc, fn.__name__)
+    return W
+
+
+# ---------------------------------------------------------------------------
+# torch.library registration (names and signatures of kernels/__init__.py:50-91)
+# ---------------------------------------------------------------------------
+
+@torch.library.custom_op("eptq::e8_forward", mutates_args=())
+def e8_forward(Q: torch.Tensor, codebook: torch.Tensor, g: torch.Tensor, h: torch.Tensor,
+               x: torch.Tensor, O_vals: torch.Tensor, O_col: torch.Tensor,
+               O_row_ptr: torch.Tensor, bias: torch.Tensor) -> torch.Tensor:
+    return linear_forward("e8_lattice", Q, codebook, g, h, x, O_vals, O_col, O_row_ptr, bias)
+
+
+@e8_forward.register_fake
+def _e8_forward_fake(Q, codebook, g, h, x, O_vals, O_col, O_row_ptr, bias):
+    return x.new_empty(x.shape[0], Q.shape[0] * 8)
+
+
+@torch.library.custom_op("eptq::e8d4_forward", mutates_args=())
+def e8d4_forward(Q: torch.Tensor, codes: torch.Tensor, g: torch.Tensor, h: torch.Tensor,
+                 x: torch.Tensor, O_vals: torch.Tensor, O_col: torch.Tensor,
+                 O_row_ptr: torch.Tensor, bias: torch.Tensor) -> torch.Tensor:
+    return linear_forward("e8_d4", Q, codes, g, h, x, O_vals, O_col, O_row_ptr, bias)
+
+
+@e8d4_forward.register_fake
+def _e8d4_forward_fake(Q, codes, g, h, x, O_vals, O_col, O_row_ptr, bias):
+    return x.new_empty(x.shape[0], Q.shape[0] * 8)
+
+
+@torch.library.custom_op("eptq::e8_forward_grouped", mutates_args=())
+def e8_forward_grouped(Q: torch.Tensor, codebook: torch.Tensor, g: torch.Tensor, h: torch.Tensor,
+                       x: torch.Tensor, O_vals: torch.Tensor, O_col: torch.Tensor,
+                       O_row_ptr: torch.Tensor, bias: torch.Tensor,
+                       S_group: torch.Tensor) -> torch.Tensor:
+    return linear_forward("e8_lattice", Q, codebook, g, h, x, O_vals, O_col, O_row_ptr, bias, S_group)
+
+
+@e8_forward_grouped.register_fake
+def _e8_forward_grouped_fake(Q, codebook, g, h, x, O_vals, O_col, O_row_ptr, bias, S_group):
+    return x.new_empty(x.shape[0], Q.shape[0] * 8)
+
+
+@torch.library.custom_op("eptq::e8d4_forward_grouped", mutates_args=())
+def e8d4_forward_grouped(Q: torch.Tensor, codes: torch.Tensor, g: torch.Tensor, h: torch.Tensor,
+                         x: torch.Tensor, O_vals: torch.Tensor, O_col: torch.Tensor,
+                         O_row_ptr: torch.Tensor, bias: torch.Tensor,
+                         S_group: torch.Tensor) -> torch.Tensor:
+    return linear_forward("e8_d4", Q, codes, g, h, x, O_vals, O_col, O_row_ptr, bias, S_group)
+
+
+@e8d4_forward_grouped.register_fake
+def _e8d4_forward_grouped_fake(Q, codes, g, h, x, O_vals, O_col, O_row_ptr, bias, S_group):
+    return x.new_empty(x.shape[0], Q.shape[0] * 8)
+
+
+@torch.library.custom_op("eptq::e8d4_dequant", mutates_args=())
+def e8d4_dequant(Q: torch.Tensor, codes: torch.Tensor, g: torch.Tensor, h: torch.Tensor,
+                 O_vals: torch.Tensor, O_col: torch.Tensor, O_row_ptr: torch.Tensor,
+                 S_group: Optional[torch.Tensor] = None) -> torch.Tensor:
+    return dequant("e8_d4", Q, codes, g, h, O_vals, O_col, O_row_ptr, S_group)
+
+
+@e8d4_dequant.register_fake
+def _e8d4_dequant_fake(Q, codes, g, h, O_vals, O_col, O_row_ptr, S_group=None):
+    return Q.new_empty(Q.shape[0] * 8, Q.shape[1], dtype=torch.float16)
+
+
+@torch.library.custom_op("eptq::e8_dequant", mutates_args=())
+def e8_dequant(Q: torch.Tensor, codes: torch.Tensor, g: torch.Tensor, h: torch.Tensor,
+               O_vals: torch.Tensor, O_col: torch.Tensor, O_row_ptr: torch.Tensor,
+               S_group: Optional[torch.Tensor] = None) -> torch.Tensor:
+    return dequant("e8_lattice", Q, codes, g, h, O_vals, O_col, O_row_ptr, S_group)
+
+
+@e8_dequant.register_fake
+def _e8_dequant_fake(Q, codes, g, h, O_vals, O_col, O_row_ptr, S_group=None):
+    return Q.new_empty(Q.shape[0] * 8, Q.shape[1], dtype=torch.float16)

@@ -1,0 +1,157 @@
+"""``EPTQLinear`` (alias ``QuantizedLinear``): a quantized ``nn.Linear`` on gfx950 kernels.
+
+Drop-in for the reference's ``kernels/linear.py:20-219``: same constructor
+signature, same ``from_quantized_data(quant_data, codebook, quantizer_type)``,
+same buffer names (``Q, g, h, O_vals, O_col, O_row_ptr, bias``), the same
+shared non-buffer codebook moved by ``_apply``, and ``forward`` mapping
+(..., in) -> (..., out) in the input dtype.
+
+Differences, all towards the reference's own reconstruct semantics:
+
+* ``codebook`` may be a loaded quantizer (``reconstruct.load_quantizer``) as
+  well as a table tensor; with a quantizer, a layer's ``chosen_r`` selects the
+  table ``raw / chosen_r`` exactly as ``dequantize_layer`` does
+  (``algorithms/eptq.py:432-457``) — the reference kernel path ignores it.
+* ``S_group`` layers stay compressed and run the fused grouped kernel instead
+  of a materialized fp16 W (``kernels/linear.py:97-120,158-164``).
+* every batch size runs a HIP kernel (decode matvec for ≤16 rows, GEMM above);
+  ``EPTQ_CUDA_DECODE`` / ``EPTQ_FORCE_TRITON`` are accepted and ignored.
+* ``dequantize()`` returns the bit-exact fp16 W of ``dequantize_layer`` from the
+  GPU (needs the fp32 table, kept alongside the fp16 kernel table).
+"""
+
+from __future__ import annotations
+
+from typing import Dict, Optional, Tuple
+
+import torch
+import torch.nn as nn
+
+from . import dequant as _dequant
+from . import linear_forward
+
+_KINDS = ("e8_lattice", "e8_d4")
+
+# Tables shared across layers: (id(source), radius, device, dtype) -> tensor.
+_TABLE_CACHE: Dict[Tuple, torch.Tensor] = {}
+
+
+def _table_for(codebook, quantizer_type: str, chosen_r: Optional[float]) -> torch.Tensor:
+    """fp32 kernel-layout table for one layer (shared when identical)."""
+    if isinstance(codebook, torch.Tensor):
+        t = codebook.float()
+        return t.reshape(512, 4).contiguous() if quantizer_type == "e8_d4" else t.reshape(-1, 8).contiguous()
+    q = codebook
+    r = getattr(q, "_radius", None)
+    key = (id(q), r if chosen_r is None else float(chosen_r), quantizer_type)
+    hit = _TABLE_CACHE.get(key)
+    if hit is not None:
+        return hit
+    if chosen_r is not None and r is not None and chosen_r != r:
+        q.set_radius(chosen_r)
+        try:
+            tab = q.flat_table().clone()
+        finally:
+            q.set_radius(r)
+    else:
+        tab = q.flat_table()
+    _TABLE_CACHE[key] = tab
+    return tab
+
+
+class EPTQLinear(nn.Module):
+    """Quantized Linear: Q (M, N) int16 indices + g/h scales + CSR outliers."""
+
+    def __init__(self, Q: torch.Tensor, codebook: torch.Tensor, g: torch.Tensor,
+                 h: torch.Tensor, O_vals: torch.Tensor, O_col: torch.Tensor,
+                 O_row_ptr: torch.Tensor, bias: Optional[torch.Tensor], quantizer_type: str,
+                 S_group: Optional[torch.Tensor] = None,
+                 table_f32: Optional[torch.Tensor] = None):
+        super().__init__()
+        if quantizer_type not in _KINDS:
+            raise ValueError(f"unknown quantizer_type {quantizer_type!r}")
+        self.in_features = int(Q.shape[1])
+        self.out_features = int(Q.shape[0]) * 8
+        self.quantizer_type = quantizer_type
+        self.register_buffer("Q", Q.contiguous())
+        self.register_buffer("g", g.contiguous())
+        self.register_buffer("h", h.contiguous())
+        self.register_buffer("O_vals", O_vals.contiguous())
+        self.register_buffer("O_col", O_col.contiguous())
+        self.register_buffer("O_row_ptr", O_row_ptr.contiguous())
+        self.register_buffer("bias", bias.contiguous() if bias is not None else None)
+        self.register_buffer("S_group", S_group.contiguous() if S_group is not None else None)
+        # Shared tables — not buffers, so they are not duplicated in state_dict.
+        self._codebook = codebook
+        self._table_f32 = table_f32 if table_f32 is not None else codebook.float()
+
+    def _apply(self, fn, *args, **kwargs):
+        super()._apply(fn, *args, **kwargs)
+        self._codebook = fn(self._codebook)
+        self._table_f32 = fn(self._table_f32)
+        return self
+
+    @classmethod
+    def from_quantized_data(cls, quant_data, codebook, quantizer_type: str) -> "EPTQLinear":
+        """Build from a ``QuantizedLayerData`` (``kernels/linear.py:83-152``).
+
+        ``codebook``: the shared table tensor (E8-D4 (4,128,4)/(512,4), E8
+        (65535, 8); fp16 or fp32, already divided by the radius) or a loaded
+        quantizer, which also honours the layer's ``chosen_r``.
+        """
+        if quantizer_type not in _KINDS:
+            raise ValueError(f"unknown quantizer_type {quantizer_type!r}")
+        Q = quant_data.Q
+        if Q.dtype != torch.int16:
+            raise ValueError(f"Q must be int16, got {Q.dtype}")
+        M = Q.shape[0]
+        tab32 = _table_for(codebook, quantizer_type, quant_data.chosen_r)
+        cb16 = tab32.to(torch.float16)
+
+        # Critical blocks — nonzero() on row-major Q is in row-major order.
+        mask = Q == 32767
+        O_row, O_col = mask.nonzero(as_tuple=True)
+        n_masked = int(O_row.shape[0])
+        if int(quant_data.O.shape[0]) != n_masked:
+            raise ValueError(f"O shape mismatch: got {quant_data.O.shape[0]} values "
+                             f"but found {n_masked} masked positions in Q")
+        counts = torch.bincount(O_row.long(), minlength=M)
+        O_row_ptr = torch.cat([torch.zeros(1, dtype=torch.int32, device=O_row.device),
+                               counts.cumsum(0).to(torch.int32)])
+        S = quant_data.S_group
+        if S is not None:
+            S = S.to(torch.float16)
+        return cls(Q=Q, codebook=cb16, g=quant_data.g.to(torch.float16),
+                   h=quant_data.h.to(torch.float16),
+                   O_vals=quant_data.O.to(torch.float16).reshape(-1, 8),
+                   O_col=O_col.to(torch.int32), O_row_ptr=O_row_ptr,
+                   bias=quant_data.bias.to(torch.float16) if quant_data.bias is not None else None,
+                   quantizer_type=quantizer_type, S_group=S, table_f32=tab32)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        shape = x.shape
+        out_dtype = x.dtype
+        x2 = x.reshape(-1, self.in_features)
+        if x2.dtype not in (torch.float16, torch.bfloat16):
+            x2 = x2.half()
+        if not x2.is_contiguous():
+            x2 = x2.contiguous()
+        y = linear_forward(self.quantizer_type, self.Q, self._codebook, self.g, self.h, x2,
+                           self.O_vals, self.O_col, self.O_row_ptr, self.bias, self.S_group)
+        if y.dtype != out_dtype:
+            y = y.to(out_dtype)
+        return y.reshape(*shape[:-1], self.out_features)
+
+    @torch.no_grad()
+    def dequantize(self) -> torch.Tensor:
+        """fp16 W (out, in), bit-exact with ``dequantize_layer`` on the same table."""
+        return _dequant(self.quantizer_type, self.Q, self._table_f32, self.g, self.h,
+                        self.O_vals, self.O_col, self.O_row_ptr, self.S_group)
+
+    def extra_repr(self) -> str:
+        return (f"in={self.in_features}, out={self.out_features}, "
+                f"quantizer={self.quantizer_type}, n_masked={self.O_col.shape[0]}"
+                + (f", groups={self.S_group.shape[0]}" if self.S_group is not None else ""))
+
+
+QuantizedLinear = EPTQLinear

@@ -1,0 +1,98 @@
+/*
+ * eptq_hip.h — C ABI of the MI355X (gfx950) EPTQ quantized-Linear library.
+ *
+ * Every entry point takes plain device pointers, sizes and a hipStream_t
+ * (passed as void*), launches asynchronously on that stream, allocates
+ * nothing, keeps no pointer after returning, and returns EPTQ_OK or an error
+ * code; eptq_last_error() then describes the failure (per host thread).
+ *
+ * Layer format (reference config.py:98-159, kernels/linear.py:83-152):
+ *   Q          int16 (M, N) row-major, stored as index - 32768; 32767 marks a
+ *              critical 8-row block.  M = out_features / 8, N = in_features.
+ *   g          fp16 (8M)          row scales
+ *   h          fp16 (N)           column scales
+ *   O_vals     fp16 (nnz, 8)      critical blocks, row-major marker order
+ *   O_col      int32 (nnz)        column of each critical block
+ *   O_row_ptr  int32 (M + 1)      CSR row pointers into O_vals / O_col
+ *   bias       fp16 (8M) or NULL
+ *   S_group    fp16 (n_groups, N) or NULL; qb = 8M / n_groups must be a
+ *              multiple of 8 (reference algorithms/eptq.py:74, :440-449)
+ *   codes      E8-D4: (512, 4) table, E8: (65535, 8) table, fp16 or fp32
+ *              (codes_dtype), already divided by the layer's radius.
+ *   x          fp16 or bf16 (B, N) row-major; y same dtype as x_dtype
+ *              (B, 8M) row-major.
+ *
+ * Alignment: Q, x, h, O_vals and S_group must be 16-byte aligned and N a
+ * multiple of 8 (EPTQ_EUNSUPPORTED otherwise).
+ */
+#ifndef EPTQ_HIP_H
+#define EPTQ_HIP_H
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  EPTQ_OK = 0,
+  EPTQ_EINVAL = 1,        /* null pointer / negative size / inconsistent args */
+  EPTQ_EUNSUPPORTED = 2,  /* shape or alignment outside what the kernels take */
+  EPTQ_EHIP = 3           /* HIP runtime reported an error at launch */
+};
+
+enum { EPTQ_F16 = 0, EPTQ_F32 = 1, EPTQ_BF16 = 2 };
+
+/* ABI revision; bumped on any signature change. */
+int eptq_abi_version(void);
+
+/* Text of the last error on this host thread ("" if none). */
+const char* eptq_last_error(void);
+
+/*
+ * Fused E8-D4 quantized Linear: y = g ⊙ (decode(Q) · (h ⊙ x)ᵀ + CSR(O)) + bias.
+ * Replaces e8d4_forward (reference csrc/eptq_kernels.h:31-41, dispatch
+ * csrc/eptq_kernels.cu:466-558) and the Triton decode path
+ * (kernels/triton_e8d4.py:160-193).  Adds the optional S_group operand that
+ * the reference serves with a materialized fp16 W (kernels/linear.py:97-120).
+ * B <= 16 runs the HBM-bound decode matvec; larger B the dequant-to-LDS
+ * MFMA GEMM.
+ */
+int eptq_e8d4_forward(const void* Q, const void* codes, int codes_dtype,
+                      const void* g, const void* h, const void* x, int x_dtype,
+                      const void* O_vals, const void* O_col, const void* O_row_ptr,
+                      const void* bias, const void* S_group, int n_groups,
+                      int M, int N, int B, void* y, void* stream);
+
+/*
+ * Fused E8-lattice quantized Linear (same math, 8-vector = codes[u]).
+ * Replaces e8_forward (reference csrc/eptq_kernels.h:15-25,
+ * kernel csrc/eptq_kernels.cu:39-150).
+ */
+int eptq_e8_forward(const void* Q, const void* codes, int codes_dtype,
+                    const void* g, const void* h, const void* x, int x_dtype,
+                    const void* O_vals, const void* O_col, const void* O_row_ptr,
+                    const void* bias, const void* S_group, int n_groups,
+                    int M, int N, int B, void* y, void* stream);
+
+/*
+ * Bit-exact dequantization to fp16 W (8M, N) row-major, the device
+ * counterpart of dequantize_layer (reference algorithms/eptq.py:406-471):
+ * W = fp16_rne((v [· S]) · g · h) with v = fp32 table row, critical blocks
+ * overwritten by fp32(O) before the g/h scaling.  codes must be fp32.
+ */
+int eptq_e8d4_dequant(const void* Q, const void* codes_f32,
+                      const void* g, const void* h,
+                      const void* O_vals, const void* O_col, const void* O_row_ptr,
+                      const void* S_group, int n_groups,
+                      int M, int N, void* W, void* stream);
+
+int eptq_e8_dequant(const void* Q, const void* codes_f32,
+                    const void* g, const void* h,
+                    const void* O_vals, const void* O_col, const void* O_row_ptr,
+                    const void* S_group, int n_groups,
+                    int M, int N, void* W, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* EPTQ_HIP_H */
