@@ -98,8 +98,12 @@ int linear_common(int kind, const void* Q, const void* codes, int codes_dtype, c
   hipStream_t s = (hipStream_t)stream;
 
   if (B <= eptq::kMatvecMaxBatch) {
-    rc = kind == eptq::KIND_E8D4 ? eptq::launch_matvec<eptq::KIND_E8D4>(a, s)
-                                 : eptq::launch_matvec<eptq::KIND_E8>(a, s);
+    if (kind == eptq::KIND_E8D4) {
+      rc = eptq::launch_decode_e8d4(a, s);
+      if (rc) rc = eptq::launch_matvec<eptq::KIND_E8D4>(a, s);
+    } else {
+      rc = eptq::launch_matvec<eptq::KIND_E8>(a, s);
+    }
   } else if (kind == eptq::KIND_E8D4) {
     rc = eptq::launch_gemm_e8d4(a, s);
   } else {

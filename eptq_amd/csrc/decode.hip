@@ -1,0 +1,426 @@
+// Persistent E8-D4 decode matvec (batch 1..8), the HBM-bound hot path.
+//
+// Same result as the reference decode kernels (csrc/eptq_kernels.cu:161-292,
+// kernels/triton_e8d4.py:47-157): y = g ⊙ (decode(Q)·(h ⊙ S ⊙ x)ᵀ + CSR(O)) + bias.
+//
+// Work split.  A workgroup is 4 waves; S waves (1, 2 or 4) share a Q-row, so
+// a workgroup works on R = 4/S adjacent rows at a time and walks row groups
+// blockIdx.x, +G, +2G, ...  Lane `lane` of segment wave `seg` owns the
+// 16-byte column chunks c = seg·64 + lane + 64·S·j (j < J) of every row, so
+// the activation side (x·h) is prepared once per workgroup and kept in
+// registers and the E8-D4 table is staged in LDS once.  S is the smallest
+// split that still gives the chip enough waves: whole-row waves (S = 1) need
+// no cross-wave reduction and no barrier; S > 1 combines the S partial sums
+// through LDS with one barrier per row group.  The index chunks of the next
+// P row groups are kept in flight in a register ring (about 8 chunks = 128
+// bytes per lane) so HBM latency is covered, and the grid holds as many
+// workgroups per CU as the registers allow so LDS latency is covered.
+//
+// Arithmetic:
+//  * B = 1: x·h is formed exactly in fp32 (product of two fp16 values) and
+//    each table component is accumulated with one mixed fp16×fp32 FMA.
+//  * B >= 2: the two indices of a 32-bit word (adjacent columns) are paired:
+//    byte permutes turn their two table vectors into (c_k(n), c_k(n+1)) fp16
+//    pairs and one v_dot2_f32_f16 per (k, b) accumulates both columns in
+//    fp32.  The activation pairs x·h are rounded to fp16 after scaling h by a
+//    workgroup-uniform power of two 2^-e with max|h|·2^-e <= 1, so |x·h·2^-e|
+//    <= |x| cannot overflow; 2^e is restored in fp32 at the output.  With
+//    S_group the pairs are multiplied by the row group's scales in fp16.
+//
+// Index decode from the raw int16 bits v, with the LDS table stored at
+// position e ^ 0x100 for table row e (u = v ^ 0x8000 needs no fix-up):
+//   rows 0..3 of the block: byte address (v >> 4) & 0xFF8
+//   rows 4..7:              same bits 10-11, bits 3-9 = (v & 127) << 3.
+// Critical blocks (v = 32767) decode as table row 511 in both halves; the
+// CSR pass adds O·(h x) minus exactly what the main loop accumulated for them.
+
+#include "common.h"
+#include "kernels.h"
+
+namespace eptq {
+
+namespace {
+
+constexpr int kT = 256;          // threads per workgroup
+constexpr int kW = kT / 64;      // waves per workgroup
+
+typedef f16 h2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint32_t perm(uint32_t hi_src, uint32_t lo_src, uint32_t sel) {
+  return __builtin_amdgcn_perm(hi_src, lo_src, sel);
+}
+
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, a), __builtin_bit_cast(h2, b), c, false);
+}
+
+__device__ __forceinline__ uint32_t pk_mul(uint32_t a, uint32_t b) {
+  return __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, a) * __builtin_bit_cast(h2, b));
+}
+
+}  // namespace
+
+template <int BT, int J, int P, int S, bool HAS_S, typename XT>
+__global__ __launch_bounds__(kT) void k_decode_e8d4(LinearArgs a) {
+  constexpr int V = BT * 8;
+  constexpr int R = kW / S;                    // rows per row group
+  __shared__ f16x4 tab[512];
+  __shared__ float red[S > 1 ? 2 : 1][kW][S > 1 ? V : 1];
+  __shared__ float wmax[kW];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int slot = wave / S, seg = wave % S;
+  const int N = a.N, M = a.M, B = a.B;
+  const int nch = N >> 3;
+  const int RG = (M + R - 1) / R;              // row groups
+  const int G = gridDim.x;
+  const char* __restrict__ tabB = (const char*)tab;
+
+  auto chunk = [&](int j) { return seg * 64 + lane + 64 * S * j; };
+
+  // ---- setup loads (table, h, x), then the index chunks of P row groups ----
+  u32x4 qv[P][J];
+  // Every load is issued unconditionally from a clamped (always valid)
+  // address and masked afterwards: with no divergent branches around loads
+  // the compiler can wait for exactly the load it needs (vmcnt counts loads
+  // in issue order) instead of draining all of them.
+  auto load_q = [&](u32x4 (&dst)[J], int rg) {
+    const int row = rg * R + slot;
+    const bool rv = row < M;
+    const u32x4* __restrict__ qrow = (const u32x4*)(a.Q + (size_t)(rv ? row : M - 1) * N);
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      const int c = chunk(j);
+      const bool ok = rv && c < nch;
+      const u32x4 v = __builtin_nontemporal_load(qrow + (c < nch ? c : nch - 1));
+      dst[j] = ok ? v : (u32x4){0u, 0u, 0u, 0u};
+    }
+  };
+  // Loads complete in issue order (vmcnt counts them in order), so the small
+  // L2-resident setup loads are issued before the HBM index stream: waiting
+  // for the table and activations then does not wait for the indices.
+  f16x4 tload[2];
+#pragma unroll
+  for (int p = 0; p < 2; ++p) tload[p] = ((const f16x4*)a.codes)[tid + kT * p];   // fp16 table
+
+  f16x8 hv[J];
+  u16x8 xload[J][BT];
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    const int c = chunk(j);
+    const int cc = (c < nch ? c : nch - 1) << 3;
+    const f16x8 hl = *(const f16x8*)(a.h + cc);
+    hv[j] = c < nch ? hl : (f16x8){0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+    for (int b = 0; b < BT; ++b) {
+      const u16x8 xl = *(const u16x8*)(a.x + (size_t)(b < B ? b : B - 1) * N + cc);
+      xload[j][b] = (c < nch && b < B) ? xl : (u16x8){0, 0, 0, 0, 0, 0, 0, 0};
+    }
+  }
+#pragma unroll
+  for (int p = 0; p < P; ++p) load_q(qv[p], blockIdx.x + p * G);
+
+  // Activation side, identical for every row this lane visits.
+  //   B = 1:  xh1[j][e] = x·h exactly in fp32
+  //   B >= 2: xhp[j][b][d] = fp16 pair (x·h·2^-e) for columns 2d, 2d+1
+  float xh1[BT == 1 ? J : 1][8];
+  uint32_t xhp[BT == 1 ? 1 : J][BT][4];
+  float out_scale = 1.0f;
+  if constexpr (BT == 1) {
+#pragma unroll
+    for (int j = 0; j < J; ++j)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) xh1[j][e] = Act<XT>::mul_f16(xload[j][0][e], hv[j][e]);
+  } else {
+    // Workgroup-uniform power-of-two scale: max|h| * 2^-e <= 1.
+    float mx = 0.0f;
+#pragma unroll
+    for (int j = 0; j < J; ++j)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) mx = fmaxf(mx, fabsf((float)hv[j][e]));
+    mx = fmaxf(mx, partner<1>(mx));
+    mx = fmaxf(mx, partner<2>(mx));
+    mx = fmaxf(mx, partner<4>(mx));
+    mx = fmaxf(mx, partner<8>(mx));
+    mx = fmaxf(mx, partner<16>(mx));
+    mx = fmaxf(mx, partner<32>(mx));
+    if (lane == 0) wmax[wave] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+    int ex = 0;
+    if (mx > 1.0f) ex = (int)((__builtin_bit_cast(uint32_t, mx) >> 23) & 0xff) - 126;  // 2^ex >= mx
+    out_scale = __builtin_ldexpf(1.0f, ex);
+    const f16 down = (f16)__builtin_ldexpf(1.0f, -ex);
+    const uint32_t down2 = __builtin_bit_cast(uint32_t, (h2){down, down});
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      const u32x4 hw = __builtin_bit_cast(u32x4, hv[j]);
+#pragma unroll
+      for (int b = 0; b < BT; ++b) {
+        const u32x4 xw = __builtin_bit_cast(u32x4, xload[j][b]);
+#pragma unroll
+        for (int d = 0; d < 4; ++d) xhp[j][b][d] = pk_mul(xw[d], pk_mul(hw[d], down2));
+      }
+    }
+  }
+
+#pragma unroll
+  for (int p = 0; p < 2; ++p) tab[(tid + kT * p) ^ 0x100] = tload[p];
+  __syncthreads();
+
+  // Marker vector as the main loop sees it.
+  const f16x4 t5 = tab[511 ^ 0x100];
+
+  int par = 0;
+  for (int rg0 = blockIdx.x; rg0 < RG; rg0 += P * G) {
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int rg = rg0 + p * G;
+    if (rg >= RG) break;                       // uniform across the workgroup
+    const int m = rg * R + slot;
+    const bool row_ok = m < M;
+    const int grp = HAS_S ? (8 * (row_ok ? m : 0)) / a.qb : 0;
+
+    float acc[V];
+#pragma unroll
+    for (int i = 0; i < V; ++i) acc[i] = 0.0f;
+
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      if (chunk(j) >= nch) break;
+      f16x8 sv;
+      if (HAS_S) sv = *(const f16x8*)(a.S + (size_t)grp * N + (chunk(j) << 3));
+      // All 16 table lookups of the chunk first, then the arithmetic, so the
+      // LDS latency is paid once per chunk rather than once per word.
+      u32x2 t1l[4], t2l[4], t1h[4], t2h[4];
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        const uint32_t w = qv[p][j][d];
+        const uint32_t a1lo = (w >> 4) & 0xFF8u;
+        const uint32_t a1hi = (w >> 20) & 0xFF8u;
+        const uint32_t a2lo = bfi(0x3F8u, w << 3, a1lo);
+        const uint32_t a2hi = bfi(0x3F8u, w >> 13, a1hi);
+        t1l[d] = *(const u32x2*)(tabB + a1lo);
+        t2l[d] = *(const u32x2*)(tabB + a2lo);
+        t1h[d] = *(const u32x2*)(tabB + a1hi);
+        t2h[d] = *(const u32x2*)(tabB + a2hi);
+      }
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        if constexpr (BT == 1) {
+          float xl = xh1[j][2 * d], xh = xh1[j][2 * d + 1];
+          if (HAS_S) { xl *= (float)sv[2 * d]; xh *= (float)sv[2 * d + 1]; }
+          const f16x4 c1l = __builtin_bit_cast(f16x4, t1l[d]), c2l = __builtin_bit_cast(f16x4, t2l[d]);
+          const f16x4 c1h = __builtin_bit_cast(f16x4, t1h[d]), c2h = __builtin_bit_cast(f16x4, t2h[d]);
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            acc[k] = fmaf((float)c1l[k], xl, acc[k]);
+            acc[k + 4] = fmaf((float)c2l[k], xl, acc[k + 4]);
+          }
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            acc[k] = fmaf((float)c1h[k], xh, acc[k]);
+            acc[k + 4] = fmaf((float)c2h[k], xh, acc[k + 4]);
+          }
+        } else {
+          // (c_k(lo), c_k(hi)) fp16 pairs for k = 0..7
+          uint32_t pr[8];
+          pr[0] = perm(t1h[d][0], t1l[d][0], 0x05040100u);
+          pr[1] = perm(t1h[d][0], t1l[d][0], 0x07060302u);
+          pr[2] = perm(t1h[d][1], t1l[d][1], 0x05040100u);
+          pr[3] = perm(t1h[d][1], t1l[d][1], 0x07060302u);
+          pr[4] = perm(t2h[d][0], t2l[d][0], 0x05040100u);
+          pr[5] = perm(t2h[d][0], t2l[d][0], 0x07060302u);
+          pr[6] = perm(t2h[d][1], t2l[d][1], 0x05040100u);
+          pr[7] = perm(t2h[d][1], t2l[d][1], 0x07060302u);
+          uint32_t sp = 0;
+          if (HAS_S) sp = __builtin_bit_cast(u32x4, sv)[d];
+#pragma unroll
+          for (int b = 0; b < BT; ++b) {
+            const uint32_t xp = HAS_S ? pk_mul(xhp[j][b][d], sp) : xhp[j][b][d];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) acc[b * 8 + k] = dot2(pr[k], xp, acc[b * 8 + k]);
+          }
+        }
+      }
+    }
+
+    // This ring slot is consumed: fetch the row group P·G ahead into it.
+    load_q(qv[p], rg + P * G);
+
+    // Critical blocks: add O·(h S x) in the accumulator's units, minus what
+    // the marker index contributed above.
+    if (row_ok) {
+      const int r0 = a.O_row_ptr[m], r1 = a.O_row_ptr[m + 1];
+      for (int i = r0 + seg * 64 + lane; i < r1; i += 64 * S) {
+        const int col = a.O_col[i];
+        const f16x8 o = *(const f16x8*)(a.O + (size_t)i * 8);
+        const f16 hc = a.h[col];
+        const float sc = HAS_S ? (float)a.S[(size_t)grp * N + col] : 1.0f;
+#pragma unroll
+        for (int b = 0; b < BT; ++b) {
+          if (b < B) {
+            const uint16_t xb = a.x[(size_t)b * N + col];
+            float xo, xm;   // x·h for O (no S); what the main loop used
+            if constexpr (BT == 1) {
+              xo = Act<XT>::mul_f16(xb, hc);
+              xm = HAS_S ? xo * sc : xo;
+            } else {
+              const f16 hd = (f16)((float)hc / out_scale);
+              const f16 xhd = (f16)((float)__builtin_bit_cast(f16, xb) * (float)hd);
+              xo = Act<XT>::mul_f16(xb, hc) / out_scale;
+              xm = HAS_S ? (float)(f16)((float)xhd * sc) : (float)xhd;
+            }
+#pragma unroll
+            for (int k = 0; k < 8; ++k)
+              acc[b * 8 + k] += (float)o[k] * xo - (float)t5[k & 3] * xm;
+          }
+        }
+      }
+    }
+
+    const int base = wave_reduce_halving<V>(acc);
+    if constexpr (S == 1) {
+      // The wave owns the row: write straight from the reducing lanes.
+      if (row_ok && WaveReduceOut<V>::writer(lane)) {
+#pragma unroll
+        for (int i = 0; i < WaveReduceOut<V>::per_lane; ++i) {
+          const int t = base + i;
+          const int b = t >> 3, k = t & 7;
+          if (b < B) {
+            const int row = 8 * m + k;
+            float sum = acc[i] * out_scale * (float)a.g[row];
+            if (a.bias) sum += (float)a.bias[row];
+            a.y[(size_t)b * (8 * M) + row] = Act<XT>::from_f32(sum);
+          }
+        }
+      }
+    } else {
+      if (WaveReduceOut<V>::writer(lane)) {
+#pragma unroll
+        for (int i = 0; i < WaveReduceOut<V>::per_lane; ++i) red[par][wave][base + i] = acc[i];
+      }
+      // One barrier per row group: red[] alternates, and the next barrier
+      // orders these reads of red[par] before its reuse two groups later.
+      __syncthreads();
+      for (int t = tid; t < R * V; t += kT) {
+        const int sl = t / V, idx = t - sl * V;
+        const int mr = rg * R + sl;
+        const int b = idx >> 3, k = idx & 7;
+        if (mr < M && b < B) {
+          float sum = 0.0f;
+#pragma unroll
+          for (int w = 0; w < S; ++w) sum += red[par][sl * S + w][idx];
+          const int row = 8 * mr + k;
+          sum = sum * out_scale * (float)a.g[row];
+          if (a.bias) sum += (float)a.bias[row];
+          a.y[(size_t)b * (8 * M) + row] = Act<XT>::from_f32(sum);
+        }
+      }
+      par ^= 1;
+    }
+  }
+  }
+}
+
+namespace {
+
+int g_cu_count = 0;
+
+int cu_count() {
+  if (g_cu_count == 0) {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
+      g_cu_count = n;
+    else
+      g_cu_count = 256;
+  }
+  return g_cu_count;
+}
+
+// Chunks per lane for a row split S ways (0 if beyond the kernel's range).
+int chunks_for(int nch, int S) {
+  const int j = (nch + 64 * S - 1) / (64 * S);
+  if (j <= 2) return 2;
+  if (j <= 4) return 4;
+  if (j <= 8) return 8;
+  return 0;
+}
+
+bool fits(int J, int B) { return J > 0 && (B == 1 || J * B <= 16); }
+
+template <int BT, int J, int S, bool HAS_S, typename XT>
+void launch_k(const LinearArgs& a, hipStream_t s) {
+  // About 8 index chunks (128 bytes) per lane in flight: P row groups of J.
+  constexpr int P = J >= 8 ? 1 : 8 / J;
+  constexpr int R = kW / S;
+  auto kern = k_decode_e8d4<BT, J, P, S, HAS_S, XT>;
+  // As many workgroups per CU as the registers allow (one wave of each
+  // workgroup per SIMD): occupancy hides the LDS lookup latency.
+  static int per_cu = 0;
+  if (per_cu == 0) {
+    hipFuncAttributes fa;
+    int v = 128;
+    if (hipFuncGetAttributes(&fa, (const void*)kern) == hipSuccess && fa.numRegs > 0) v = fa.numRegs;
+    const int waves = 512 / ((v + 7) / 8 * 8);
+    per_cu = waves < 1 ? 1 : (waves > 8 ? 8 : waves);
+  }
+  const int RG = (a.M + R - 1) / R;
+  int grid = cu_count() * per_cu;
+  if (grid > RG) grid = RG;
+  kern<<<grid, kT, 0, s>>>(a);
+}
+
+template <int BT, int S, bool HAS_S, typename XT>
+int launch_s(const LinearArgs& a, hipStream_t s) {
+  const int J = chunks_for(a.N >> 3, S);
+  if (!fits(J, BT)) return -1;
+  if (J == 2) { launch_k<BT, 2, S, HAS_S, XT>(a, s); return 0; }
+  if constexpr (BT <= 4) if (J == 4) { launch_k<BT, 4, S, HAS_S, XT>(a, s); return 0; }
+  if constexpr (BT <= 2) if (J == 8) { launch_k<BT, 8, S, HAS_S, XT>(a, s); return 0; }
+  return -1;
+}
+
+template <int BT, bool HAS_S, typename XT>
+int launch_bt(const LinearArgs& a, hipStream_t s) {
+  const int nch = a.N >> 3;
+  // Smallest row split that gives the chip about 8 waves per CU; the
+  // register budget of the activation pairs can force a wider split.
+  const int want = cu_count() * 8;
+  int S = 4;
+  for (int cand = 1; cand <= 4; cand *= 2) {
+    if (!fits(chunks_for(nch, cand), BT)) continue;
+    S = cand;
+    if ((long)a.M * cand >= want) break;
+  }
+  if (!fits(chunks_for(nch, S), BT)) return -1;
+  if (S == 1) return launch_s<BT, 1, HAS_S, XT>(a, s);
+  if (S == 2) return launch_s<BT, 2, HAS_S, XT>(a, s);
+  return launch_s<BT, 4, HAS_S, XT>(a, s);
+}
+
+template <bool HAS_S, typename XT>
+int launch_b(const LinearArgs& a, hipStream_t s) {
+  if (a.B == 1) return launch_bt<1, HAS_S, XT>(a, s);
+  if (a.B == 2) return launch_bt<2, HAS_S, XT>(a, s);
+  if (a.B <= 4) return launch_bt<4, HAS_S, XT>(a, s);
+  if (a.B <= 8) return launch_bt<8, HAS_S, XT>(a, s);
+  return -1;
+}
+
+}  // namespace
+
+// Returns 0 if launched, -1 if this layer/batch is outside the kernel's range.
+int launch_decode_e8d4(const LinearArgs& a, hipStream_t s) {
+  if (a.B < 1 || a.B > 8) return -1;
+  if (a.codes_f32) return -1;  // fp32 tables take the generic kernel
+  if (a.x_bf16) {
+    if (a.B >= 2) return -1;   // fp16 activation pairs only
+    return a.S ? launch_b<true, bf16>(a, s) : launch_b<false, bf16>(a, s);
+  }
+  return a.S ? launch_b<true, f16>(a, s) : launch_b<false, f16>(a, s);
+}
+
+}  // namespace eptq

@@ -45,6 +45,8 @@ struct LinearArgs {
 template <int KIND> int launch_dequant(const DequantArgs& a, hipStream_t s);
 template <int KIND> int launch_matvec(const LinearArgs& a, hipStream_t s);
 int launch_gemm_e8d4(const LinearArgs& a, hipStream_t s);
+// Persistent E8-D4 decode (B <= 8); -1 when the layer/batch is outside its range.
+int launch_decode_e8d4(const LinearArgs& a, hipStream_t s);
 
 // Largest batch served by the decode matvec; larger batches take the GEMM.
 constexpr int kMatvecMaxBatch = 16;
