@@ -1,13 +1,347 @@
-// Prefill path for E8-D4 layers with more than 16 activation rows.
+// Prefill GEMM for E8-D4 layers: y = (decode(Q)·diag(h·S)) · xᵀ ⊙ g + CSR + bias.
 //
-// Batch tiles of 16 rows through the decode matvec: each tile re-streams Q.
+// Counterpart of the reference's large-batch path e8d4_wmma_v2_kernel +
+// at::mul(x, h) (csrc/eptq_kernels.cu:309-461, :520-537), rebuilt for gfx950
+// MFMA.  The contraction is a genuine dense GEMM, so the quantized weight is
+// dequantized tile by tile into LDS and fed to v_mfma_f32_16x16x32_f16.
+//
+// Tiling: a workgroup (4 waves) computes 128 output features (16 Q-rows) ×
+// 128 tokens; each wave a 64 × 64 sub-tile as 4 × 4 MFMA tiles of 16 × 16,
+// accumulated in fp32 over K-steps of 32 input columns.  Per K-step:
+//  * every thread decodes one 32-bit word of Q (two adjacent columns of one
+//    Q-row) through the LDS table (4 lookups), pairs the two columns per
+//    output row with byte permutes, scales the pairs by (h·S) of the two
+//    columns in fp16 and writes 8 words of the W tile (rows × K, fp16);
+//  * the activation tile x[t, k0..k0+31] is copied to LDS unscaled (h lives on
+//    the weight side, so x is never rounded);
+//  * the step is software-pipelined: the table lookups of step s+1 are issued
+//    before the MFMAs of step s and its W/X tiles written after them, into
+//    the other half of a double-buffered LDS tile (one barrier per step);
+//    the global loads run kPF steps ahead in a register ring.
+// Critical blocks decode as table row 511 in the main loop.  Their exact
+// contribution is restored in the same pass: the workgroup stages its rows'
+// CSR entries in LDS once (Δ = O·h − fp16(row511·h·S) per output row), 16
+// walker threads list the entries whose column falls in each K-step, and the
+// waves holding those rows add Δ·x from the activation tile already in LDS.
+// The output is g ⊙ acc + bias, written as fp16.
 
 #include "common.h"
 #include "kernels.h"
 
 namespace eptq {
 
+namespace {
+
+constexpr int kGT = 256;            // threads
+constexpr int kBM = 128;            // output features per workgroup (16 Q-rows)
+constexpr int kBQ = kBM / 8;        // Q-rows per workgroup
+constexpr int kBN = 128;            // tokens per workgroup
+constexpr int kBK = 32;             // input columns per K-step
+constexpr int kLd = kBK + 8;        // LDS row stride in halves (80 bytes)
+constexpr int kEntCap = 512;        // CSR entries staged in LDS per workgroup
+constexpr int kPerStep = kBK;       // max entries of one Q-row inside one K-step
+
+typedef f16 h2 __attribute__((ext_vector_type(2)));
+typedef f16 h8 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ uint32_t gperm(uint32_t hi_src, uint32_t lo_src, uint32_t sel) {
+  return __builtin_amdgcn_perm(hi_src, lo_src, sel);
+}
+__device__ __forceinline__ uint32_t gpk_mul(uint32_t a, uint32_t b) {
+  return __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, a) * __builtin_bit_cast(h2, b));
+}
+
+}  // namespace
+
+template <bool HAS_S>
+__global__ __launch_bounds__(kGT, 2) void k_gemm_e8d4(LinearArgs a, int OB) {
+  __shared__ f16x4 tab[512];
+  __shared__ __attribute__((aligned(16))) f16 Ws[2][kBM][kLd];
+  __shared__ __attribute__((aligned(16))) f16 Xs[2][kBN][kLd];
+  __shared__ int ent_col[kEntCap];
+  __shared__ __attribute__((aligned(16))) h8 ent_delta[kEntCap];
+  __shared__ uint16_t lst[2][kBQ][kPerStep];
+  __shared__ int lcnt[2][kBQ];
+  __shared__ unsigned lmask[2];
+  __shared__ int rps[kBQ + 1];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;      // wave's 64 x 64 sub-tile
+  const int N = a.N, M = a.M, T = a.B;
+  const int ob = blockIdx.x % OB;               // consecutive workgroups share a token tile
+  const int tb = blockIdx.x / OB;
+  const int m0 = ob * kBQ;                      // first Q-row
+  const int t0 = tb * kBN;                      // first token
+  const int nsteps = N / kBK;
+  const char* __restrict__ tabB = (const char*)tab;
+
+  // ---- per-thread roles for the tile loads ----
+  const int dq = tid >> 4;                      // Q-row of the word this thread decodes
+  const int dc = (tid & 15) * 2;                // its first column inside the step
+  const int qrow = m0 + dq;                      // < M: the launcher requires M % 16 == 0
+  const uint32_t* __restrict__ qsrc = (const uint32_t*)(a.Q + (size_t)qrow * N);
+  const int grp = HAS_S ? (8 * qrow) / a.qb : 0;
+  // x chunks: two 16-byte pieces, token xt[i], column chunk xc[i]
+  int xt[2], xc[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int idx = tid + kGT * i;
+    xt[i] = idx >> 2;
+    xc[i] = (idx & 3) * 8;
+  }
+
+  // ---- table and CSR staging ----
+#pragma unroll
+  for (int p = 0; p < 2; ++p) tab[(tid + kGT * p) ^ 0x100] = ((const f16x4*)a.codes)[tid + kGT * p];
+  if (tid <= kBQ) rps[tid] = a.O_row_ptr[m0 + tid < M ? m0 + tid : M];
+  __syncthreads();
+  const int e0 = rps[0];
+  const int ecount = rps[kBQ] - e0;
+  const f16x4 t5 = tab[511 ^ 0x100];
+  for (int e = tid; e < ecount && e < kEntCap; e += kGT) {
+    const int gi = e0 + e;
+    const int col = a.O_col[gi];
+    int q = 0;
+#pragma unroll
+    for (int r = 1; r < kBQ; ++r) q += (gi >= rps[r]) ? 1 : 0;
+    const f16x8 o = *(const f16x8*)(a.O + (size_t)gi * 8);
+    const f16 hc = a.h[col];
+    f16 hs = hc;
+    if (HAS_S) {
+      const int g2 = (8 * (m0 + q)) / a.qb;
+      hs = (f16)((float)hc * (float)a.S[(size_t)g2 * N + col]);
+    }
+    h8 d;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const f16 wm_marker = (f16)((float)t5[k & 3] * (float)hs);   // what the tile holds
+      d[k] = (f16)((float)o[k] * (float)hc - (float)wm_marker);
+    }
+    ent_col[e] = col;
+    ent_delta[e] = d;
+  }
+  __syncthreads();   // staged entries are read by the walkers and the waves
+  // Walker thread q (tid < 16) owns Q-row q's entry cursor.
+  int wcur = 0, wend = 0;
+  if (tid < kBQ) {
+    wcur = rps[tid] - e0;
+    wend = rps[tid + 1] - e0;
+  }
+
+  // ---- register ring: the global loads of the next kPF steps are in flight ----
+  constexpr int kPF = 3;
+  uint32_t qw[kPF], hsw[kPF];
+  u32x4 xr[kPF][2];
+  auto load_step = [&](int slot, int s) {
+    const int k0 = (s < nsteps ? s : nsteps - 1) * kBK;
+    qw[slot] = qsrc[(k0 + dc) >> 1];
+    uint32_t hw = *(const uint32_t*)(a.h + k0 + dc);
+    if (HAS_S) hw = gpk_mul(hw, *(const uint32_t*)(a.S + (size_t)grp * N + k0 + dc));
+    hsw[slot] = hw;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      // Tokens past T read a valid row; their output columns are never stored.
+      const int tt = t0 + xt[i];
+      xr[slot][i] = *(const u32x4*)(a.x + (size_t)(tt < T ? tt : T - 1) * N + k0 + xc[i]);
+    }
+  };
+
+  // Step pipeline: the 4 table lookups of the next step are issued before
+  // this step's MFMAs and the W/X tiles of the next step are written after
+  // them, so LDS latency and dequantization overlap the matrix work.
+  u32x2 lk[4];
+  auto lookups = [&](int slot) {
+    const uint32_t w = qw[slot];
+    const uint32_t a1lo = (w >> 4) & 0xFF8u;
+    const uint32_t a1hi = (w >> 20) & 0xFF8u;
+    const uint32_t a2lo = bfi(0x3F8u, w << 3, a1lo);
+    const uint32_t a2hi = bfi(0x3F8u, w >> 13, a1hi);
+    lk[0] = *(const u32x2*)(tabB + a1lo);
+    lk[1] = *(const u32x2*)(tabB + a2lo);
+    lk[2] = *(const u32x2*)(tabB + a1hi);
+    lk[3] = *(const u32x2*)(tabB + a2hi);
+  };
+  auto write_tiles = [&](int slot, int buf, int k0) {
+    const u32x2 t1l = lk[0], t2l = lk[1], t1h = lk[2], t2h = lk[3];
+    uint32_t pr[8];
+    pr[0] = gperm(t1h[0], t1l[0], 0x05040100u);
+    pr[1] = gperm(t1h[0], t1l[0], 0x07060302u);
+    pr[2] = gperm(t1h[1], t1l[1], 0x05040100u);
+    pr[3] = gperm(t1h[1], t1l[1], 0x07060302u);
+    pr[4] = gperm(t2h[0], t2l[0], 0x05040100u);
+    pr[5] = gperm(t2h[0], t2l[0], 0x07060302u);
+    pr[6] = gperm(t2h[1], t2l[1], 0x05040100u);
+    pr[7] = gperm(t2h[1], t2l[1], 0x07060302u);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) *(uint32_t*)&Ws[buf][8 * dq + k][dc] = gpk_mul(pr[k], hsw[slot]);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) *(u32x4*)&Xs[buf][xt[i]][xc[i]] = xr[slot][i];
+    // Walkers: list this step's critical blocks per Q-row; bit q of the
+    // step mask says Q-row q has some.
+    int nw = 0;
+    if (tid < kBQ) {
+      while (wcur < wend && wcur < kEntCap && ent_col[wcur] < k0 + kBK) {
+        lst[buf][tid][nw++] = (uint16_t)wcur;
+        ++wcur;
+      }
+      lcnt[buf][tid] = nw;
+    }
+    if (tid < 64) {   // the walkers are lanes 0..15 of wave 0
+      const unsigned long long b = __ballot(nw > 0);
+      if (tid == 0) lmask[buf] = (unsigned)b;
+    }
+  };
+
+#pragma unroll
+  for (int p = 0; p < kPF; ++p) load_step(p, p);
+
+  f32x4 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+  // prologue: step 0's tiles
+  lookups(0);
+  write_tiles(0, 0, 0);
+  load_step(0, kPF);
+  __syncthreads();
+
+  for (int s0 = 0; s0 < nsteps; s0 += kPF) {
+#pragma unroll
+  for (int p = 0; p < kPF; ++p) {
+    const int s = s0 + p;
+    if (s >= nsteps) break;
+    const int buf = s & 1;
+    const int k0 = s * kBK;
+    const int pn = (p + 1) % kPF;              // ring slot holding step s + 1
+    const bool more = s + 1 < nsteps;
+
+    h8 af[4], bf[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      af[i] = *(const h8*)&Ws[buf][64 * wm + 16 * i + (lane & 15)][8 * (lane >> 4)];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      bf[j] = *(const h8*)&Xs[buf][64 * wn + 16 * j + (lane & 15)][8 * (lane >> 4)];
+    if (more) lookups(pn);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+    if (more) {
+      write_tiles(pn, buf ^ 1, k0 + kBK);
+      load_step(pn, s + 1 + kPF);
+    }
+
+    // -- critical-block corrections of this step for this wave's 8 Q-rows --
+    // D layout: lane holds rows 4·(lane/16)+v of a 16-row tile, token lane%16.
+    const unsigned rows_here = (lmask[buf] >> (8 * wm)) & 0xFFu;
+    if (rows_here) {
+      for (int qq = 0; qq < 8; ++qq) {
+        if (!((rows_here >> qq) & 1u)) continue;   // uniform
+        const int q = 8 * wm + qq;
+        const int n = lcnt[buf][q];
+        const int ti = qq >> 1;                    // 16-row tile holding rows 8q..8q+7
+        const int lg = lane >> 4;
+        const bool mine = (lg >> 1) == (qq & 1);   // lane groups 2(q%2), 2(q%2)+1
+        for (int e = 0; e < n; ++e) {
+          const int idx = lst[buf][q][e];
+          const int c = ent_col[idx] - k0;
+          const h8 d = ent_delta[idx];
+          if (mine) {
+            const int kb = 4 * (lg & 1);           // first of this lane's 4 rows within 8q..
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const float xv = (float)Xs[buf][64 * wn + 16 * j + (lane & 15)][c];
+#pragma unroll
+              for (int v = 0; v < 4; ++v) acc[ti][j][v] += (float)d[kb + v] * xv;
+            }
+          }
+        }
+      }
+    }
+    __syncthreads();
+  }
+  }
+
+  // Entries beyond the LDS cap (only for very dense critical-block layers):
+  // apply them from global memory.
+  if (ecount > kEntCap) {
+    __syncthreads();
+    for (int qq = 0; qq < 8; ++qq) {
+      const int q = 8 * wm + qq;
+      const int lo = rps[q] - e0, hi = rps[q + 1] - e0;
+      const int ti = qq >> 1;
+      const int lg = lane >> 4;
+      const bool mine = (lg >> 1) == (qq & 1);
+      for (int e = (lo > kEntCap ? lo : kEntCap); e < hi; ++e) {
+        const int gi = e0 + e;
+        const int col = a.O_col[gi];
+        const f16x8 o = *(const f16x8*)(a.O + (size_t)gi * 8);
+        const f16 hc = a.h[col];
+        f16 hs = hc;
+        if (HAS_S) hs = (f16)((float)hc * (float)a.S[(size_t)((8 * (m0 + q)) / a.qb) * N + col]);
+        if (mine) {
+          const int kb = 4 * (lg & 1);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int tt = t0 + 64 * wn + 16 * j + (lane & 15);
+            const float xv = tt < T ? (float)__builtin_bit_cast(f16, a.x[(size_t)tt * N + col]) : 0.f;
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+              const int k = kb + v;
+              const f16 wmk = (f16)((float)t5[k & 3] * (float)hs);
+              const float dv = (float)(f16)((float)o[k] * (float)hc - (float)wmk);
+              acc[ti][j][v] += dv * xv;
+            }
+          }
+        }
+      }
+    }
+  }
+
+  // ---- epilogue: g, bias, fp16 ----
+  const int lg = lane >> 4;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r0 = 8 * m0 + 64 * wm + 16 * i + 4 * lg;   // first of this lane's 4 rows
+    if (r0 >= 8 * M) continue;
+    float gv[4], bv[4];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      gv[v] = (float)a.g[r0 + v];
+      bv[v] = a.bias ? (float)a.bias[r0 + v] : 0.0f;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int tt = t0 + 64 * wn + 16 * j + (lane & 15);
+      if (tt >= T) continue;
+      f16x4 o;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) o[v] = (f16)(acc[i][j][v] * gv[v] + bv[v]);
+      *(f16x4*)((f16*)a.y + (size_t)tt * (8 * M) + r0) = o;
+    }
+  }
+}
+
 int launch_gemm_e8d4(const LinearArgs& a, hipStream_t s) {
+  // MFMA path: fp16 activations, fp16 table, whole 16-Q-row tiles, K-steps
+  // of 32.  Anything else takes batch tiles of the decode matvec.
+  const bool mfma_ok = !a.x_bf16 && !a.codes_f32 && (a.N % kBK) == 0 && (a.M % kBQ) == 0 &&
+                       (!a.S || (a.qb % 8) == 0);
+  if (mfma_ok) {
+    const int OB = a.M / kBQ;
+    const int TB = (a.B + kBN - 1) / kBN;
+    const long grid = (long)OB * TB;
+    if (grid <= 0x7fffffff) {
+      if (a.S) k_gemm_e8d4<true><<<(unsigned)grid, kGT, 0, s>>>(a, OB);
+      else k_gemm_e8d4<false><<<(unsigned)grid, kGT, 0, s>>>(a, OB);
+      return 0;
+    }
+  }
   for (int b0 = 0; b0 < a.B; b0 += kMatvecMaxBatch) {
     LinearArgs t = a;
     t.B = a.B - b0 < kMatvecMaxBatch ? a.B - b0 : kMatvecMaxBatch;

@@ -1,0 +1,234 @@
+"""Self-contained Llama decoder whose Linears are ``EPTQLinear`` (synthetic weights).
+
+Counterpart of the reference's decode benchmark driver (``bench_decode.py:44-71``:
+prefill untimed, then a timed token-by-token loop over a static KV cache),
+without HuggingFace model loading: the model is built from its config with
+every decoder Linear (q/k/v/o, gate/up/down) a synthetic E8-D4
+``QuantizedLayerData`` and the embedding, norms and ``lm_head`` random fp16
+(the reference keeps ``lm_head`` unquantized, ``quantize.py:86-90``).
+
+The decode step has static shapes (the KV cache is preallocated and the
+current position lives in a device tensor), so it is captured once in a HIP
+graph and replayed per token.  Greedy decoding.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from typing import List, Optional
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from .kernels.linear import EPTQLinear
+from .quantizers import E8D4Quantizer
+from .synthetic import make_layer
+
+
+@dataclass
+class LlamaConfig:
+    hidden: int = 4096
+    ffn: int = 11008
+    layers: int = 32
+    heads: int = 32
+    kv_heads: int = 32
+    vocab: int = 32000
+    rope_theta: float = 10000.0
+    eps: float = 1e-5
+
+    @property
+    def head_dim(self) -> int:
+        return self.hidden // self.heads
+
+
+LLAMA2_7B = LlamaConfig()
+
+
+class RMSNorm(nn.Module):
+    def __init__(self, dim: int, eps: float):
+        super().__init__()
+        self.weight = nn.Parameter(torch.ones(dim, dtype=torch.float16), requires_grad=False)
+        self.eps = eps
+
+    def forward(self, x):
+        xf = x.float()
+        xf = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + self.eps)
+        return (xf * self.weight.float()).to(x.dtype)
+
+
+def _rope(x, cos, sin):
+    # x: (B, H, T, D); rotate halves as in the HF Llama implementation
+    d = x.shape[-1] // 2
+    x1, x2 = x[..., :d], x[..., d:]
+    rot = torch.cat((-x2, x1), dim=-1)
+    return (x.float() * cos + rot.float() * sin).to(x.dtype)
+
+
+class DecoderLayer(nn.Module):
+    def __init__(self, cfg: LlamaConfig, linears: dict):
+        super().__init__()
+        self.cfg = cfg
+        self.input_layernorm = RMSNorm(cfg.hidden, cfg.eps)
+        self.post_attention_layernorm = RMSNorm(cfg.hidden, cfg.eps)
+        for name, mod in linears.items():
+            setattr(self, name, mod)
+
+    def forward(self, x, cos, sin, kc, vc, pos, mask):
+        """x: (B, T, hidden); kc: (B, Hkv, D, L) and vc: (B, Hkv, L, D) cache; pos: (T,) positions;
+        mask: (T, L) additive attention mask."""
+        cfg = self.cfg
+        B, T, _ = x.shape
+        H, Hk, D = cfg.heads, cfg.kv_heads, cfg.head_dim
+        h = self.input_layernorm(x)
+        q = self.q_proj(h).view(B, T, H, D).transpose(1, 2)
+        k = self.k_proj(h).view(B, T, Hk, D).transpose(1, 2)
+        v = self.v_proj(h).view(B, T, Hk, D).transpose(1, 2)
+        q = _rope(q, cos, sin).contiguous()
+        k = _rope(k, cos, sin)
+        # K is cached transposed, (B, Hkv, D, L), so both attention products
+        # take contiguous operands.
+        kc.index_copy_(3, pos, k.transpose(2, 3))
+        vc.index_copy_(2, pos, v)
+        kk, vv = kc, vc
+        if Hk != H:
+            kk = kk.repeat_interleave(H // Hk, dim=1)
+            vv = vv.repeat_interleave(H // Hk, dim=1)
+        s = torch.matmul(q, kk).float() * (1.0 / math.sqrt(D)) + mask
+        p = torch.softmax(s, dim=-1).to(x.dtype)
+        o = torch.matmul(p, vv)
+        o = o.transpose(1, 2).reshape(B, T, H * D)
+        x = x + self.o_proj(o)
+        h = self.post_attention_layernorm(x)
+        a = F.silu(self.gate_proj(h).float()) * self.up_proj(h).float()
+        x = x + self.down_proj(a.to(x.dtype))
+        return x
+
+
+class QuantLlama(nn.Module):
+    """Llama with EPTQ-quantized decoder Linears and a static KV cache."""
+
+    def __init__(self, cfg: LlamaConfig, layers: List[DecoderLayer], embed, norm, lm_head):
+        super().__init__()
+        self.cfg = cfg
+        self.layers = nn.ModuleList(layers)
+        self.embed_tokens = embed
+        self.norm = norm
+        self.lm_head = lm_head
+        self.kc: Optional[list] = None
+
+    def alloc_cache(self, batch: int, max_len: int, device):
+        cfg = self.cfg
+        kshape = (batch, cfg.kv_heads, cfg.head_dim, max_len)
+        vshape = (batch, cfg.kv_heads, max_len, cfg.head_dim)
+        self.kc = [torch.zeros(kshape, dtype=torch.float16, device=device) for _ in self.layers]
+        self.vc = [torch.zeros(vshape, dtype=torch.float16, device=device) for _ in self.layers]
+        self.max_len = max_len
+        inv = 1.0 / (cfg.rope_theta ** (torch.arange(0, cfg.head_dim, 2, device=device).float() / cfg.head_dim))
+        t = torch.arange(max_len, device=device).float()
+        f = torch.outer(t, inv)
+        emb = torch.cat((f, f), dim=-1)
+        self.cos_tab, self.sin_tab = emb.cos(), emb.sin()
+
+    def forward_tokens(self, ids, pos):
+        """ids: (B, T) int64, pos: (T,) int64 positions -> logits (B, T, vocab)."""
+        x = self.embed_tokens(ids)
+        T = ids.shape[1]
+        cos = self.cos_tab.index_select(0, pos)[None, None]
+        sin = self.sin_tab.index_select(0, pos)[None, None]
+        L = self.max_len
+        allowed = torch.arange(L, device=ids.device)[None, :] <= pos[:, None]
+        mask = torch.zeros((T, L), dtype=torch.float32, device=ids.device).masked_fill(~allowed, float("-inf"))
+        for i, layer in enumerate(self.layers):
+            x = layer(x, cos, sin, self.kc[i], self.vc[i], pos, mask)
+        x = self.norm(x)
+        return self.lm_head(x)
+
+
+def build_synthetic(cfg: LlamaConfig = LLAMA2_7B, device="cuda", seed: int = 4000,
+                    percmask: float = 0.002, radius: float = 1.75) -> QuantLlama:
+    """Random-init Llama whose decoder Linears are synthetic E8-D4 layers."""
+    quant = E8D4Quantizer(device=str(device), radius=radius)
+    shapes = {"q_proj": (cfg.hidden, cfg.hidden),
+              "k_proj": (cfg.kv_heads * cfg.head_dim, cfg.hidden),
+              "v_proj": (cfg.kv_heads * cfg.head_dim, cfg.hidden),
+              "o_proj": (cfg.hidden, cfg.hidden),
+              "gate_proj": (cfg.ffn, cfg.hidden),
+              "up_proj": (cfg.ffn, cfg.hidden),
+              "down_proj": (cfg.hidden, cfg.ffn)}
+    gen = torch.Generator(device=device).manual_seed(seed)
+    layers = []
+    for li in range(cfg.layers):
+        lin = {}
+        for idx, (name, (out, inp)) in enumerate(shapes.items()):
+            qd = make_layer(out, inp, seed=seed + 10 * li + idx, percmask=percmask, device=device)
+            lin[name] = EPTQLinear.from_quantized_data(qd, quant, "e8_d4")
+        layer = DecoderLayer(cfg, lin)
+        with torch.no_grad():
+            layer.input_layernorm.weight.copy_(1.0 + 0.05 * torch.randn(cfg.hidden, generator=gen, device=device))
+            layer.post_attention_layernorm.weight.copy_(1.0 + 0.05 * torch.randn(cfg.hidden, generator=gen, device=device))
+        layers.append(layer.to(device))
+    embed = nn.Embedding(cfg.vocab, cfg.hidden).to(device=device, dtype=torch.float16)
+    lm_head = nn.Linear(cfg.hidden, cfg.vocab, bias=False).to(device=device, dtype=torch.float16)
+    norm = RMSNorm(cfg.hidden, cfg.eps).to(device)
+    with torch.no_grad():
+        embed.weight.copy_(torch.randn(cfg.vocab, cfg.hidden, generator=gen, device=device) * 0.02)
+        lm_head.weight.copy_(torch.randn(cfg.vocab, cfg.hidden, generator=gen, device=device) * 0.02)
+    embed.weight.requires_grad_(False)
+    lm_head.weight.requires_grad_(False)
+    return QuantLlama(cfg, layers, embed, norm, lm_head).eval()
+
+
+class GraphDecoder:
+    """Greedy decode with the per-token step captured in a HIP graph."""
+
+    def __init__(self, model: QuantLlama, batch: int, max_len: int, device="cuda"):
+        self.model = model
+        self.batch = batch
+        self.device = torch.device(device)
+        model.alloc_cache(batch, max_len, self.device)
+        self.tok = torch.zeros((batch, 1), dtype=torch.long, device=self.device)
+        self.pos = torch.zeros((1,), dtype=torch.long, device=self.device)
+        self.graph = None
+
+    @torch.no_grad()
+    def prefill(self, prompt: torch.Tensor) -> torch.Tensor:
+        T = prompt.shape[1]
+        pos = torch.arange(T, device=self.device)
+        logits = self.model.forward_tokens(prompt, pos)
+        nxt = logits[:, -1].argmax(-1, keepdim=True)
+        self.tok.copy_(nxt)
+        self.pos.fill_(T)
+        return nxt
+
+    @torch.no_grad()
+    def _step(self):
+        logits = self.model.forward_tokens(self.tok, self.pos)
+        self.tok.copy_(logits[:, -1].argmax(-1, keepdim=True))
+        self.pos.add_(1)
+
+    @torch.no_grad()
+    def capture(self):
+        # Warm up on a side stream (allocator and kernels), then capture.
+        saved_tok, saved_pos = self.tok.clone(), self.pos.clone()
+        side = torch.cuda.Stream(device=self.device)
+        side.wait_stream(torch.cuda.current_stream(self.device))
+        with torch.cuda.stream(side):
+            self._step()
+        torch.cuda.current_stream(self.device).wait_stream(side)
+        self.tok.copy_(saved_tok)
+        self.pos.copy_(saved_pos)
+        torch.cuda.synchronize(self.device)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self._step()
+        self.tok.copy_(saved_tok)
+        self.pos.copy_(saved_pos)
+        torch.cuda.synchronize(self.device)
+
+    def step(self):
+        if self.graph is None:
+            self._step()
+        else:
+            self.graph.replay()
