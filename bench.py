@@ -1,28 +1,50 @@
 #!/usr/bin/env python3
 """Benchmark: E8-D4 fused decode matvec on synthetic Llama-2-7B layers, one MI355X.
 
-Workload (batch 1): the seven quantized Linears of
-every one of Llama-2-7B's 32 decoder layers — q/k/v/o 4096x4096, gate/up
-11008x4096, down 4096x11008 — E8-D4 codebook at radius 1.75, 0.1% critical
-blocks, seeded synthetic indices and scales.  One step = one token's worth of
-quantized-Linear work: 224 launches over 32 distinct layers (1.66 GB of
-algorithmic bytes, far above the 256 MB MALL, so the bytes come from HBM).
-The step is captured once in a HIP graph and replayed.
+Workload (``config.workload`` = llama2_7b_decoder_linears_decode; BASELINE
+configuration 1 at batch 1): the seven quantized Linears of each of
+Llama-2-7B's 32 decoder layers — q/k/v/o 4096x4096, gate/up 11008x4096, down
+4096x11008 — E8-D4 codebook at radius 1.75, 0.1% critical blocks, seeded
+synthetic indices and scales, generated on the GPU.  One step = one token's
+quantized-Linear work: 224 launches over 224 distinct layers (1.66 GB of
+algorithmic bytes, far above the 256 MB MALL, so the bytes stream from HBM).
+The step is captured once in a HIP graph and replayed ``--steps`` times.
 
-Reported: ``value`` = algorithmic GB/s over the timed steps (inputs resident
-in HBM), ``roofline`` for the matvec kernel (algorithmic bytes per launch over
-its average launch duration measured with HIP events on the launch stream),
-and ``cpu_baseline`` = the reference CPU path (dequantize_layer restatement +
-fp32 matmul) on one q_proj layer, timed on this host's cores.
+JSON fields beyond the driver contract:
+
+* ``roofline`` — the decode kernel: algorithmic bytes per launch (mean over
+  the 224 launches) over the mean launch duration, which is the HIP-event time
+  of the timed graph replays (recorded on the stream the graph is launched
+  on) divided by the launches they hold; every launch in the step is this
+  kernel.  ``per_shape`` times each shape's 32 launches back to back with
+  events around the group and the queue backed up by a device sleep.  ``traffic`` = HBM bytes
+  per launch from two ``rocprofv3 --pmc`` passes (FETCH_SIZE, WRITE_SIZE) over
+  one step, each scaled by the same counter's reading for a 512 MiB device
+  copy; the passes run as child processes before this process touches the GPU.
+* ``e2e`` — tokens/s of the synthetic Llama-2-7B (every decoder Linear a
+  synthetic E8-D4 layer): 128-token prompt, greedy
+  decode, graph-captured step, prefill untimed, batch 1 and 8.
+* ``prefill`` — the MFMA GEMM on the Llama-2-13B shapes at 2048 tokens
+  TFLOP/s and fraction of the 2.5 PFLOP/s fp16
+  dense MFMA peak.
+* ``cpu_baseline`` — the reference CPU path (per-column ``dequantize_layer``
+  restatement + fp32 ``torch.matmul``) on one decoder layer's seven Linears at
+  batch 1, timed on this host's cores.
 """
 
 from __future__ import annotations
 
 import argparse
+import csv
+import glob
 import json
 import os
+import shutil
+import signal
 import statistics
+import subprocess
 import sys
+import tempfile
 import time
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
@@ -31,8 +53,12 @@ if ROOT not in sys.path:
 
 METRIC = "dequant-matvec GB/s (% HBM peak); tok/s synthetic Llama-2-7B bs=1"
 HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0
 LLAMA2_7B = [("q", 4096, 4096), ("k", 4096, 4096), ("v", 4096, 4096), ("o", 4096, 4096),
              ("gate", 11008, 4096), ("up", 11008, 4096), ("down", 4096, 11008)]
+LLAMA2_13B = [("qkvo", 5120, 5120), ("gate_up", 13824, 5120), ("down", 5120, 13824)]
+DECODE_KERNEL = "k_decode_e8d4"
+CALIB_BYTES = 512 << 20
 
 
 def algo_bytes(out, inp, B, nnz, bias=False, n_groups=0):
@@ -43,9 +69,168 @@ def algo_bytes(out, inp, B, nnz, bias=False, n_groups=0):
             + (2 * out if bias else 0) + 2 * B * inp + 2 * B * out)
 
 
+# ---------------------------------------------------------------------------
+# Workload
+# ---------------------------------------------------------------------------
+
+def make_workload(torch, dev, n_layers, B):
+    from eptq_amd.quantizers import E8D4Quantizer
+    from eptq_amd.synthetic import make_layer, make_x
+
+    codes = E8D4Quantizer(radius=1.75).flat_table().half().to(dev)
+
+    def csr(Q):
+        rows, cols = (Q == 32767).nonzero(as_tuple=True)
+        counts = torch.bincount(rows, minlength=Q.shape[0])
+        rp = torch.cat([torch.zeros(1, dtype=torch.int32, device=dev), counts.cumsum(0).to(torch.int32)])
+        return cols.to(torch.int32), rp
+
+    layers = []
+    for li in range(n_layers):
+        for idx, (name, out, inp) in enumerate(LLAMA2_7B):
+            qd = make_layer(out, inp, seed=1000 + 10 * li + idx, percmask=0.001, device=dev)
+            ocol, orp = csr(qd.Q)
+            layers.append(dict(name=name, out=out, inp=inp, Q=qd.Q, g=qd.g, h=qd.h,
+                               O=qd.O, O_col=ocol, O_row_ptr=orp, nnz=int(qd.O.shape[0])))
+    xs = {inp: make_x(B, inp, seed=7 + inp, device=dev) for inp in {l["inp"] for l in layers}}
+    ys = {out: torch.empty((B, out), dtype=torch.float16, device=dev) for out in {l["out"] for l in layers}}
+    return codes, layers, xs, ys
+
+
+def make_launcher(codes, xs, ys):
+    """Return launch(layer, stream) with argument pointers resolved once per layer."""
+    from eptq_amd.kernels import _lib
+    lib = _lib.load()
+    fn = lib.eptq_e8d4_forward
+
+    def p(t):
+        return None if t is None or t.numel() == 0 else t.data_ptr()
+
+    def launch(l, stream):
+        args = l.get("_args")
+        if args is None:
+            x, y = xs[l["inp"]], ys[l["out"]]
+            args = (p(l["Q"]), p(codes), _lib.EPTQ_F16, p(l["g"]), p(l["h"]), p(x), _lib.EPTQ_F16,
+                    p(l["O"]), p(l["O_col"]), p(l["O_row_ptr"]), None, None, 0,
+                    int(l["Q"].shape[0]), int(l["Q"].shape[1]), int(x.shape[0]), p(y))
+            l["_args"] = args
+        rc = fn(*args, stream)
+        if rc:
+            _lib.check(rc, "eptq_e8d4_forward")
+
+    return launch
+
+
+def event_timed(torch, fns, stream, sleep_cycles=20_000_000):
+    """GPU duration (ms) of each of ``fns`` launched back to back on ``stream``.
+
+    Consecutive launches are separated by timing events; a device sleep ahead
+    of them keeps the queue backed up so that host-side launch overhead falls
+    outside the brackets.  Returns (durations, backed_up)."""
+    n = len(fns)
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(n + 1)]
+    backed = False
+    for _ in range(4):
+        with torch.cuda.stream(stream):
+            torch.cuda._sleep(sleep_cycles)
+            guard = torch.cuda.Event()
+            guard.record(stream)
+            evs[0].record(stream)
+            for i, f in enumerate(fns):
+                f()
+                evs[i + 1].record(stream)
+            backed = not guard.query()
+        torch.cuda.synchronize()
+        if backed:
+            break
+        sleep_cycles *= 4
+    return [evs[i].elapsed_time(evs[i + 1]) for i in range(n)], backed
+
+
+# ---------------------------------------------------------------------------
+# HBM traffic from rocprofv3 counters (child processes, before GPU init here)
+# ---------------------------------------------------------------------------
+
+def traffic_probe(args):
+    """Child of ``rocprofv3 --pmc``: one 512 MiB calibration copy, then one
+    eager step of the decode workload."""
+    import torch
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    codes, layers, xs, ys = make_workload(torch, dev, args.layers, args.batch)
+    src = torch.ones(CALIB_BYTES, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+    launch = make_launcher(codes, xs, ys)
+    s = torch.cuda.current_stream().cuda_stream
+    for l in layers:
+        launch(l, s)
+    torch.cuda.synchronize()
+    print("probe done", flush=True)
+
+
+def _pmc_pass(counter, args, tmp):
+    rocprof = shutil.which("rocprofv3")
+    if rocprof is None:
+        raise RuntimeError("rocprofv3 not found")
+    out = os.path.join(tmp, counter)
+    cmd = [rocprof, "--pmc", counter, "--output-format", "csv", "-d", out, "-o", "p", "--",
+           sys.executable, "-u", os.path.abspath(__file__), "--probe-traffic",
+           "--layers", str(args.layers), "--batch", str(args.batch)]
+    proc = subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT,
+                            start_new_session=True, text=True)
+    try:
+        log, _ = proc.communicate(timeout=args.pmc_timeout)
+    except subprocess.TimeoutExpired:
+        os.killpg(proc.pid, signal.SIGKILL)
+        proc.communicate()
+        raise RuntimeError(f"rocprofv3 --pmc {counter} timed out")
+    if proc.returncode != 0 and "probe done" not in log:
+        raise RuntimeError(f"rocprofv3 --pmc {counter} exited {proc.returncode}: {log[-400:]}")
+    files = glob.glob(os.path.join(out, "**", "*counter_collection.csv"), recursive=True)
+    if not files:
+        raise RuntimeError(f"no counter_collection.csv from the {counter} pass")
+    per_dispatch = {}
+    with open(files[0], newline="") as f:
+        for row in csv.DictReader(f):
+            if row["Counter_Name"] != counter:
+                continue
+            key = row["Dispatch_Id"]
+            d = per_dispatch.setdefault(key, {"name": row["Kernel_Name"], "v": 0.0})
+            d["v"] += float(row["Counter_Value"])
+    calib = [d["v"] for d in per_dispatch.values() if "copyBuffer" in d["name"]]
+    dec = [d["v"] for d in per_dispatch.values() if DECODE_KERNEL in d["name"]]
+    if not calib or not dec:
+        raise RuntimeError(f"{counter}: calibration copy or decode dispatches missing")
+    kib_copy = max(calib)
+    factor = CALIB_BYTES / (kib_copy * 1024.0)
+    return {"counter": counter, "copy_kib": kib_copy, "factor": round(factor, 4),
+            "decode_dispatches": len(dec),
+            "bytes_per_launch": statistics.fmean(dec) * 1024.0 * factor}
+
+
+def measure_traffic(args):
+    tmp = tempfile.mkdtemp(prefix="eptq_pmc_")
+    try:
+        fetch = _pmc_pass("FETCH_SIZE", args, tmp)
+        write = _pmc_pass("WRITE_SIZE", args, tmp)
+    finally:
+        shutil.rmtree(tmp, ignore_errors=True)
+    return {"bytes_per_launch": fetch["bytes_per_launch"] + write["bytes_per_launch"],
+            "fetch": fetch, "write": write}
+
+
+# ---------------------------------------------------------------------------
+# Side measurements
+# ---------------------------------------------------------------------------
+
 def cpu_baseline(seed=1000):
-    """Reference CPU path on one Llama-2-7B q_proj at B=1: the per-column
-    dequantize_layer restatement (algorithms/eptq.py:406-471) + fp32 matmul."""
+    """Reference CPU path on one Llama-2-7B decoder layer's seven Linears at
+    B=1: per-column dequantize_layer restatement (algorithms/eptq.py:406-471)
+    followed by an fp32 torch.matmul, per Linear."""
     import torch
     from eptq_amd.quantizers import E8D4Quantizer
     from eptq_amd.synthetic import make_layer, make_x
@@ -53,24 +238,100 @@ def cpu_baseline(seed=1000):
 
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
-    qd = make_layer(4096, 4096, seed=seed, percmask=0.001)
-    x = make_x(1, 4096, seed=seed + 1)
     tab = E8D4Quantizer(radius=1.75).flat_table().numpy()
+    work = []
+    for idx, (name, out, inp) in enumerate(LLAMA2_7B):
+        qd = make_layer(out, inp, seed=seed + idx, percmask=0.001)
+        work.append((qd, make_x(1, inp, seed=seed + 100 + idx), algo_bytes(out, inp, 1, qd.O.shape[0])))
+    total_bytes = sum(w[2] for w in work)
     times = []
     for _ in range(3):
         t0 = time.perf_counter()
-        W = dequantize_layer_torch_loop(qd.Q.numpy(), qd.g.numpy(), qd.h.numpy(), qd.O.numpy(),
-                                        tab, "e8_d4")
-        y = torch.matmul(x.float(), W.float().T)
+        for qd, x, _ in work:
+            W = dequantize_layer_torch_loop(qd.Q.numpy(), qd.g.numpy(), qd.h.numpy(), qd.O.numpy(),
+                                            tab, "e8_d4")
+            y = torch.matmul(x.float(), W.float().T)
         times.append(time.perf_counter() - t0)
     del y
-    t = statistics.median(times)
-    nbytes = algo_bytes(4096, 4096, 1, qd.O.shape[0])
-    return {"value": round(nbytes / t / 1e9, 6), "unit": "GB/s", "cores": torch.get_num_threads(),
+    t = min(times)
+    return {"value": round(total_bytes / t / 1e9, 6), "unit": "GB/s", "cores": torch.get_num_threads(),
             "kind": "port",
-            "sample": f"one q_proj 4096x4096 B=1 (E8-D4 r=1.75, p=0.001): per-column "
-                      f"dequantize_layer + fp32 torch.matmul, median of 3 = {t:.3f} s"}
+            "sample": f"one Llama-2-7B decoder layer (q,k,v,o,gate,up,down; E8-D4 r=1.75, p=0.001) "
+                      f"at B=1: per-column dequantize_layer + fp32 torch.matmul per Linear, "
+                      f"best of 3 = {t:.2f} s for {total_bytes} algorithmic bytes"}
 
+
+def e2e_decode(torch, dev, batches=(1, 8), new_tokens=256, prompt_len=128):
+    """Synthetic Llama-2-7B greedy decode tok/s (prefill untimed)."""
+    from eptq_amd.llama import LLAMA2_7B as CFG, GraphDecoder, build_synthetic
+    model = build_synthetic(CFG, device=dev, percmask=0.002)
+    res = {}
+    for B in batches:
+        dec = GraphDecoder(model, B, prompt_len + new_tokens, device=dev)
+        gen = torch.Generator(device=dev).manual_seed(11)
+        prompt = torch.randint(0, CFG.vocab, (B, prompt_len), generator=gen, device=dev)
+        dec.prefill(prompt)
+        dec.capture()
+        best = None
+        for _ in range(2):
+            torch.cuda.synchronize()
+            tp = time.perf_counter()
+            dec.prefill(prompt)
+            torch.cuda.synchronize()
+            prefill_s = time.perf_counter() - tp
+            t0 = time.perf_counter()
+            for _ in range(new_tokens - 1):
+                dec.step()
+            torch.cuda.synchronize()
+            dt = time.perf_counter() - t0
+            if best is None or dt < best[0]:
+                best = (dt, prefill_s)
+        dt, prefill_s = best
+        res[f"b{B}"] = {"tok_s": round(B * (new_tokens - 1) / dt, 1),
+                        "tok_s_per_seq": round((new_tokens - 1) / dt, 1),
+                        "ms_per_token_step": round(dt / (new_tokens - 1) * 1e3, 3),
+                        "prefill_ms": round(prefill_s * 1e3, 2)}
+        del dec
+    del model
+    torch.cuda.empty_cache()
+    res["config"] = {"model": "llama-2-7b (random init)", "prompt_len": prompt_len,
+                     "new_tokens": new_tokens, "codebook": "e8_d4", "radius": 1.75,
+                     "percmask": 0.002, "lm_head": "fp16", "hip_graph": True,
+                     "timing": "(new_tokens-1) decode steps after an untimed prefill, best of 2"}
+    return res
+
+
+def prefill_gemm(torch, dev, T=2048, reps=10):
+    from eptq_amd.kernels import _lib
+    from eptq_amd.quantizers import E8D4Quantizer
+    from eptq_amd.synthetic import make_layer, make_x
+
+    codes = E8D4Quantizer(radius=1.75).flat_table().half().to(dev)
+    stream = torch.cuda.current_stream()
+    out = {}
+    for idx, (name, o, i) in enumerate(LLAMA2_13B):
+        qd = make_layer(o, i, seed=3000 + idx, percmask=0.002, device=dev)
+        rows, cols = (qd.Q == 32767).nonzero(as_tuple=True)
+        rp = torch.cat([torch.zeros(1, dtype=torch.int32, device=dev),
+                        torch.bincount(rows, minlength=qd.Q.shape[0]).cumsum(0).to(torch.int32)])
+        cols = cols.to(torch.int32)
+        x = make_x(T, i, seed=3100 + idx, device=dev)
+        y = torch.empty((T, o), dtype=torch.float16, device=dev)
+
+        def f():
+            _lib.forward_into("e8_d4", qd.Q, codes, qd.g, qd.h, x, qd.O, cols, rp, None, None,
+                              y, stream.cuda_stream)
+        f()
+        d, _ = event_timed(torch, [f] * reps, stream)
+        us = statistics.median(d) * 1e3
+        tflops = 2.0 * T * o * i / (us * 1e-6) / 1e12
+        out[name] = {"shape": f"{o}x{i}", "tokens": T, "us": round(us, 1), "tflops": round(tflops, 1),
+                     "frac_mfma_f16": round(tflops / MFMA_F16_PEAK_TFLOPS, 4)}
+        del qd, x, y
+    return out
+
+
+# ---------------------------------------------------------------------------
 
 def main():
     ap = argparse.ArgumentParser()
@@ -80,89 +341,80 @@ def main():
     ap.add_argument("--layers", type=int, default=32)
     ap.add_argument("--batch", type=int, default=1)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 --pmc passes")
+    ap.add_argument("--no-e2e", action="store_true")
+    ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--pmc-timeout", type=int, default=240)
+    ap.add_argument("--probe-traffic", action="store_true", help=argparse.SUPPRESS)
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(the quantized Linear is a single-GPU kernel; sharding is a design note).",
+              "(the quantized Linear is a single-GPU kernel; how it would shard is a design note).",
               file=sys.stderr)
         sys.exit(2)
+    if args.probe_traffic:
+        traffic_probe(args)
+        return
+
+    traffic, traffic_note = None, None
+    if not args.no_traffic:
+        try:
+            traffic = measure_traffic(args)
+        except Exception as e:  # counters are evidence, not the measurement itself
+            traffic_note = f"unavailable: {e}"
+        print(f"# traffic: {traffic if traffic else traffic_note}", file=sys.stderr, flush=True)
 
     import torch
-    from eptq_amd.kernels import _lib
-    from eptq_amd.quantizers import E8D4Quantizer
-    from eptq_amd.synthetic import make_layer, make_x
-
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     B = args.batch
-    codes = E8D4Quantizer(radius=1.75).flat_table().half().to(dev)
-
-    def csr(Q):
-        rows, cols = (Q == 32767).nonzero(as_tuple=True)
-        counts = torch.bincount(rows, minlength=Q.shape[0])
-        rp = torch.cat([torch.zeros(1, dtype=torch.int32, device=dev), counts.cumsum(0).to(torch.int32)])
-        return cols.to(torch.int32), rp
-
     t0 = time.time()
-    layers = []
-    for li in range(args.layers):
-        for idx, (name, out, inp) in enumerate(LLAMA2_7B):
-            qd = make_layer(out, inp, seed=1000 + 10 * li + idx, percmask=0.001, device=dev)
-            ocol, orp = csr(qd.Q)
-            layers.append(dict(name=name, out=out, inp=inp, Q=qd.Q, g=qd.g, h=qd.h,
-                               O=qd.O, O_col=ocol, O_row_ptr=orp, nnz=int(qd.O.shape[0])))
-    xs = {inp: make_x(B, inp, seed=7 + inp, device=dev) for inp in {l["inp"] for l in layers}}
-    ys = {out: torch.empty((B, out), dtype=torch.float16, device=dev) for out in {l["out"] for l in layers}}
+    codes, layers, xs, ys = make_workload(torch, dev, args.layers, B)
     torch.cuda.synchronize()
     print(f"# generated {len(layers)} layers in {time.time() - t0:.1f}s", file=sys.stderr, flush=True)
-
     step_bytes = sum(algo_bytes(l["out"], l["inp"], B, l["nnz"]) for l in layers)
+    launch = make_launcher(codes, xs, ys)
 
-    def launch(l, stream):
-        _lib.forward_into("e8_d4", l["Q"], codes, l["g"], l["h"], xs[l["inp"]], l["O"],
-                          l["O_col"], l["O_row_ptr"], None, None, ys[l["out"]], stream)
-
-    def run_step(stream):
-        for l in layers:
-            launch(l, stream)
-
-    # Per-launch kernel durations with HIP events on the launch stream.
     cur = torch.cuda.current_stream()
-    run_step(cur.cuda_stream)
+    for l in layers:
+        launch(l, cur.cuda_stream)
     torch.cuda.synchronize()
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in layers]
-    per_launch = [0.0] * len(layers)
-    reps = 3
-    for _ in range(reps):
-        for i, l in enumerate(layers):
-            evs[i][0].record(cur)
-            launch(l, cur.cuda_stream)
-            evs[i][1].record(cur)
-        torch.cuda.synchronize()
-        for i in range(len(layers)):
-            per_launch[i] += evs[i][0].elapsed_time(evs[i][1]) / reps
-    kern_ms = sum(per_launch)
-    per_shape = {}
-    for i, l in enumerate(layers):
-        d = per_shape.setdefault(l["name"], {"shape": f"{l['out']}x{l['inp']}", "us": 0.0, "n": 0, "bytes": 0})
-        d["us"] += per_launch[i] * 1e3
-        d["n"] += 1
-        d["bytes"] += algo_bytes(l["out"], l["inp"], B, l["nnz"])
-    for d in per_shape.values():
-        d["gbs"] = round(d["bytes"] / (d["us"] * 1e-6) / 1e9, 1)
-        d["us"] = round(d["us"] / d["n"], 3)
-        del d["bytes"], d["n"]
 
-    # Capture one step in a graph and replay it.
+    # Per-shape kernel durations: the launches of each shape back to back on
+    # the launch stream, HIP events around each group, host overhead hidden
+    # behind a device sleep.
+    names = [n for n, _, _ in LLAMA2_7B]
+    groups = {n: [l for l in layers if l["name"] == n] for n in names}
+    fns = [(lambda g=groups[n]: [launch(l, cur.cuda_stream) for l in g]) for n in names]
+    reps = 3
+    group_ms = [0.0] * len(names)
+    all_backed = True
+    for _ in range(reps):
+        d, backed = event_timed(torch, fns, cur)
+        all_backed &= backed
+        for i, v in enumerate(d):
+            group_ms[i] += v / reps
+    per_shape = {}
+    for i, n in enumerate(names):
+        g = groups[n]
+        nbytes = sum(algo_bytes(l["out"], l["inp"], B, l["nnz"]) for l in g)
+        per_shape[n] = {"shape": f"{g[0]['out']}x{g[0]['inp']}",
+                        "us": round(group_ms[i] * 1e3 / len(g), 3),
+                        "gbs": round(nbytes / (group_ms[i] * 1e-3) / 1e9, 1)}
+
+    # The timed region: one step captured in a graph, replayed.
     graph = torch.cuda.CUDAGraph()
     side = torch.cuda.Stream()
     side.wait_stream(cur)
     with torch.cuda.stream(side):
-        run_step(side.cuda_stream)
+        for l in layers:
+            launch(l, side.cuda_stream)
     cur.wait_stream(side)
     torch.cuda.synchronize()
     with torch.cuda.graph(graph):
-        run_step(torch.cuda.current_stream().cuda_stream)
+        gs = torch.cuda.current_stream().cuda_stream
+        for l in layers:
+            launch(l, gs)
     torch.cuda.synchronize()
     for _ in range(args.warmup):
         graph.replay()
@@ -176,24 +428,52 @@ def main():
     ms = start.elapsed_time(end) / args.steps
     value = step_bytes / (ms * 1e-3) / 1e9
 
-    achieved = step_bytes / (kern_ms * 1e-3) / 1e9
+    n = len(layers)
+    bytes_per_launch = step_bytes / n
+    avg_us = ms * 1e3 / n
+    achieved = bytes_per_launch / (avg_us * 1e-6) / 1e9
+    roofline = {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4),
+                "traffic": round(traffic["bytes_per_launch"]) if traffic else None,
+                "kernel": f"{DECODE_KERNEL} (B={B})", "avg_launch_us": round(avg_us, 3),
+                "avg_launch_us_source": "HIP events around the timed graph replays / launches",
+                "algorithmic_bytes_per_launch": round(bytes_per_launch),
+                "launches": n, "per_shape_events_backed_up": all_backed}
+    if traffic:
+        roofline["traffic_detail"] = {
+            "fetch_factor": traffic["fetch"]["factor"], "write_factor": traffic["write"]["factor"],
+            "fetch_bytes_per_launch": round(traffic["fetch"]["bytes_per_launch"]),
+            "write_bytes_per_launch": round(traffic["write"]["bytes_per_launch"]),
+            "calibration": f"{CALIB_BYTES} B device copy (copyBuffer) per counter"}
+    else:
+        roofline["traffic_note"] = traffic_note or "skipped (--no-traffic)"
+
+    del graph
+    for l in layers:
+        l.clear()
+    del layers, xs, ys
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+
     rec = {
         "metric": METRIC, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 5),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "fp16", "data": "synthetic",
         "config": {"workload": "llama2_7b_decoder_linears_decode", "batch": B,
-                   "layers": args.layers, "linears_per_step": len(layers),
+                   "layers": args.layers, "linears_per_step": n,
                    "codebook": "e8_d4", "radius": 1.75, "percmask": 0.001,
                    "algorithmic_bytes_per_step": step_bytes, "hip_graph": True},
         "hbm_frac": round(value / HBM_PEAK_GBS, 4),
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "k_matvec<E8D4,BT=1>",
-                     "avg_launch_us": round(kern_ms * 1e3 / len(layers), 3),
-                     "algorithmic_bytes_per_launch": round(step_bytes / len(layers))},
+        "roofline": roofline,
         "per_shape": per_shape,
     }
+    if not args.no_e2e:
+        rec["e2e"] = e2e_decode(torch, dev)
+        print(f"# e2e: {rec['e2e']}", file=sys.stderr, flush=True)
+    if not args.no_prefill:
+        rec["prefill"] = prefill_gemm(torch, dev)
+        print(f"# prefill: {rec['prefill']}", file=sys.stderr, flush=True)
     if not args.no_cpu_baseline:
         rec["cpu_baseline"] = cpu_baseline()
     print(json.dumps(rec), flush=True)
