@@ -139,6 +139,22 @@ __device__ __forceinline__ int wave_reduce_halving(float (&v)[V]) {
   return base;
 }
 
+// The value index that wave_reduce_halving<V> leaves in `lane` (a function
+// of the lane bits only, so epilogue operands can be fetched before the sums).
+template <int V>
+__device__ __forceinline__ int reduce_base(int lane) {
+  int base = 0, cnt = V;
+#pragma unroll
+  for (int s = 0; s < 6; ++s) {
+    if (cnt > 1) {
+      const int half = cnt >> 1;
+      if (lane & kReduceBits[s]) base += half;
+      cnt = half;
+    }
+  }
+  return base;
+}
+
 template <int V> struct WaveReduceOut {
   static constexpr int per_lane = V >= 64 ? V / 64 : 1;
   static constexpr int used_bits() {

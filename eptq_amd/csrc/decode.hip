@@ -42,6 +42,8 @@ namespace eptq {
 namespace {
 
 constexpr int kT = 256;          // threads per workgroup
+constexpr int kBufferWord3 = 0x00020000;   // buffer resource word 3 (gfx9 family)
+constexpr int kNonTemporal = 2;            // buffer load cache policy: nt
 constexpr int kW = kT / 64;      // waves per workgroup
 
 typedef f16 h2 __attribute__((ext_vector_type(2)));
@@ -54,6 +56,22 @@ __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
   return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, a), __builtin_bit_cast(h2, b), c, false);
 }
 
+// By value: __builtin_bit_cast applied directly to a vector-element lvalue
+// (v[1], v.y) reads element 0 with this compiler.
+__device__ __forceinline__ h2 as_h2(uint32_t v) { return __builtin_bit_cast(h2, v); }
+
+// acc + (float)lo/hi half of a packed fp16 pair, one mixed-precision FMA.
+__device__ __forceinline__ float add_lo(uint32_t p, float acc) {
+  float r;
+  asm("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(p), "v"(acc));
+  return r;
+}
+__device__ __forceinline__ float add_hi(uint32_t p, float acc) {
+  float r;
+  asm("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(p), "v"(acc));
+  return r;
+}
+
 __device__ __forceinline__ uint32_t pk_mul(uint32_t a, uint32_t b) {
   return __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, a) * __builtin_bit_cast(h2, b));
 }
@@ -64,12 +82,14 @@ template <int BT, int J, int P, int S, bool HAS_S, typename XT>
 __global__ __launch_bounds__(kT) void k_decode_e8d4(LinearArgs a) {
   constexpr int V = BT * 8;
   constexpr int R = kW / S;                    // rows per row group
+  static_assert(V <= 64 && R * V <= kT, "one output per thread after the reduction");
   __shared__ f16x4 tab[512];
   __shared__ float red[S > 1 ? 2 : 1][kW][S > 1 ? V : 1];
   __shared__ float wmax[kW];
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int slot = wave / S, seg = wave % S;
   const int N = a.N, M = a.M, B = a.B;
   const int nch = N >> 3;
@@ -79,23 +99,32 @@ __global__ __launch_bounds__(kT) void k_decode_e8d4(LinearArgs a) {
 
   auto chunk = [&](int j) { return seg * 64 + lane + 64 * S * j; };
 
+  // ---- critical-block rows: [rb, re) of O_col/O for this wave's row ----
+  // Scalar loads, kept one row group ahead of their use so that the entry
+  // loads they address never wait for them.
+  auto row_range = [&](int rg, int& rb, int& re) {
+    const int row = rg * R + slot;             // wave-uniform
+    const int rr = row < M ? row : M;
+    rb = a.O_row_ptr[rr];
+    re = a.O_row_ptr[row < M ? rr + 1 : rr];
+  };
+  int crb, cre, nrb, nre;
+  row_range(blockIdx.x, crb, cre);
+  row_range(blockIdx.x + G, nrb, nre);
+
   // ---- setup loads (table, h, x), then the index chunks of P row groups ----
   u32x4 qv[P][J];
-  // Every load is issued unconditionally from a clamped (always valid)
-  // address and masked afterwards: with no divergent branches around loads
-  // the compiler can wait for exactly the load it needs (vmcnt counts loads
-  // in issue order) instead of draining all of them.
+  // Index chunks are read through a buffer resource spanning one row (an
+  // empty one past the last row): out-of-range chunks read as zero, so the
+  // loads need no branches or clamps, and the compiler can wait for exactly
+  // the load it needs (vmcnt counts loads in issue order).
   auto load_q = [&](u32x4 (&dst)[J], int rg) {
-    const int row = rg * R + slot;
-    const bool rv = row < M;
-    const u32x4* __restrict__ qrow = (const u32x4*)(a.Q + (size_t)(rv ? row : M - 1) * N);
+    const int row = rg * R + slot;            // wave-uniform
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(a.Q + (size_t)(row < M ? row : 0) * N), (short)0, row < M ? N * 2 : 0, kBufferWord3);
 #pragma unroll
-    for (int j = 0; j < J; ++j) {
-      const int c = chunk(j);
-      const bool ok = rv && c < nch;
-      const u32x4 v = __builtin_nontemporal_load(qrow + (c < nch ? c : nch - 1));
-      dst[j] = ok ? v : (u32x4){0u, 0u, 0u, 0u};
-    }
+    for (int j = 0; j < J; ++j)
+      dst[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, chunk(j) * 16, 0, kNonTemporal));
   };
   // Loads complete in issue order (vmcnt counts them in order), so the small
   // L2-resident setup loads are issued before the HBM index stream: waiting
@@ -104,41 +133,72 @@ __global__ __launch_bounds__(kT) void k_decode_e8d4(LinearArgs a) {
 #pragma unroll
   for (int p = 0; p < 2; ++p) tload[p] = ((const f16x4*)a.codes)[tid + kT * p];   // fp16 table
 
+  // h and the x rows through buffer resources: chunks past N (and batch
+  // rows past B) read as zero, with no branches around the loads.
+  const __amdgpu_buffer_rsrc_t rh = __builtin_amdgcn_make_buffer_rsrc((void*)a.h, (short)0, N * 2, kBufferWord3);
+  const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void*)a.x, (short)0, B * N * 2, kBufferWord3);
   f16x8 hv[J];
   u16x8 xload[J][BT];
 #pragma unroll
   for (int j = 0; j < J; ++j) {
     const int c = chunk(j);
-    const int cc = (c < nch ? c : nch - 1) << 3;
-    const f16x8 hl = *(const f16x8*)(a.h + cc);
-    hv[j] = c < nch ? hl : (f16x8){0, 0, 0, 0, 0, 0, 0, 0};
+    const bool cv = c < nch;
+    hv[j] = __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(rh, cv ? c * 16 : N * 2, 0, 0));
 #pragma unroll
     for (int b = 0; b < BT; ++b) {
-      const u16x8 xl = *(const u16x8*)(a.x + (size_t)(b < B ? b : B - 1) * N + cc);
-      xload[j][b] = (c < nch && b < B) ? xl : (u16x8){0, 0, 0, 0, 0, 0, 0, 0};
+      const int off = cv && b < B ? b * N * 2 + c * 16 : B * N * 2;   // past the end: zero
+      xload[j][b] = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(rx, off, 0, 0));
     }
   }
 #pragma unroll
   for (int p = 0; p < P; ++p) load_q(qv[p], blockIdx.x + p * G);
+  // Keep the index stream issued ahead of the activation arithmetic below
+  // (which waits for h and x).
+  __builtin_amdgcn_sched_barrier(0);
 
-  // Activation side, identical for every row this lane visits.
-  //   B = 1:  xh1[j][e] = x·h exactly in fp32
-  //   B >= 2: xhp[j][b][d] = fp16 pair (x·h·2^-e) for columns 2d, 2d+1
-  float xh1[BT == 1 ? J : 1][8];
-  uint32_t xhp[BT == 1 ? 1 : J][BT][4];
+  // Critical blocks, first 64·S entries of a row: lane `ent` of the row's
+  // S waves holds entry rb + ent (its column and O vector).  Buffer resources
+  // span exactly the row's entries, so lanes past the end read zeros.
+  const int ent = seg * 64 + lane;
+  int ecol;
+  u32x4 eo;
+  auto load_entries = [&](int rb, int re) {
+    const int cnt = re - rb;
+    const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(a.O_col + rb), (short)0, cnt * 4, kBufferWord3);
+    const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(a.O + (size_t)rb * 8), (short)0, cnt * 16, kBufferWord3);
+    ecol = (int)__builtin_amdgcn_raw_buffer_load_b32(rc, ent * 4, 0, 0);
+    eo = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(ro, ent * 16, 0, 0));
+  };
+  load_entries(crb, cre);
+  __builtin_amdgcn_sched_barrier(0);
+
+  // Activation side, identical for every row this lane visits: fp16 pairs
+  // xhp[j][b][d] = x·h·2^-e for columns 2d, 2d+1 of chunk j, with 2^-e a
+  // workgroup-uniform power of two.
+  //   B = 1:  max|x·h|·2^-e <= 1, so the fp16 accumulation of table values
+  //           (|c| < 2) over a chunk stays far from overflow;
+  //   B >= 2: max|h|·2^-e <= 1, so |x·h·2^-e| <= |x| (fp32 dot2 accumulation).
+  uint32_t xhp[J][BT][4];
   float out_scale = 1.0f;
-  if constexpr (BT == 1) {
-#pragma unroll
-    for (int j = 0; j < J; ++j)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) xh1[j][e] = Act<XT>::mul_f16(xload[j][0][e], hv[j][e]);
-  } else {
-    // Workgroup-uniform power-of-two scale: max|h| * 2^-e <= 1.
+  {
     float mx = 0.0f;
+    float xf[BT == 1 ? J : 1][8];
+    if constexpr (BT == 1) {
 #pragma unroll
-    for (int j = 0; j < J; ++j)
+      for (int j = 0; j < J; ++j)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) mx = fmaxf(mx, fabsf((float)hv[j][e]));
+        for (int e = 0; e < 8; ++e) {
+          xf[j][e] = Act<XT>::mul_f16(xload[j][0][e], hv[j][e]);
+          mx = fmaxf(mx, fabsf(xf[j][e]));
+        }
+    } else {
+#pragma unroll
+      for (int j = 0; j < J; ++j)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) mx = fmaxf(mx, fabsf((float)hv[j][e]));
+    }
     mx = fmaxf(mx, partner<1>(mx));
     mx = fmaxf(mx, partner<2>(mx));
     mx = fmaxf(mx, partner<4>(mx));
@@ -151,16 +211,25 @@ __global__ __launch_bounds__(kT) void k_decode_e8d4(LinearArgs a) {
     int ex = 0;
     if (mx > 1.0f) ex = (int)((__builtin_bit_cast(uint32_t, mx) >> 23) & 0xff) - 126;  // 2^ex >= mx
     out_scale = __builtin_ldexpf(1.0f, ex);
-    const f16 down = (f16)__builtin_ldexpf(1.0f, -ex);
-    const uint32_t down2 = __builtin_bit_cast(uint32_t, (h2){down, down});
+    if constexpr (BT == 1) {
+      const float inv = __builtin_ldexpf(1.0f, -ex);
 #pragma unroll
-    for (int j = 0; j < J; ++j) {
-      const u32x4 hw = __builtin_bit_cast(u32x4, hv[j]);
+      for (int j = 0; j < J; ++j)
 #pragma unroll
-      for (int b = 0; b < BT; ++b) {
-        const u32x4 xw = __builtin_bit_cast(u32x4, xload[j][b]);
+        for (int d = 0; d < 4; ++d)
+          xhp[j][0][d] = __builtin_bit_cast(uint32_t, (h2){(f16)(xf[j][2 * d] * inv), (f16)(xf[j][2 * d + 1] * inv)});
+    } else {
+      const f16 down = (f16)__builtin_ldexpf(1.0f, -ex);
+      const uint32_t down2 = __builtin_bit_cast(uint32_t, (h2){down, down});
 #pragma unroll
-        for (int d = 0; d < 4; ++d) xhp[j][b][d] = pk_mul(xw[d], pk_mul(hw[d], down2));
+      for (int j = 0; j < J; ++j) {
+        const u32x4 hw = __builtin_bit_cast(u32x4, hv[j]);
+#pragma unroll
+        for (int b = 0; b < BT; ++b) {
+          const u32x4 xw = __builtin_bit_cast(u32x4, xload[j][b]);
+#pragma unroll
+          for (int d = 0; d < 4; ++d) xhp[j][b][d] = pk_mul(xw[d], pk_mul(hw[d], down2));
+        }
       }
     }
   }
@@ -171,6 +240,12 @@ __global__ __launch_bounds__(kT) void k_decode_e8d4(LinearArgs a) {
 
   // Marker vector as the main loop sees it.
   const f16x4 t5 = tab[511 ^ 0x100];
+  // bias (or nothing: an empty resource reads zeros).
+  const __amdgpu_buffer_rsrc_t rbias = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)a.bias, (short)0, a.bias ? 16 * M : 0, kBufferWord3);
+  // The output (batch row, block row) this thread writes after the reduction.
+  const int wbase = S == 1 ? reduce_base<V>(lane) : (tid < R * V ? tid % V : 0);
+  const int wb = wbase >> 3, wk = wbase & 7;
 
   int par = 0;
   for (int rg0 = blockIdx.x; rg0 < RG; rg0 += P * G) {
@@ -182,15 +257,39 @@ __global__ __launch_bounds__(kT) void k_decode_e8d4(LinearArgs a) {
     const bool row_ok = m < M;
     const int grp = HAS_S ? (8 * (row_ok ? m : 0)) / a.qb : 0;
 
+    // Epilogue operands for this thread's output row, fetched early.
+    const int orow = S == 1 ? m : rg * R + (tid < R * V ? tid / V : 0);
+    const int oidx = 8 * (orow < M ? orow : M - 1) + wk;
+    const f16 og = a.g[oidx];
+    const f16 ob = __builtin_bit_cast(f16, (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(rbias, oidx * 2, 0, 0));
+    // Row pointers two row groups ahead (their entries are loaded next).
+    int frb, fre;
+    row_range(rg + 2 * G, frb, fre);
+
+    // Activation gathers for this row's critical blocks (x, h, S at their
+    // columns), issued part-way through the chunk loop once the entry
+    // columns have arrived.
+    uint16_t gx[BT];
+    f16 gh, gs = (f16)1.0f;
+    auto load_gather = [&]() {
+      const int col = (unsigned)ecol < (unsigned)N ? ecol : 0;
+      gh = a.h[col];
+#pragma unroll
+      for (int b = 0; b < BT; ++b) gx[b] = a.x[(size_t)(b < B ? b : B - 1) * N + col];
+      if (HAS_S) gs = a.S[(size_t)grp * N + col];
+    };
+
     float acc[V];
 #pragma unroll
     for (int i = 0; i < V; ++i) acc[i] = 0.0f;
 
+    bool gathered = false;
 #pragma unroll
     for (int j = 0; j < J; ++j) {
-      if (chunk(j) >= nch) break;
+      if (seg * 64 + 64 * S * j >= nch) break;   // uniform: no lane has a chunk left
+      if (j == J / 2) { load_gather(); gathered = true; }
       f16x8 sv;
-      if (HAS_S) sv = *(const f16x8*)(a.S + (size_t)grp * N + (chunk(j) << 3));
+      if (HAS_S) sv = *(const f16x8*)(a.S + (size_t)grp * N + ((chunk(j) < nch ? chunk(j) : 0) << 3));
       // All 16 table lookups of the chunk first, then the arithmetic, so the
       // LDS latency is paid once per chunk rather than once per word.
       u32x2 t1l[4], t2l[4], t1h[4], t2h[4];
@@ -206,22 +305,20 @@ __global__ __launch_bounds__(kT) void k_decode_e8d4(LinearArgs a) {
         t1h[d] = *(const u32x2*)(tabB + a1hi);
         t2h[d] = *(const u32x2*)(tabB + a2hi);
       }
+      h2 acc16[4];   // B = 1: rows (0,1) (2,3) (4,5) (6,7) of this chunk, fp16
 #pragma unroll
       for (int d = 0; d < 4; ++d) {
         if constexpr (BT == 1) {
-          float xl = xh1[j][2 * d], xh = xh1[j][2 * d + 1];
-          if (HAS_S) { xl *= (float)sv[2 * d]; xh *= (float)sv[2 * d + 1]; }
-          const f16x4 c1l = __builtin_bit_cast(f16x4, t1l[d]), c2l = __builtin_bit_cast(f16x4, t2l[d]);
-          const f16x4 c1h = __builtin_bit_cast(f16x4, t1h[d]), c2h = __builtin_bit_cast(f16x4, t2h[d]);
+          // Packed fp16 FMAs, two rows per op, both columns of the word.
+          const uint32_t xp = HAS_S ? pk_mul(xhp[j][0][d], __builtin_bit_cast(u32x4, sv)[d]) : xhp[j][0][d];
+          const h2 xx = __builtin_bit_cast(h2, xp);
+          const h2 xl = {xx.x, xx.x}, xh = {xx.y, xx.y};
+          const h2 c[8] = {as_h2(t1l[d][0]), as_h2(t1l[d][1]), as_h2(t2l[d][0]), as_h2(t2l[d][1]),
+                           as_h2(t1h[d][0]), as_h2(t1h[d][1]), as_h2(t2h[d][0]), as_h2(t2h[d][1])};
 #pragma unroll
-          for (int k = 0; k < 4; ++k) {
-            acc[k] = fmaf((float)c1l[k], xl, acc[k]);
-            acc[k + 4] = fmaf((float)c2l[k], xl, acc[k + 4]);
-          }
-#pragma unroll
-          for (int k = 0; k < 4; ++k) {
-            acc[k] = fmaf((float)c1h[k], xh, acc[k]);
-            acc[k + 4] = fmaf((float)c2h[k], xh, acc[k + 4]);
+          for (int q = 0; q < 4; ++q) {
+            acc16[q] = d == 0 ? c[q] * xl : __builtin_elementwise_fma(c[q], xl, acc16[q]);
+            acc16[q] = __builtin_elementwise_fma(c[q + 4], xh, acc16[q]);
           }
         } else {
           // (c_k(lo), c_k(hi)) fp16 pairs for k = 0..7
@@ -244,57 +341,67 @@ __global__ __launch_bounds__(kT) void k_decode_e8d4(LinearArgs a) {
           }
         }
       }
-    }
-
-    // This ring slot is consumed: fetch the row group P·G ahead into it.
-    load_q(qv[p], rg + P * G);
-
-    // Critical blocks: add O·(h S x) in the accumulator's units, minus what
-    // the marker index contributed above.
-    if (row_ok) {
-      const int r0 = a.O_row_ptr[m], r1 = a.O_row_ptr[m + 1];
-      for (int i = r0 + seg * 64 + lane; i < r1; i += 64 * S) {
-        const int col = a.O_col[i];
-        const f16x8 o = *(const f16x8*)(a.O + (size_t)i * 8);
-        const f16 hc = a.h[col];
-        const float sc = HAS_S ? (float)a.S[(size_t)grp * N + col] : 1.0f;
+      if constexpr (BT == 1) {
+        // Chunk partial sums (8 columns) into the fp32 accumulators.
 #pragma unroll
-        for (int b = 0; b < BT; ++b) {
-          if (b < B) {
-            const uint16_t xb = a.x[(size_t)b * N + col];
-            float xo, xm;   // x·h for O (no S); what the main loop used
-            if constexpr (BT == 1) {
-              xo = Act<XT>::mul_f16(xb, hc);
-              xm = HAS_S ? xo * sc : xo;
-            } else {
-              const f16 hd = (f16)((float)hc / out_scale);
-              const f16 xhd = (f16)((float)__builtin_bit_cast(f16, xb) * (float)hd);
-              xo = Act<XT>::mul_f16(xb, hc) / out_scale;
-              xm = HAS_S ? (float)(f16)((float)xhd * sc) : (float)xhd;
-            }
-#pragma unroll
-            for (int k = 0; k < 8; ++k)
-              acc[b * 8 + k] += (float)o[k] * xo - (float)t5[k & 3] * xm;
-          }
+        for (int q = 0; q < 4; ++q) {
+          const uint32_t pq = __builtin_bit_cast(uint32_t, acc16[q]);
+          acc[2 * q] = add_lo(pq, acc[2 * q]);
+          acc[2 * q + 1] = add_hi(pq, acc[2 * q + 1]);
         }
       }
     }
+    if (!gathered) load_gather();
+
+    // Critical blocks: add O·(h S x) in the accumulator's units, minus what
+    // the marker index contributed in the main loop (table row 511).
+    auto correct = [&](const f16x8 o, int col, uint16_t (&xs)[BT], f16 hc, float sc) {
+#pragma unroll
+      for (int b = 0; b < BT; ++b) {
+        if (b < B) {
+          float xo, xm;   // x·h for O (no S); what the main loop used
+          if constexpr (BT == 1) {
+            xo = Act<XT>::mul_f16(xs[b], hc) / out_scale;
+            const f16 x16 = (f16)xo;
+            xm = HAS_S ? (float)(f16)((float)x16 * sc) : (float)x16;
+          } else {
+            const f16 hd = (f16)((float)hc / out_scale);
+            const f16 xhd = (f16)((float)__builtin_bit_cast(f16, xs[b]) * (float)hd);
+            xo = Act<XT>::mul_f16(xs[b], hc) / out_scale;
+            xm = HAS_S ? (float)(f16)((float)xhd * sc) : (float)xhd;
+          }
+#pragma unroll
+          for (int k = 0; k < 8; ++k)
+            acc[b * 8 + k] += (float)o[k] * xo - (float)t5[k & 3] * xm;
+        }
+      }
+    };
+    if (row_ok && ent < cre - crb)
+      correct(__builtin_bit_cast(f16x8, eo), ecol, gx, gh, (float)gs);
+    // Rows with more than 64·S critical blocks: the rest, synchronously.
+    if (row_ok) {
+      for (int i = crb + 64 * S + ent; i < cre; i += 64 * S) {
+        const int col = a.O_col[i];
+        uint16_t xs[BT];
+#pragma unroll
+        for (int b = 0; b < BT; ++b) xs[b] = a.x[(size_t)(b < B ? b : B - 1) * N + col];
+        const float sc = HAS_S ? (float)a.S[(size_t)grp * N + col] : 1.0f;
+        correct(*(const f16x8*)(a.O + (size_t)i * 8), col, xs, a.h[col], sc);
+      }
+    }
+
+    // Next row group's entries, then this ring slot's refill.
+    load_entries(nrb, nre);
+    load_q(qv[p], rg + P * G);
+    crb = nrb; cre = nre;
+    nrb = frb; nre = fre;
 
     const int base = wave_reduce_halving<V>(acc);
     if constexpr (S == 1) {
       // The wave owns the row: write straight from the reducing lanes.
-      if (row_ok && WaveReduceOut<V>::writer(lane)) {
-#pragma unroll
-        for (int i = 0; i < WaveReduceOut<V>::per_lane; ++i) {
-          const int t = base + i;
-          const int b = t >> 3, k = t & 7;
-          if (b < B) {
-            const int row = 8 * m + k;
-            float sum = acc[i] * out_scale * (float)a.g[row];
-            if (a.bias) sum += (float)a.bias[row];
-            a.y[(size_t)b * (8 * M) + row] = Act<XT>::from_f32(sum);
-          }
-        }
+      if (row_ok && WaveReduceOut<V>::writer(lane) && wb < B) {
+        const float sum = acc[0] * out_scale * (float)og + (float)ob;
+        a.y[(size_t)wb * (8 * M) + 8 * m + wk] = Act<XT>::from_f32(sum);
       }
     } else {
       if (WaveReduceOut<V>::writer(lane)) {
@@ -304,18 +411,14 @@ __global__ __launch_bounds__(kT) void k_decode_e8d4(LinearArgs a) {
       // One barrier per row group: red[] alternates, and the next barrier
       // orders these reads of red[par] before its reuse two groups later.
       __syncthreads();
-      for (int t = tid; t < R * V; t += kT) {
-        const int sl = t / V, idx = t - sl * V;
-        const int mr = rg * R + sl;
-        const int b = idx >> 3, k = idx & 7;
-        if (mr < M && b < B) {
+      if (tid < R * V) {
+        const int sl = tid / V;
+        if (orow < M && wb < B) {
           float sum = 0.0f;
 #pragma unroll
-          for (int w = 0; w < S; ++w) sum += red[par][sl * S + w][idx];
-          const int row = 8 * mr + k;
-          sum = sum * out_scale * (float)a.g[row];
-          if (a.bias) sum += (float)a.bias[row];
-          a.y[(size_t)b * (8 * M) + row] = Act<XT>::from_f32(sum);
+          for (int w = 0; w < S; ++w) sum += red[par][sl * S + w][wbase];
+          sum = sum * out_scale * (float)og + (float)ob;
+          a.y[(size_t)wb * (8 * M) + 8 * orow + wk] = Act<XT>::from_f32(sum);
         }
       }
       par ^= 1;
