@@ -60,15 +60,15 @@ __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
 // (v[1], v.y) reads element 0 with this compiler.
 __device__ __forceinline__ h2 as_h2(uint32_t v) { return __builtin_bit_cast(h2, v); }
 
-// acc + (float)lo/hi half of a packed fp16 pair, one mixed-precision FMA.
-__device__ __forceinline__ float add_lo(uint32_t p, float acc) {
+// acc + (float)(lo or hi half of a packed fp16 pair) · s, one mixed-precision FMA.
+__device__ __forceinline__ float fma_lo(uint32_t p, float s, float acc) {
   float r;
-  asm("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(p), "v"(acc));
+  asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(p), "v"(s), "v"(acc));
   return r;
 }
-__device__ __forceinline__ float add_hi(uint32_t p, float acc) {
+__device__ __forceinline__ float fma_hi(uint32_t p, float s, float acc) {
   float r;
-  asm("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(p), "v"(acc));
+  asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(p), "v"(s), "v"(acc));
   return r;
 }
 
@@ -86,6 +86,9 @@ __global__ __launch_bounds__(kT) void k_decode_e8d4(LinearArgs a) {
   __shared__ f16x4 tab[512];
   __shared__ float red[S > 1 ? 2 : 1][kW][S > 1 ? V : 1];
   __shared__ float wmax[kW];
+  // Activation side, shared by the workgroup: xs[b][n] = fp16 x·h (scaled),
+  // rows padded by one zero chunk; for B = 1 also csc[c] = the scale of chunk c.
+  extern __shared__ __align__(16) char dyn[];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -93,9 +96,12 @@ __global__ __launch_bounds__(kT) void k_decode_e8d4(LinearArgs a) {
   const int slot = wave / S, seg = wave % S;
   const int N = a.N, M = a.M, B = a.B;
   const int nch = N >> 3;
+  const int NP = N + 8;
   const int RG = (M + R - 1) / R;              // row groups
   const int G = gridDim.x;
   const char* __restrict__ tabB = (const char*)tab;
+  uint16_t* __restrict__ xs = (uint16_t*)dyn;
+  float* __restrict__ csc = (float*)(dyn + BT * NP * 2);
 
   auto chunk = [&](int j) { return seg * 64 + lane + 64 * S * j; };
 
@@ -112,7 +118,117 @@ __global__ __launch_bounds__(kT) void k_decode_e8d4(LinearArgs a) {
   row_range(blockIdx.x, crb, cre);
   row_range(blockIdx.x + G, nrb, nre);
 
-  // ---- setup loads (table, h, x), then the index chunks of P row groups ----
+  // ---- loads: table and activations first; the activation table is built
+  // before the index stream is requested, so its loads are not queued behind
+  // the HBM index traffic (vmcnt also counts loads in issue order). ----
+  f16x4 tload[2];
+#pragma unroll
+  for (int p = 0; p < 2; ++p) tload[p] = ((const f16x4*)a.codes)[tid + kT * p];   // fp16 table
+
+  // h and x rows through buffer resources (offsets past the end read zero).
+  // Each thread prepares chunks c = tid + kT·k of the activation table; the
+  // first CAP of them are loaded together up front, any others one by one.
+  constexpr int CA = (J * S) / 4 < 1 ? 1 : (J * S) / 4;   // >= ceil(nch / kT)
+  constexpr int CAP = CA < 18 / (BT + 1) ? CA : 18 / (BT + 1);
+  const __amdgpu_buffer_rsrc_t rh = __builtin_amdgcn_make_buffer_rsrc((void*)a.h, (short)0, N * 2, kBufferWord3);
+  const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void*)a.x, (short)0, B * N * 2, kBufferWord3);
+  auto load_hx = [&](int c, u32x4& hw, u32x4 (&xw)[BT]) {
+    const bool cv = c < nch;
+    hw = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rh, cv ? c * 16 : N * 2, 0, 0));
+#pragma unroll
+    for (int b = 0; b < BT; ++b)
+      xw[b] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+          rx, cv && b < B ? b * N * 2 + c * 16 : B * N * 2, 0, 0));
+  };
+  u32x4 hpre[CAP], xpre[CAP][BT];
+#pragma unroll
+  for (int k = 0; k < CAP; ++k) load_hx(tid + kT * k, hpre[k], xpre[k]);
+
+  // ---- activation side into LDS ----
+  float out_scale = 1.0f;
+  if (tid == 0) {   // the zero chunk past the end of every row
+#pragma unroll
+    for (int b = 0; b < BT; ++b) *(u32x4*)(xs + b * NP + nch * 8) = (u32x4){0u, 0u, 0u, 0u};
+    if (BT == 1) csc[nch] = 1.0f;
+  }
+  if constexpr (BT == 1) {
+    // Per chunk of 8 columns: xs = fp16(x·h·2^-e), csc = 2^e with
+    // max|x·h|·2^-e in [0.5, 1), so the fp16 accumulation of a chunk (|c| < 2,
+    // 8 columns) cannot overflow; the main loop applies 2^e in fp32.
+    auto prep = [&](int c, const u32x4 hw, const u32x4 xw) {
+      const f16x8 hv = __builtin_bit_cast(f16x8, hw);
+      const u16x8 xv = __builtin_bit_cast(u16x8, xw);
+      float xf[8], mx = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        xf[e] = Act<XT>::mul_f16(xv[e], hv[e]);
+        mx = fmaxf(mx, fabsf(xf[e]));
+      }
+      const int ex = mx > 0.0f ? (int)((__builtin_bit_cast(uint32_t, mx) >> 23) & 0xff) - 126 : 0;
+      const float down = __builtin_ldexpf(1.0f, -ex);
+      u32x4 w;
+#pragma unroll
+      for (int d = 0; d < 4; ++d)
+        w[d] = __builtin_bit_cast(uint32_t, (h2){(f16)(xf[2 * d] * down), (f16)(xf[2 * d + 1] * down)});
+      if (c < nch) {
+        *(u32x4*)(xs + c * 8) = w;
+        csc[c] = __builtin_ldexpf(1.0f, ex);
+      }
+    };
+#pragma unroll
+    for (int k = 0; k < CAP; ++k) prep(tid + kT * k, hpre[k], xpre[k][0]);
+    for (int c = tid + kT * CAP; c < nch; c += kT) {
+      u32x4 hw, xw[BT];
+      load_hx(c, hw, xw);
+      prep(c, hw, xw[0]);
+    }
+  } else {
+    // Workgroup-uniform power-of-two scale with max|h|·2^-e <= 1, so the fp16
+    // pairs |x·h·2^-e| <= |x| cannot overflow (dot2 accumulates in fp32).
+    float mx = 0.0f;
+    auto hmax = [&](const u32x4 hw) {
+      const f16x8 hv = __builtin_bit_cast(f16x8, hw);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) mx = fmaxf(mx, fabsf((float)hv[e]));
+    };
+#pragma unroll
+    for (int k = 0; k < CAP; ++k) hmax(hpre[k]);
+    for (int c = tid + kT * CAP; c < nch; c += kT)
+      hmax(__builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rh, c * 16, 0, 0)));
+    mx = fmaxf(mx, partner<1>(mx));
+    mx = fmaxf(mx, partner<2>(mx));
+    mx = fmaxf(mx, partner<4>(mx));
+    mx = fmaxf(mx, partner<8>(mx));
+    mx = fmaxf(mx, partner<16>(mx));
+    mx = fmaxf(mx, partner<32>(mx));
+    if (lane == 0) wmax[wave] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+    int ex = 0;
+    if (mx > 1.0f) ex = (int)((__builtin_bit_cast(uint32_t, mx) >> 23) & 0xff) - 126;  // 2^ex >= mx
+    out_scale = __builtin_ldexpf(1.0f, ex);
+    const f16 down = (f16)__builtin_ldexpf(1.0f, -ex);
+    const uint32_t down2 = __builtin_bit_cast(uint32_t, (h2){down, down});
+    auto prep = [&](int c, const u32x4 hw, const u32x4 (&xw)[BT]) {
+      if (c < nch) {
+#pragma unroll
+        for (int b = 0; b < BT; ++b) {
+          u32x4 w;
+#pragma unroll
+          for (int d = 0; d < 4; ++d) w[d] = pk_mul(xw[b][d], pk_mul(hw[d], down2));
+          *(u32x4*)(xs + b * NP + c * 8) = w;
+        }
+      }
+    };
+#pragma unroll
+    for (int k = 0; k < CAP; ++k) prep(tid + kT * k, hpre[k], xpre[k]);
+    for (int c = tid + kT * CAP; c < nch; c += kT) {
+      u32x4 hw, xw[BT];
+      load_hx(c, hw, xw);
+      prep(c, hw, xw);
+    }
+  }
+
   u32x4 qv[P][J];
   // Index chunks are read through a buffer resource spanning one row (an
   // empty one past the last row): out-of-range chunks read as zero, so the
@@ -126,35 +242,8 @@ __global__ __launch_bounds__(kT) void k_decode_e8d4(LinearArgs a) {
     for (int j = 0; j < J; ++j)
       dst[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, chunk(j) * 16, 0, kNonTemporal));
   };
-  // Loads complete in issue order (vmcnt counts them in order), so the small
-  // L2-resident setup loads are issued before the HBM index stream: waiting
-  // for the table and activations then does not wait for the indices.
-  f16x4 tload[2];
-#pragma unroll
-  for (int p = 0; p < 2; ++p) tload[p] = ((const f16x4*)a.codes)[tid + kT * p];   // fp16 table
-
-  // h and the x rows through buffer resources: chunks past N (and batch
-  // rows past B) read as zero, with no branches around the loads.
-  const __amdgpu_buffer_rsrc_t rh = __builtin_amdgcn_make_buffer_rsrc((void*)a.h, (short)0, N * 2, kBufferWord3);
-  const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void*)a.x, (short)0, B * N * 2, kBufferWord3);
-  f16x8 hv[J];
-  u16x8 xload[J][BT];
-#pragma unroll
-  for (int j = 0; j < J; ++j) {
-    const int c = chunk(j);
-    const bool cv = c < nch;
-    hv[j] = __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(rh, cv ? c * 16 : N * 2, 0, 0));
-#pragma unroll
-    for (int b = 0; b < BT; ++b) {
-      const int off = cv && b < B ? b * N * 2 + c * 16 : B * N * 2;   // past the end: zero
-      xload[j][b] = __builtin_bit_cast(u16x8, __builtin_amdgcn_raw_buffer_load_b128(rx, off, 0, 0));
-    }
-  }
 #pragma unroll
   for (int p = 0; p < P; ++p) load_q(qv[p], blockIdx.x + p * G);
-  // Keep the index stream issued ahead of the activation arithmetic below
-  // (which waits for h and x).
-  __builtin_amdgcn_sched_barrier(0);
 
   // Critical blocks, first 64·S entries of a row: lane `ent` of the row's
   // S waves holds entry rb + ent (its column and O vector).  Buffer resources
@@ -173,66 +262,6 @@ __global__ __launch_bounds__(kT) void k_decode_e8d4(LinearArgs a) {
   };
   load_entries(crb, cre);
   __builtin_amdgcn_sched_barrier(0);
-
-  // Activation side, identical for every row this lane visits: fp16 pairs
-  // xhp[j][b][d] = x·h·2^-e for columns 2d, 2d+1 of chunk j, with 2^-e a
-  // workgroup-uniform power of two.
-  //   B = 1:  max|x·h|·2^-e <= 1, so the fp16 accumulation of table values
-  //           (|c| < 2) over a chunk stays far from overflow;
-  //   B >= 2: max|h|·2^-e <= 1, so |x·h·2^-e| <= |x| (fp32 dot2 accumulation).
-  uint32_t xhp[J][BT][4];
-  float out_scale = 1.0f;
-  {
-    float mx = 0.0f;
-    float xf[BT == 1 ? J : 1][8];
-    if constexpr (BT == 1) {
-#pragma unroll
-      for (int j = 0; j < J; ++j)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          xf[j][e] = Act<XT>::mul_f16(xload[j][0][e], hv[j][e]);
-          mx = fmaxf(mx, fabsf(xf[j][e]));
-        }
-    } else {
-#pragma unroll
-      for (int j = 0; j < J; ++j)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) mx = fmaxf(mx, fabsf((float)hv[j][e]));
-    }
-    mx = fmaxf(mx, partner<1>(mx));
-    mx = fmaxf(mx, partner<2>(mx));
-    mx = fmaxf(mx, partner<4>(mx));
-    mx = fmaxf(mx, partner<8>(mx));
-    mx = fmaxf(mx, partner<16>(mx));
-    mx = fmaxf(mx, partner<32>(mx));
-    if (lane == 0) wmax[wave] = mx;
-    __syncthreads();
-    mx = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
-    int ex = 0;
-    if (mx > 1.0f) ex = (int)((__builtin_bit_cast(uint32_t, mx) >> 23) & 0xff) - 126;  // 2^ex >= mx
-    out_scale = __builtin_ldexpf(1.0f, ex);
-    if constexpr (BT == 1) {
-      const float inv = __builtin_ldexpf(1.0f, -ex);
-#pragma unroll
-      for (int j = 0; j < J; ++j)
-#pragma unroll
-        for (int d = 0; d < 4; ++d)
-          xhp[j][0][d] = __builtin_bit_cast(uint32_t, (h2){(f16)(xf[j][2 * d] * inv), (f16)(xf[j][2 * d + 1] * inv)});
-    } else {
-      const f16 down = (f16)__builtin_ldexpf(1.0f, -ex);
-      const uint32_t down2 = __builtin_bit_cast(uint32_t, (h2){down, down});
-#pragma unroll
-      for (int j = 0; j < J; ++j) {
-        const u32x4 hw = __builtin_bit_cast(u32x4, hv[j]);
-#pragma unroll
-        for (int b = 0; b < BT; ++b) {
-          const u32x4 xw = __builtin_bit_cast(u32x4, xload[j][b]);
-#pragma unroll
-          for (int d = 0; d < 4; ++d) xhp[j][b][d] = pk_mul(xw[d], pk_mul(hw[d], down2));
-        }
-      }
-    }
-  }
 
 #pragma unroll
   for (int p = 0; p < 2; ++p) tab[(tid + kT * p) ^ 0x100] = tload[p];
@@ -265,18 +294,14 @@ __global__ __launch_bounds__(kT) void k_decode_e8d4(LinearArgs a) {
     // Row pointers two row groups ahead (their entries are loaded next).
     int frb, fre;
     row_range(rg + 2 * G, frb, fre);
-
-    // Activation gathers for this row's critical blocks (x, h, S at their
-    // columns), issued part-way through the chunk loop once the entry
-    // columns have arrived.
-    uint16_t gx[BT];
-    f16 gh, gs = (f16)1.0f;
+    // S at the critical blocks' columns (grouped layers), issued part-way
+    // through the chunk loop once the entry columns have arrived.
+    f16 gs = (f16)1.0f;
     auto load_gather = [&]() {
-      const int col = (unsigned)ecol < (unsigned)N ? ecol : 0;
-      gh = a.h[col];
-#pragma unroll
-      for (int b = 0; b < BT; ++b) gx[b] = a.x[(size_t)(b < B ? b : B - 1) * N + col];
-      if (HAS_S) gs = a.S[(size_t)grp * N + col];
+      if constexpr (HAS_S) {
+        const int col = (unsigned)ecol < (unsigned)N ? ecol : 0;
+        gs = a.S[(size_t)grp * N + col];
+      }
     };
 
     float acc[V];
@@ -288,8 +313,12 @@ __global__ __launch_bounds__(kT) void k_decode_e8d4(LinearArgs a) {
     for (int j = 0; j < J; ++j) {
       if (seg * 64 + 64 * S * j >= nch) break;   // uniform: no lane has a chunk left
       if (j == J / 2) { load_gather(); gathered = true; }
+      const int cj = chunk(j) < nch ? chunk(j) : nch;   // past the end: the zero chunk
       f16x8 sv;
-      if (HAS_S) sv = *(const f16x8*)(a.S + (size_t)grp * N + ((chunk(j) < nch ? chunk(j) : 0) << 3));
+      if (HAS_S) sv = *(const f16x8*)(a.S + (size_t)grp * N + ((cj < nch ? cj : 0) << 3));
+      u32x4 xw[BT];
+#pragma unroll
+      for (int b = 0; b < BT; ++b) xw[b] = *(const u32x4*)(xs + b * NP + cj * 8);
       // All 16 table lookups of the chunk first, then the arithmetic, so the
       // LDS latency is paid once per chunk rather than once per word.
       u32x2 t1l[4], t2l[4], t1h[4], t2h[4];
@@ -305,12 +334,13 @@ __global__ __launch_bounds__(kT) void k_decode_e8d4(LinearArgs a) {
         t1h[d] = *(const u32x2*)(tabB + a1hi);
         t2h[d] = *(const u32x2*)(tabB + a2hi);
       }
-      h2 acc16[4];   // B = 1: rows (0,1) (2,3) (4,5) (6,7) of this chunk, fp16
+      if constexpr (BT == 1) {
+        const float sc = csc[cj];
+        h2 acc16[4];   // rows (0,1) (2,3) (4,5) (6,7) of this chunk, fp16
 #pragma unroll
-      for (int d = 0; d < 4; ++d) {
-        if constexpr (BT == 1) {
+        for (int d = 0; d < 4; ++d) {
           // Packed fp16 FMAs, two rows per op, both columns of the word.
-          const uint32_t xp = HAS_S ? pk_mul(xhp[j][0][d], __builtin_bit_cast(u32x4, sv)[d]) : xhp[j][0][d];
+          const uint32_t xp = HAS_S ? pk_mul(xw[0][d], __builtin_bit_cast(u32x4, sv)[d]) : xw[0][d];
           const h2 xx = __builtin_bit_cast(h2, xp);
           const h2 xl = {xx.x, xx.x}, xh = {xx.y, xx.y};
           const h2 c[8] = {as_h2(t1l[d][0]), as_h2(t1l[d][1]), as_h2(t2l[d][0]), as_h2(t2l[d][1]),
@@ -320,7 +350,17 @@ __global__ __launch_bounds__(kT) void k_decode_e8d4(LinearArgs a) {
             acc16[q] = d == 0 ? c[q] * xl : __builtin_elementwise_fma(c[q], xl, acc16[q]);
             acc16[q] = __builtin_elementwise_fma(c[q + 4], xh, acc16[q]);
           }
-        } else {
+        }
+        // Chunk partial sums (8 columns) into the fp32 accumulators, times 2^e.
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const uint32_t pq = __builtin_bit_cast(uint32_t, acc16[q]);
+          acc[2 * q] = fma_lo(pq, sc, acc[2 * q]);
+          acc[2 * q + 1] = fma_hi(pq, sc, acc[2 * q + 1]);
+        }
+      } else {
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
           // (c_k(lo), c_k(hi)) fp16 pairs for k = 0..7
           uint32_t pr[8];
           pr[0] = perm(t1h[d][0], t1l[d][0], 0x05040100u);
@@ -335,41 +375,26 @@ __global__ __launch_bounds__(kT) void k_decode_e8d4(LinearArgs a) {
           if (HAS_S) sp = __builtin_bit_cast(u32x4, sv)[d];
 #pragma unroll
           for (int b = 0; b < BT; ++b) {
-            const uint32_t xp = HAS_S ? pk_mul(xhp[j][b][d], sp) : xhp[j][b][d];
+            const uint32_t xp = HAS_S ? pk_mul(xw[b][d], sp) : xw[b][d];
 #pragma unroll
             for (int k = 0; k < 8; ++k) acc[b * 8 + k] = dot2(pr[k], xp, acc[b * 8 + k]);
           }
         }
       }
-      if constexpr (BT == 1) {
-        // Chunk partial sums (8 columns) into the fp32 accumulators.
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const uint32_t pq = __builtin_bit_cast(uint32_t, acc16[q]);
-          acc[2 * q] = add_lo(pq, acc[2 * q]);
-          acc[2 * q + 1] = add_hi(pq, acc[2 * q + 1]);
-        }
-      }
     }
     if (!gathered) load_gather();
 
-    // Critical blocks: add O·(h S x) in the accumulator's units, minus what
-    // the marker index contributed in the main loop (table row 511).
-    auto correct = [&](const f16x8 o, int col, uint16_t (&xs)[BT], f16 hc, float sc) {
+    // Critical blocks: add O·(x h) in the accumulator's units, minus what the
+    // marker index contributed in the main loop (table row 511 against the
+    // same activation operand).  x·h for O is the activation table's value.
+    auto correct = [&](const f16x8 o, int col, float sc) {
+      const float csx = BT == 1 ? csc[col >> 3] : 1.0f;
 #pragma unroll
       for (int b = 0; b < BT; ++b) {
         if (b < B) {
-          float xo, xm;   // x·h for O (no S); what the main loop used
-          if constexpr (BT == 1) {
-            xo = Act<XT>::mul_f16(xs[b], hc) / out_scale;
-            const f16 x16 = (f16)xo;
-            xm = HAS_S ? (float)(f16)((float)x16 * sc) : (float)x16;
-          } else {
-            const f16 hd = (f16)((float)hc / out_scale);
-            const f16 xhd = (f16)((float)__builtin_bit_cast(f16, xs[b]) * (float)hd);
-            xo = Act<XT>::mul_f16(xs[b], hc) / out_scale;
-            xm = HAS_S ? (float)(f16)((float)xhd * sc) : (float)xhd;
-          }
+          const f16 x16 = __builtin_bit_cast(f16, xs[b * NP + col]);
+          const float xo = (float)x16 * csx;
+          const float xm = HAS_S ? (float)(f16)((float)x16 * sc) * csx : xo;
 #pragma unroll
           for (int k = 0; k < 8; ++k)
             acc[b * 8 + k] += (float)o[k] * xo - (float)t5[k & 3] * xm;
@@ -377,16 +402,13 @@ __global__ __launch_bounds__(kT) void k_decode_e8d4(LinearArgs a) {
       }
     };
     if (row_ok && ent < cre - crb)
-      correct(__builtin_bit_cast(f16x8, eo), ecol, gx, gh, (float)gs);
+      correct(__builtin_bit_cast(f16x8, eo), (unsigned)ecol < (unsigned)N ? ecol : 0, (float)gs);
     // Rows with more than 64·S critical blocks: the rest, synchronously.
     if (row_ok) {
       for (int i = crb + 64 * S + ent; i < cre; i += 64 * S) {
         const int col = a.O_col[i];
-        uint16_t xs[BT];
-#pragma unroll
-        for (int b = 0; b < BT; ++b) xs[b] = a.x[(size_t)(b < B ? b : B - 1) * N + col];
         const float sc = HAS_S ? (float)a.S[(size_t)grp * N + col] : 1.0f;
-        correct(*(const f16x8*)(a.O + (size_t)i * 8), col, xs, a.h[col], sc);
+        correct(*(const f16x8*)(a.O + (size_t)i * 8), col, sc);
       }
     }
 
@@ -399,6 +421,7 @@ __global__ __launch_bounds__(kT) void k_decode_e8d4(LinearArgs a) {
     const int base = wave_reduce_halving<V>(acc);
     if constexpr (S == 1) {
       // The wave owns the row: write straight from the reducing lanes.
+      (void)base;
       if (row_ok && WaveReduceOut<V>::writer(lane) && wb < B) {
         const float sum = acc[0] * out_scale * (float)og + (float)ob;
         a.y[(size_t)wb * (8 * M) + 8 * m + wk] = Act<XT>::from_f32(sum);
@@ -452,7 +475,15 @@ int chunks_for(int nch, int S) {
   return 0;
 }
 
-bool fits(int J, int B) { return J > 0 && (B == 1 || J * B <= 16); }
+// Dynamic LDS of the activation side: BT padded fp16 rows, plus the per-chunk
+// scales for B = 1.
+size_t act_lds_bytes(int N, int BT) {
+  return (size_t)BT * (N + 8) * 2 + (BT == 1 ? (size_t)((N >> 3) + 1) * 4 : 0);
+}
+constexpr size_t kActLdsMax = 64 * 1024;
+constexpr size_t kLdsPerCu = 160 * 1024;
+
+bool fits(int J, int N, int BT) { return J > 0 && act_lds_bytes(N, BT) <= kActLdsMax; }
 
 template <int BT, int J, int S, bool HAS_S, typename XT>
 void launch_k(const LinearArgs& a, hipStream_t s) {
@@ -460,45 +491,53 @@ void launch_k(const LinearArgs& a, hipStream_t s) {
   constexpr int P = J >= 8 ? 1 : 8 / J;
   constexpr int R = kW / S;
   auto kern = k_decode_e8d4<BT, J, P, S, HAS_S, XT>;
-  // As many workgroups per CU as the registers allow (one wave of each
+  // As many workgroups per CU as registers and LDS allow (one wave of each
   // workgroup per SIMD): occupancy hides the LDS lookup latency.
-  static int per_cu = 0;
-  if (per_cu == 0) {
+  static int reg_cu = 0;
+  static size_t static_lds = 0;
+  if (reg_cu == 0) {
     hipFuncAttributes fa;
     int v = 128;
-    if (hipFuncGetAttributes(&fa, (const void*)kern) == hipSuccess && fa.numRegs > 0) v = fa.numRegs;
+    if (hipFuncGetAttributes(&fa, (const void*)kern) == hipSuccess) {
+      if (fa.numRegs > 0) v = fa.numRegs;
+      static_lds = fa.sharedSizeBytes;
+    }
     const int waves = 512 / ((v + 7) / 8 * 8);
-    per_cu = waves < 1 ? 1 : (waves > 8 ? 8 : waves);
+    reg_cu = waves < 1 ? 1 : (waves > 8 ? 8 : waves);
   }
+  const size_t dyn = act_lds_bytes(a.N, BT);
+  int per_cu = (int)(kLdsPerCu / (static_lds + dyn + 256));
+  if (per_cu > reg_cu) per_cu = reg_cu;
+  if (per_cu < 1) per_cu = 1;
   const int RG = (a.M + R - 1) / R;
   int grid = cu_count() * per_cu;
   if (grid > RG) grid = RG;
-  kern<<<grid, kT, 0, s>>>(a);
+  kern<<<grid, kT, dyn, s>>>(a);
 }
 
 template <int BT, int S, bool HAS_S, typename XT>
 int launch_s(const LinearArgs& a, hipStream_t s) {
   const int J = chunks_for(a.N >> 3, S);
-  if (!fits(J, BT)) return -1;
+  if (!fits(J, a.N, BT)) return -1;
   if (J == 2) { launch_k<BT, 2, S, HAS_S, XT>(a, s); return 0; }
-  if constexpr (BT <= 4) if (J == 4) { launch_k<BT, 4, S, HAS_S, XT>(a, s); return 0; }
-  if constexpr (BT <= 2) if (J == 8) { launch_k<BT, 8, S, HAS_S, XT>(a, s); return 0; }
+  if (J == 4) { launch_k<BT, 4, S, HAS_S, XT>(a, s); return 0; }
+  if (J == 8) { launch_k<BT, 8, S, HAS_S, XT>(a, s); return 0; }
   return -1;
 }
 
 template <int BT, bool HAS_S, typename XT>
 int launch_bt(const LinearArgs& a, hipStream_t s) {
   const int nch = a.N >> 3;
-  // Smallest row split that gives the chip about 8 waves per CU; the
-  // register budget of the activation pairs can force a wider split.
+  // Smallest row split that gives the chip about 8 waves per CU (and keeps
+  // the chunks per lane within the kernel's range).
   const int want = cu_count() * 8;
   int S = 4;
   for (int cand = 1; cand <= 4; cand *= 2) {
-    if (!fits(chunks_for(nch, cand), BT)) continue;
+    if (!fits(chunks_for(nch, cand), a.N, BT)) continue;
     S = cand;
     if ((long)a.M * cand >= want) break;
   }
-  if (!fits(chunks_for(nch, S), BT)) return -1;
+  if (!fits(chunks_for(nch, S), a.N, BT)) return -1;
   if (S == 1) return launch_s<BT, 1, HAS_S, XT>(a, s);
   if (S == 2) return launch_s<BT, 2, HAS_S, XT>(a, s);
   return launch_s<BT, 4, HAS_S, XT>(a, s);
@@ -520,8 +559,8 @@ int launch_decode_e8d4(const LinearArgs& a, hipStream_t s) {
   if (a.B < 1 || a.B > 8) return -1;
   if (a.codes_f32) return -1;  // fp32 tables take the generic kernel
   if (a.x_bf16) {
-    if (a.B >= 2) return -1;   // fp16 activation pairs only
-    return a.S ? launch_b<true, bf16>(a, s) : launch_b<false, bf16>(a, s);
+    if (a.B >= 2) return -1;   // the B >= 2 pairs are formed in fp16 arithmetic
+    return a.S ? launch_bt<1, true, bf16>(a, s) : launch_bt<1, false, bf16>(a, s);
   }
   return a.S ? launch_b<true, f16>(a, s) : launch_b<false, f16>(a, s);
 }
