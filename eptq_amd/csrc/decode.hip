@@ -229,21 +229,27 @@ __global__ __launch_bounds__(kT) void k_decode_e8d4(LinearArgs a) {
     }
   }
 
-  u32x4 qv[P][J];
+  // Index chunks in flight: K of each of the P row groups of the ring.  A
+  // slot is refilled as soon as its chunk's table addresses are formed —
+  // with the chunk K ahead in the same row, else the matching chunk of the row
+  // group P·G ahead — so each wave's requests reach HBM in a steady stream.
+  constexpr int K = J > 4 ? 4 : J;
+  static_assert(J % K == 0, "chunks per row must be a multiple of the chunks in flight");
+  u32x4 qv[P][K];
   // Index chunks are read through a buffer resource spanning one row (an
   // empty one past the last row): out-of-range chunks read as zero, so the
   // loads need no branches or clamps, and the compiler can wait for exactly
   // the load it needs (vmcnt counts loads in issue order).
-  auto load_q = [&](u32x4 (&dst)[J], int rg) {
+  auto load_chunk = [&](u32x4& dst, int rg, int j) {
     const int row = rg * R + slot;            // wave-uniform
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
         (void*)(a.Q + (size_t)(row < M ? row : 0) * N), (short)0, row < M ? N * 2 : 0, kBufferWord3);
-#pragma unroll
-    for (int j = 0; j < J; ++j)
-      dst[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, chunk(j) * 16, 0, kNonTemporal));
+    dst = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, chunk(j) * 16, 0, kNonTemporal));
   };
 #pragma unroll
-  for (int p = 0; p < P; ++p) load_q(qv[p], blockIdx.x + p * G);
+  for (int p = 0; p < P; ++p)
+#pragma unroll
+    for (int j = 0; j < K; ++j) load_chunk(qv[p][j], blockIdx.x + p * G, j);
 
   // Critical blocks, first 64·S entries of a row: lane `ent` of the row's
   // S waves holds entry rb + ent (its column and O vector).  Buffer resources
@@ -308,32 +314,37 @@ __global__ __launch_bounds__(kT) void k_decode_e8d4(LinearArgs a) {
 #pragma unroll
     for (int i = 0; i < V; ++i) acc[i] = 0.0f;
 
-    bool gathered = false;
 #pragma unroll
     for (int j = 0; j < J; ++j) {
-      if (seg * 64 + 64 * S * j >= nch) break;   // uniform: no lane has a chunk left
-      if (j == J / 2) { load_gather(); gathered = true; }
+      const bool live = seg * 64 + 64 * S * j < nch;   // uniform: some lane has this chunk
+      if (j == J / 2) load_gather();
       const int cj = chunk(j) < nch ? chunk(j) : nch;   // past the end: the zero chunk
       f16x8 sv;
-      if (HAS_S) sv = *(const f16x8*)(a.S + (size_t)grp * N + ((cj < nch ? cj : 0) << 3));
       u32x4 xw[BT];
-#pragma unroll
-      for (int b = 0; b < BT; ++b) xw[b] = *(const u32x4*)(xs + b * NP + cj * 8);
       // All 16 table lookups of the chunk first, then the arithmetic, so the
       // LDS latency is paid once per chunk rather than once per word.
       u32x2 t1l[4], t2l[4], t1h[4], t2h[4];
+      if (live) {
+        if (HAS_S) sv = *(const f16x8*)(a.S + (size_t)grp * N + ((cj < nch ? cj : 0) << 3));
 #pragma unroll
-      for (int d = 0; d < 4; ++d) {
-        const uint32_t w = qv[p][j][d];
-        const uint32_t a1lo = (w >> 4) & 0xFF8u;
-        const uint32_t a1hi = (w >> 20) & 0xFF8u;
-        const uint32_t a2lo = bfi(0x3F8u, w << 3, a1lo);
-        const uint32_t a2hi = bfi(0x3F8u, w >> 13, a1hi);
-        t1l[d] = *(const u32x2*)(tabB + a1lo);
-        t2l[d] = *(const u32x2*)(tabB + a2lo);
-        t1h[d] = *(const u32x2*)(tabB + a1hi);
-        t2h[d] = *(const u32x2*)(tabB + a2hi);
+        for (int b = 0; b < BT; ++b) xw[b] = *(const u32x4*)(xs + b * NP + cj * 8);
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+          const uint32_t w = qv[p][j % K][d];
+          const uint32_t a1lo = (w >> 4) & 0xFF8u;
+          const uint32_t a1hi = (w >> 20) & 0xFF8u;
+          const uint32_t a2lo = bfi(0x3F8u, w << 3, a1lo);
+          const uint32_t a2hi = bfi(0x3F8u, w >> 13, a1hi);
+          t1l[d] = *(const u32x2*)(tabB + a1lo);
+          t2l[d] = *(const u32x2*)(tabB + a2lo);
+          t1h[d] = *(const u32x2*)(tabB + a1hi);
+          t2h[d] = *(const u32x2*)(tabB + a2hi);
+        }
       }
+      // Refill this chunk's ring slot.
+      if (j + K < J) load_chunk(qv[p][j % K], rg, j + K);
+      else load_chunk(qv[p][j % K], rg + P * G, j + K - J);
+      if (!live) continue;
       if constexpr (BT == 1) {
         const float sc = csc[cj];
         h2 acc16[4];   // rows (0,1) (2,3) (4,5) (6,7) of this chunk, fp16
@@ -382,7 +393,6 @@ __global__ __launch_bounds__(kT) void k_decode_e8d4(LinearArgs a) {
         }
       }
     }
-    if (!gathered) load_gather();
 
     // Critical blocks: add O·(x h) in the accumulator's units, minus what the
     // marker index contributed in the main loop (table row 511 against the
@@ -412,9 +422,8 @@ __global__ __launch_bounds__(kT) void k_decode_e8d4(LinearArgs a) {
       }
     }
 
-    // Next row group's entries, then this ring slot's refill.
+    // Next row group's entries.
     load_entries(nrb, nre);
-    load_q(qv[p], rg + P * G);
     crb = nrb; cre = nre;
     nrb = frb; nre = fre;
 
@@ -487,8 +496,9 @@ bool fits(int J, int N, int BT) { return J > 0 && act_lds_bytes(N, BT) <= kActLd
 
 template <int BT, int J, int S, bool HAS_S, typename XT>
 void launch_k(const LinearArgs& a, hipStream_t s) {
-  // About 8 index chunks (128 bytes) per lane in flight: P row groups of J.
-  constexpr int P = J >= 8 ? 1 : 8 / J;
+  // About 8 index chunks (128 bytes) per lane in flight: P row groups of
+  // min(J, 4) chunks.
+  constexpr int P = 8 / (J > 4 ? 4 : J);
   constexpr int R = kW / S;
   auto kern = k_decode_e8d4<BT, J, P, S, HAS_S, XT>;
   // As many workgroups per CU as registers and LDS allow (one wave of each
