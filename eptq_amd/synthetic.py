@@ -55,3 +55,57 @@ def make_layer(out_features: int, in_features: int, *, seed: int, percmask: floa
 def make_x(batch: int, in_features: int, *, seed: int, device="cpu") -> torch.Tensor:
     gen = torch.Generator(device=device).manual_seed(seed)
     return torch.randn((batch, in_features), generator=gen, device=device).half()
+
+
+def write_quantized_model(out_dir, hf_config, quantizer_type: str = "e8_d4", radius: float = 1.75,
+                          percmask: float = 0.01, seed: int = 0, tokenizer=None,
+                          qb_size: Optional[int] = None) -> None:
+    """Write a synthetic quantized-model directory in the reference layout
+    (``README.md:127-152``; writers ``quantize.py:36-105,425-433``).
+
+    ``hf_config`` is a ``transformers`` config (Llama or OPT architecture);
+    every decoder ``nn.Linear`` becomes a seeded ``QuantizedLayerData``, the
+    remaining parameters are random.  ``tokenizer``, if given, is saved under
+    ``tokenizer/``.
+    """
+    import json
+    from pathlib import Path
+
+    from accelerate import init_empty_weights
+    from transformers import AutoModelForCausalLM
+
+    from .handlers import ModelHandler, get_model_handler_by_type
+    from .quantizers import E8D4Quantizer, E8LatticeQuantizer
+    from .reconstruct import save_quantizer
+
+    out = Path(out_dir)
+    out.mkdir(parents=True, exist_ok=True)
+    with open(out / "quant_config.json", "w") as f:
+        json.dump({"quantizer_type": quantizer_type, "codebook_radius": radius,
+                   "model_name": None}, f, indent=2)
+    q = E8D4Quantizer(radius=radius) if quantizer_type == "e8_d4" else E8LatticeQuantizer(radius=radius)
+    save_quantizer(q, out, quantizer_type)
+    hf_config.save_pretrained(out)
+    if tokenizer is not None:
+        tokenizer.save_pretrained(out / "tokenizer")
+
+    with init_empty_weights():
+        model = AutoModelForCausalLM.from_config(hf_config)
+    handler = get_model_handler_by_type(ModelHandler.detect_model_type(model))
+    gen = torch.Generator().manual_seed(seed)
+    quantized = set()
+    for lid, layer in enumerate(handler.get_layers(model)):
+        layer_dir = out / f"layer_{lid}"
+        layer_dir.mkdir(exist_ok=True)
+        for k, (name, lin) in enumerate(handler.get_linear_layers(layer).items()):
+            qd = make_layer(lin.out_features, lin.in_features, seed=seed + 1000 * lid + k,
+                            percmask=percmask, bias=lin.bias is not None, qb_size=qb_size)
+            qd.save(layer_dir / f"{name}.pt")
+            quantized.update({f"{name}.weight", f"{name}.bias"})
+        other = {n: (torch.randn(p.shape, generator=gen) * 0.02 + (1.0 if "norm" in n else 0.0)).half()
+                 for n, p in layer.named_parameters() if n not in quantized}
+        torch.save(other, layer_dir / "non_quantized.pt")
+    layer_prefix = {id(p) for l in handler.get_layers(model) for p in l.parameters()}
+    glob = {n: (torch.randn(p.shape, generator=gen) * 0.02 + (1.0 if "norm" in n else 0.0)).half()
+            for n, p in model.named_parameters() if id(p) not in layer_prefix}
+    torch.save(glob, out / "non_quantized_params.pt")

@@ -1,0 +1,103 @@
+"""The C ABI boundary on the CPU: the library loads, exports every symbol that
+``include/eptq_hip.h`` declares with the ctypes signatures the Python side
+binds, and rejects invalid arguments with the documented codes before touching
+the GPU (no compute calls here)."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from eptq_amd.kernels import _lib
+
+HEADER = Path(__file__).resolve().parent.parent / "include" / "eptq_hip.h"
+
+
+def header_functions():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(eptq_\w+)\s*\(", text, flags=re.M)
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not _lib.LIB_PATH.exists():
+        pytest.skip("libeptq_hip.so not built (run __graft_entry__.build())")
+    return _lib.load()
+
+
+def test_header_declares_the_bound_functions():
+    names = header_functions()
+    assert len(names) == len(set(names))
+    assert set(names) == set(_lib.SIGNATURES)
+
+
+def test_every_declared_symbol_is_exported(lib):
+    for name in header_functions():
+        assert hasattr(lib, name), name
+        assert isinstance(getattr(lib, name), ctypes._CFuncPtr)
+
+
+def test_abi_version(lib):
+    assert lib.eptq_abi_version() == 1
+    assert lib.eptq_last_error() is not None
+
+
+def _fwd_args(**over):
+    a = dict(Q=16, codes=16, codes_dtype=_lib.EPTQ_F16, g=16, h=16, x=16, x_dtype=_lib.EPTQ_F16,
+             O_vals=None, O_col=None, O_row_ptr=16, bias=None, S_group=None, n_groups=0,
+             M=4, N=64, B=1, y=16, stream=None)
+    a.update(over)
+    return list(a.values())
+
+
+@pytest.mark.parametrize("fn", ["eptq_e8d4_forward", "eptq_e8_forward"])
+@pytest.mark.parametrize("over,code,msg", [
+    (dict(Q=None), _lib.EPTQ_EINVAL, "null"),
+    (dict(O_row_ptr=None), _lib.EPTQ_EINVAL, "null"),
+    (dict(M=0), _lib.EPTQ_EINVAL, "positive"),
+    (dict(N=-8), _lib.EPTQ_EINVAL, "positive"),
+    (dict(B=-1), _lib.EPTQ_EINVAL, "B=-1"),
+    (dict(x=None), _lib.EPTQ_EINVAL, "null x/y"),
+    (dict(O_vals=16), _lib.EPTQ_EINVAL, "both"),
+    (dict(codes_dtype=7), _lib.EPTQ_EINVAL, "codes_dtype"),
+    (dict(x_dtype=_lib.EPTQ_F32), _lib.EPTQ_EINVAL, "x_dtype"),
+    (dict(N=60), _lib.EPTQ_EUNSUPPORTED, "multiple of 8"),
+    (dict(Q=18), _lib.EPTQ_EUNSUPPORTED, "aligned"),
+    (dict(S_group=16, n_groups=3), _lib.EPTQ_EINVAL, "divide"),
+    (dict(S_group=16, n_groups=8), _lib.EPTQ_EUNSUPPORTED, "multiple of 8"),
+])
+def test_forward_rejects_invalid_arguments(lib, fn, over, code, msg):
+    rc = getattr(lib, fn)(*_fwd_args(**over))
+    assert rc == code
+    assert msg in lib.eptq_last_error().decode()
+    assert fn in lib.eptq_last_error().decode()
+
+
+def test_forward_empty_batch_is_a_no_op(lib):
+    assert lib.eptq_e8d4_forward(*_fwd_args(B=0, x=None, y=None)) == _lib.EPTQ_OK
+
+
+@pytest.mark.parametrize("fn", ["eptq_e8d4_dequant", "eptq_e8_dequant"])
+def test_dequant_rejects_invalid_arguments(lib, fn):
+    f = getattr(lib, fn)
+    ok = dict(Q=16, codes=16, g=16, h=16, O_vals=None, O_col=None, O_row_ptr=16, S_group=None,
+              n_groups=0, M=4, N=64, W=16, stream=None)
+    rc = f(*{**ok, "W": None}.values())
+    assert rc == _lib.EPTQ_EINVAL and "null W" in lib.eptq_last_error().decode()
+    rc = f(*{**ok, "codes": 24}.values())
+    assert rc == _lib.EPTQ_EUNSUPPORTED and "aligned" in lib.eptq_last_error().decode()
+    rc = f(*{**ok, "W": 20}.values())
+    assert rc == _lib.EPTQ_EUNSUPPORTED and "8-byte" in lib.eptq_last_error().decode()
+
+
+def test_python_wrapper_raises_on_error_codes(lib):
+    with pytest.raises(_lib.EptqError, match="eptq_e8d4_forward"):
+        _lib.check(lib.eptq_e8d4_forward(*_fwd_args(Q=None)), "eptq_e8d4_forward")
+
+
+def test_missing_library_fails_loudly(tmp_path):
+    with pytest.raises(_lib.EptqError, match="not built"):
+        _lib.load(tmp_path / "missing.so")
