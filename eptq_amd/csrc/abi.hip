@@ -55,49 +55,51 @@ int check_common(const char* fn, const void* Q, const void* codes, const void* g
   return EPTQ_OK;
 }
 
-int linear_common(int kind, const void* Q, const void* codes, int codes_dtype, const void* g,
-                  const void* h, const void* x, int x_dtype, const void* O_vals,
-                  const void* O_col, const void* O_row_ptr, const void* bias,
-                  const void* S_group, int n_groups, int M, int N, int B, void* y,
-                  void* stream) {
-  const char* fn = kind == eptq::KIND_E8D4 ? "eptq_e8d4_forward" : "eptq_e8_forward";
+// Validate one layer's operands and fill its kernel arguments (y, ldy set by
+// the caller).
+int layer_args(const char* fn, int kind, const void* Q, const void* codes, int codes_dtype,
+               const void* g, const void* h, const void* x, int x_dtype, const void* O_vals,
+               const void* O_col, const void* O_row_ptr, const void* bias, const void* S_group,
+               int n_groups, int M, int N, int B, eptq::LinearArgs* a) {
   int qb = 1;
   int rc = check_common(fn, Q, codes, g, h, O_vals, O_col, O_row_ptr, S_group, n_groups, M, N, &qb);
   if (rc) return rc;
   if (B < 0) return fail(EPTQ_EINVAL, "%s: B=%d", fn, B);
-  if (B == 0) return EPTQ_OK;
-  if (!x || !y) return fail(EPTQ_EINVAL, "%s: null x/y", fn);
+  if (B > 0 && !x) return fail(EPTQ_EINVAL, "%s: null x/y", fn);
   if (codes_dtype != EPTQ_F16 && codes_dtype != EPTQ_F32)
     return fail(EPTQ_EINVAL, "%s: codes_dtype must be EPTQ_F16 or EPTQ_F32", fn);
   if (x_dtype != EPTQ_F16 && x_dtype != EPTQ_BF16)
     return fail(EPTQ_EINVAL, "%s: x_dtype must be EPTQ_F16 or EPTQ_BF16", fn);
   if (N % 8 != 0) return fail(EPTQ_EUNSUPPORTED, "%s: in_features=%d not a multiple of 8", fn, N);
-  if (!aligned16(Q) || !aligned16(x) || !aligned16(h) || (S_group && !aligned16(S_group)))
+  if (!aligned16(Q) || (B > 0 && !aligned16(x)) || !aligned16(h) || (S_group && !aligned16(S_group)))
     return fail(EPTQ_EUNSUPPORTED, "%s: Q, x, h and S_group must be 16-byte aligned", fn);
   if (kind == eptq::KIND_E8 && !aligned16(codes))
     return fail(EPTQ_EUNSUPPORTED, "%s: E8 codebook must be 16-byte aligned", fn);
+  a->Q = (const int16_t*)Q;
+  a->codes = codes;
+  a->codes_f32 = codes_dtype == EPTQ_F32;
+  a->g = (const eptq::f16*)g;
+  a->h = (const eptq::f16*)h;
+  a->x = (const uint16_t*)x;
+  a->x_bf16 = x_dtype == EPTQ_BF16;
+  a->O = (const eptq::f16*)O_vals;
+  a->O_col = (const int32_t*)O_col;
+  a->O_row_ptr = (const int32_t*)O_row_ptr;
+  a->bias = (const eptq::f16*)bias;
+  a->S = (const eptq::f16*)S_group;
+  a->qb = qb;
+  a->M = M;
+  a->N = N;
+  a->B = B;
+  a->y = nullptr;
+  a->ldy = 8 * M;
+  return EPTQ_OK;
+}
 
-  eptq::LinearArgs a;
-  a.Q = (const int16_t*)Q;
-  a.codes = codes;
-  a.codes_f32 = codes_dtype == EPTQ_F32;
-  a.g = (const eptq::f16*)g;
-  a.h = (const eptq::f16*)h;
-  a.x = (const uint16_t*)x;
-  a.x_bf16 = x_dtype == EPTQ_BF16;
-  a.O = (const eptq::f16*)O_vals;
-  a.O_col = (const int32_t*)O_col;
-  a.O_row_ptr = (const int32_t*)O_row_ptr;
-  a.bias = (const eptq::f16*)bias;
-  a.S = (const eptq::f16*)S_group;
-  a.qb = qb;
-  a.M = M;
-  a.N = N;
-  a.B = B;
-  a.y = (uint16_t*)y;
-  hipStream_t s = (hipStream_t)stream;
-
-  if (B <= eptq::kMatvecMaxBatch) {
+// Launch one layer on the kernel for its codebook and batch size.
+int dispatch(const char* fn, int kind, const eptq::LinearArgs& a, hipStream_t s) {
+  int rc = 0;
+  if (a.B <= eptq::kMatvecMaxBatch) {
     if (kind == eptq::KIND_E8D4) {
       rc = eptq::launch_decode_e8d4(a, s);
       if (rc) rc = eptq::launch_matvec<eptq::KIND_E8D4>(a, s);
@@ -108,15 +110,33 @@ int linear_common(int kind, const void* Q, const void* codes, int codes_dtype, c
     rc = eptq::launch_gemm_e8d4(a, s);
   } else {
     // E8 at large batch: batch tiles through the decode matvec.
-    for (int b0 = 0; b0 < B && rc == 0; b0 += eptq::kMatvecMaxBatch) {
+    for (int b0 = 0; b0 < a.B && rc == 0; b0 += eptq::kMatvecMaxBatch) {
       eptq::LinearArgs t = a;
-      t.B = B - b0 < eptq::kMatvecMaxBatch ? B - b0 : eptq::kMatvecMaxBatch;
-      t.x = a.x + (size_t)b0 * N;
-      t.y = a.y + (size_t)b0 * 8 * M;
+      t.B = a.B - b0 < eptq::kMatvecMaxBatch ? a.B - b0 : eptq::kMatvecMaxBatch;
+      t.x = a.x + (size_t)b0 * a.N;
+      t.y = a.y + (size_t)b0 * a.ldy;
       rc = eptq::launch_matvec<eptq::KIND_E8>(t, s);
     }
   }
-  if (rc) return fail(EPTQ_EUNSUPPORTED, "%s: no kernel for M=%d N=%d B=%d", fn, M, N, B);
+  if (rc) return fail(EPTQ_EUNSUPPORTED, "%s: no kernel for M=%d N=%d B=%d", fn, a.M, a.N, a.B);
+  return EPTQ_OK;
+}
+
+int linear_common(int kind, const void* Q, const void* codes, int codes_dtype, const void* g,
+                  const void* h, const void* x, int x_dtype, const void* O_vals,
+                  const void* O_col, const void* O_row_ptr, const void* bias,
+                  const void* S_group, int n_groups, int M, int N, int B, void* y,
+                  void* stream) {
+  const char* fn = kind == eptq::KIND_E8D4 ? "eptq_e8d4_forward" : "eptq_e8_forward";
+  eptq::LinearArgs a;
+  int rc = layer_args(fn, kind, Q, codes, codes_dtype, g, h, x, x_dtype, O_vals, O_col, O_row_ptr,
+                      bias, S_group, n_groups, M, N, B, &a);
+  if (rc) return rc;
+  if (B == 0) return EPTQ_OK;
+  if (!y) return fail(EPTQ_EINVAL, "%s: null x/y", fn);
+  a.y = (uint16_t*)y;
+  rc = dispatch(fn, kind, a, (hipStream_t)stream);
+  if (rc) return rc;
   return check_launch(fn);
 }
 
@@ -177,6 +197,47 @@ int eptq_e8_forward(const void* Q, const void* codes, int codes_dtype, const voi
                     void* stream) {
   return linear_common(eptq::KIND_E8, Q, codes, codes_dtype, g, h, x, x_dtype, O_vals, O_col,
                        O_row_ptr, bias, S_group, n_groups, M, N, B, y, stream);
+}
+
+int eptq_e8d4_forward_multi(int n_layers, const eptq_layer* layers, const void* codes,
+                            int codes_dtype, const void* x, int x_dtype, int N, int B, void* y,
+                            int ldy, void* stream) {
+  const char* fn = "eptq_e8d4_forward_multi";
+  if (n_layers <= 0 || !layers) return fail(EPTQ_EINVAL, "%s: n_layers=%d", fn, n_layers);
+  if (B < 0) return fail(EPTQ_EINVAL, "%s: B=%d", fn, B);
+  if (B > 0 && (!x || !y)) return fail(EPTQ_EINVAL, "%s: null x/y", fn);
+  eptq::LinearArgs a[eptq::kMaxLayers];
+  const int n = n_layers;
+  // Validate every layer first; each writes columns [y_offset, y_offset + 8M) of y.
+  for (int l = 0; l < n; ++l) {
+    const eptq_layer& L = layers[l];
+    eptq::LinearArgs t;
+    int rc = layer_args(fn, eptq::KIND_E8D4, L.Q, codes, codes_dtype, L.g, L.h, x, x_dtype, L.O_vals,
+                        L.O_col, L.O_row_ptr, L.bias, L.S_group, L.n_groups, L.M, N, B, &t);
+    if (rc) return rc;
+    if (L.y_offset < 0 || L.y_offset + 8LL * L.M > (long long)ldy || (L.y_offset & 3))
+      return fail(EPTQ_EINVAL, "%s: layer %d columns [%lld, %lld) outside a y row of %d (offset %% 4 == 0)",
+                  fn, l, L.y_offset, L.y_offset + 8LL * L.M, ldy);
+    t.y = (uint16_t*)y + L.y_offset;
+    t.ldy = ldy;
+    if (l < eptq::kMaxLayers) a[l] = t;
+  }
+  if (B == 0) return EPTQ_OK;
+  hipStream_t s = (hipStream_t)stream;
+  // One launch when the decode kernel takes them all, else one per layer.
+  if (n > eptq::kMaxLayers || eptq::launch_decode_e8d4_multi(a, n, s) != 0) {
+    for (int l = 0; l < n; ++l) {
+      eptq::LinearArgs t;
+      const eptq_layer& L = layers[l];
+      layer_args(fn, eptq::KIND_E8D4, L.Q, codes, codes_dtype, L.g, L.h, x, x_dtype, L.O_vals, L.O_col,
+                 L.O_row_ptr, L.bias, L.S_group, L.n_groups, L.M, N, B, &t);
+      t.y = (uint16_t*)y + L.y_offset;
+      t.ldy = ldy;
+      const int rc = dispatch(fn, eptq::KIND_E8D4, t, s);
+      if (rc) return rc;
+    }
+  }
+  return check_launch(fn);
 }
 
 int eptq_e8d4_dequant(const void* Q, const void* codes_f32, const void* g, const void* h,

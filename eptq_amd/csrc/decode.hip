@@ -79,7 +79,7 @@ __device__ __forceinline__ uint32_t pk_mul(uint32_t a, uint32_t b) {
 }  // namespace
 
 template <int BT, int J, int P, int S, bool HAS_S, typename XT>
-__global__ __launch_bounds__(kT) void k_decode_e8d4(LinearArgs a) {
+__global__ __launch_bounds__(kT) void k_decode_e8d4(MultiArgs ma) {
   constexpr int V = BT * 8;
   constexpr int R = kW / S;                    // rows per row group
   static_assert(V <= 64 && R * V <= kT, "one output per thread after the reduction");
@@ -90,6 +90,15 @@ __global__ __launch_bounds__(kT) void k_decode_e8d4(LinearArgs a) {
   // rows padded by one zero chunk; for B = 1 also csc[c] = the scale of chunk c.
   extern __shared__ __align__(16) char dyn[];
 
+  // This workgroup's layer and its index among the layer's workgroups.
+  int li = 0;
+#pragma unroll
+  for (int l = 1; l < kMaxLayers; ++l)
+    if (l < ma.n && (int)blockIdx.x >= ma.start[l]) li = l;
+  const LinearArgs a = li == 0 ? ma.l[0] : li == 1 ? ma.l[1] : li == 2 ? ma.l[2] : ma.l[3];
+  const int wg = (int)blockIdx.x - ma.start[li];
+  const int G = ma.start[li + 1] - ma.start[li];
+
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -98,7 +107,6 @@ __global__ __launch_bounds__(kT) void k_decode_e8d4(LinearArgs a) {
   const int nch = N >> 3;
   const int NP = N + 8;
   const int RG = (M + R - 1) / R;              // row groups
-  const int G = gridDim.x;
   const char* __restrict__ tabB = (const char*)tab;
   uint16_t* __restrict__ xs = (uint16_t*)dyn;
   float* __restrict__ csc = (float*)(dyn + BT * NP * 2);
@@ -115,8 +123,8 @@ __global__ __launch_bounds__(kT) void k_decode_e8d4(LinearArgs a) {
     re = a.O_row_ptr[row < M ? rr + 1 : rr];
   };
   int crb, cre, nrb, nre;
-  row_range(blockIdx.x, crb, cre);
-  row_range(blockIdx.x + G, nrb, nre);
+  row_range(wg, crb, cre);
+  row_range(wg + G, nrb, nre);
 
   // ---- loads: table and activations first; the activation table is built
   // before the index stream is requested, so its loads are not queued behind
@@ -249,7 +257,7 @@ __global__ __launch_bounds__(kT) void k_decode_e8d4(LinearArgs a) {
 #pragma unroll
   for (int p = 0; p < P; ++p)
 #pragma unroll
-    for (int j = 0; j < K; ++j) load_chunk(qv[p][j], blockIdx.x + p * G, j);
+    for (int j = 0; j < K; ++j) load_chunk(qv[p][j], wg + p * G, j);
 
   // Critical blocks, first 64·S entries of a row: lane `ent` of the row's
   // S waves holds entry rb + ent (its column and O vector).  Buffer resources
@@ -283,7 +291,7 @@ __global__ __launch_bounds__(kT) void k_decode_e8d4(LinearArgs a) {
   const int wb = wbase >> 3, wk = wbase & 7;
 
   int par = 0;
-  for (int rg0 = blockIdx.x; rg0 < RG; rg0 += P * G) {
+  for (int rg0 = wg; rg0 < RG; rg0 += P * G) {
 #pragma unroll
   for (int p = 0; p < P; ++p) {
     const int rg = rg0 + p * G;
@@ -433,7 +441,7 @@ __global__ __launch_bounds__(kT) void k_decode_e8d4(LinearArgs a) {
       (void)base;
       if (row_ok && WaveReduceOut<V>::writer(lane) && wb < B) {
         const float sum = acc[0] * out_scale * (float)og + (float)ob;
-        a.y[(size_t)wb * (8 * M) + 8 * m + wk] = Act<XT>::from_f32(sum);
+        a.y[(size_t)wb * a.ldy + 8 * m + wk] = Act<XT>::from_f32(sum);
       }
     } else {
       if (WaveReduceOut<V>::writer(lane)) {
@@ -450,7 +458,7 @@ __global__ __launch_bounds__(kT) void k_decode_e8d4(LinearArgs a) {
 #pragma unroll
           for (int w = 0; w < S; ++w) sum += red[par][sl * S + w][wbase];
           sum = sum * out_scale * (float)og + (float)ob;
-          a.y[(size_t)wb * (8 * M) + 8 * orow + wk] = Act<XT>::from_f32(sum);
+          a.y[(size_t)wb * a.ldy + 8 * orow + wk] = Act<XT>::from_f32(sum);
         }
       }
       par ^= 1;
@@ -495,7 +503,7 @@ constexpr size_t kLdsPerCu = 160 * 1024;
 bool fits(int J, int N, int BT) { return J > 0 && act_lds_bytes(N, BT) <= kActLdsMax; }
 
 template <int BT, int J, int S, bool HAS_S, typename XT>
-void launch_k(const LinearArgs& a, hipStream_t s) {
+void launch_k(const LinearArgs* layers, int n, hipStream_t s) {
   // About 8 index chunks (128 bytes) per lane in flight: P row groups of
   // min(J, 4) chunks.
   constexpr int P = 8 / (J > 4 ? 4 : J);
@@ -515,64 +523,87 @@ void launch_k(const LinearArgs& a, hipStream_t s) {
     const int waves = 512 / ((v + 7) / 8 * 8);
     reg_cu = waves < 1 ? 1 : (waves > 8 ? 8 : waves);
   }
-  const size_t dyn = act_lds_bytes(a.N, BT);
+  const size_t dyn = act_lds_bytes(layers[0].N, BT);
   int per_cu = (int)(kLdsPerCu / (static_lds + dyn + 256));
   if (per_cu > reg_cu) per_cu = reg_cu;
   if (per_cu < 1) per_cu = 1;
-  const int RG = (a.M + R - 1) / R;
-  int grid = cu_count() * per_cu;
-  if (grid > RG) grid = RG;
-  kern<<<grid, kT, dyn, s>>>(a);
+  MultiArgs ma;
+  ma.n = n;
+  ma.start[0] = 0;
+  for (int l = 0; l < kMaxLayers; ++l) {
+    if (l < n) {
+      ma.l[l] = layers[l];
+      const int RG = (layers[l].M + R - 1) / R;
+      const int g = cu_count() * per_cu < RG ? cu_count() * per_cu : RG;
+      ma.start[l + 1] = ma.start[l] + g;
+    } else {
+      ma.l[l] = layers[0];
+      ma.start[l + 1] = ma.start[l];
+    }
+  }
+  kern<<<ma.start[n], kT, dyn, s>>>(ma);
 }
 
 template <int BT, int S, bool HAS_S, typename XT>
-int launch_s(const LinearArgs& a, hipStream_t s) {
-  const int J = chunks_for(a.N >> 3, S);
-  if (!fits(J, a.N, BT)) return -1;
-  if (J == 2) { launch_k<BT, 2, S, HAS_S, XT>(a, s); return 0; }
-  if (J == 4) { launch_k<BT, 4, S, HAS_S, XT>(a, s); return 0; }
-  if (J == 8) { launch_k<BT, 8, S, HAS_S, XT>(a, s); return 0; }
+int launch_s(const LinearArgs* l, int n, hipStream_t s) {
+  const int J = chunks_for(l[0].N >> 3, S);
+  if (!fits(J, l[0].N, BT)) return -1;
+  if (J == 2) { launch_k<BT, 2, S, HAS_S, XT>(l, n, s); return 0; }
+  if (J == 4) { launch_k<BT, 4, S, HAS_S, XT>(l, n, s); return 0; }
+  if (J == 8) { launch_k<BT, 8, S, HAS_S, XT>(l, n, s); return 0; }
   return -1;
 }
 
 template <int BT, bool HAS_S, typename XT>
-int launch_bt(const LinearArgs& a, hipStream_t s) {
-  const int nch = a.N >> 3;
+int launch_bt(const LinearArgs* l, int n, hipStream_t s) {
+  const int N = l[0].N;
+  const int nch = N >> 3;
+  long Mt = 0;
+  for (int i = 0; i < n; ++i) Mt += l[i].M;
   // Smallest row split that gives the chip about 8 waves per CU (and keeps
   // the chunks per lane within the kernel's range).
   const int want = cu_count() * 8;
   int S = 4;
   for (int cand = 1; cand <= 4; cand *= 2) {
-    if (!fits(chunks_for(nch, cand), a.N, BT)) continue;
+    if (!fits(chunks_for(nch, cand), N, BT)) continue;
     S = cand;
-    if ((long)a.M * cand >= want) break;
+    if (Mt * cand >= want) break;
   }
-  if (!fits(chunks_for(nch, S), a.N, BT)) return -1;
-  if (S == 1) return launch_s<BT, 1, HAS_S, XT>(a, s);
-  if (S == 2) return launch_s<BT, 2, HAS_S, XT>(a, s);
-  return launch_s<BT, 4, HAS_S, XT>(a, s);
+  if (!fits(chunks_for(nch, S), N, BT)) return -1;
+  if (S == 1) return launch_s<BT, 1, HAS_S, XT>(l, n, s);
+  if (S == 2) return launch_s<BT, 2, HAS_S, XT>(l, n, s);
+  return launch_s<BT, 4, HAS_S, XT>(l, n, s);
 }
 
 template <bool HAS_S, typename XT>
-int launch_b(const LinearArgs& a, hipStream_t s) {
-  if (a.B == 1) return launch_bt<1, HAS_S, XT>(a, s);
-  if (a.B == 2) return launch_bt<2, HAS_S, XT>(a, s);
-  if (a.B <= 4) return launch_bt<4, HAS_S, XT>(a, s);
-  if (a.B <= 8) return launch_bt<8, HAS_S, XT>(a, s);
+int launch_b(const LinearArgs* l, int n, hipStream_t s) {
+  const int B = l[0].B;
+  if (B == 1) return launch_bt<1, HAS_S, XT>(l, n, s);
+  if (B == 2) return launch_bt<2, HAS_S, XT>(l, n, s);
+  if (B <= 4) return launch_bt<4, HAS_S, XT>(l, n, s);
+  if (B <= 8) return launch_bt<8, HAS_S, XT>(l, n, s);
   return -1;
 }
 
 }  // namespace
 
-// Returns 0 if launched, -1 if this layer/batch is outside the kernel's range.
-int launch_decode_e8d4(const LinearArgs& a, hipStream_t s) {
+// Returns 0 if launched, -1 if the layers/batch are outside the kernel's range.
+int launch_decode_e8d4_multi(const LinearArgs* l, int n, hipStream_t s) {
+  if (n < 1 || n > kMaxLayers) return -1;
+  const LinearArgs& a = l[0];
+  for (int i = 1; i < n; ++i)
+    if (l[i].N != a.N || l[i].B != a.B || l[i].x != a.x || l[i].codes != a.codes ||
+        l[i].codes_f32 != a.codes_f32 || l[i].x_bf16 != a.x_bf16 || (l[i].S != nullptr) != (a.S != nullptr))
+      return -1;
   if (a.B < 1 || a.B > 8) return -1;
   if (a.codes_f32) return -1;  // fp32 tables take the generic kernel
   if (a.x_bf16) {
     if (a.B >= 2) return -1;   // the B >= 2 pairs are formed in fp16 arithmetic
-    return a.S ? launch_bt<1, true, bf16>(a, s) : launch_bt<1, false, bf16>(a, s);
+    return a.S ? launch_bt<1, true, bf16>(l, n, s) : launch_bt<1, false, bf16>(l, n, s);
   }
-  return a.S ? launch_b<true, f16>(a, s) : launch_b<false, f16>(a, s);
+  return a.S ? launch_b<true, f16>(l, n, s) : launch_b<false, f16>(l, n, s);
 }
+
+int launch_decode_e8d4(const LinearArgs& a, hipStream_t s) { return launch_decode_e8d4_multi(&a, 1, s); }
 
 }  // namespace eptq

@@ -322,7 +322,7 @@ __global__ __launch_bounds__(kGT, 2) void k_gemm_e8d4(LinearArgs a, int OB) {
       f16x4 o;
 #pragma unroll
       for (int v = 0; v < 4; ++v) o[v] = (f16)(acc[i][j][v] * gv[v] + bv[v]);
-      *(f16x4*)((f16*)a.y + (size_t)tt * (8 * M) + r0) = o;
+      *(f16x4*)((f16*)a.y + (size_t)tt * a.ldy + r0) = o;
     }
   }
 }
@@ -346,7 +346,7 @@ int launch_gemm_e8d4(const LinearArgs& a, hipStream_t s) {
     LinearArgs t = a;
     t.B = a.B - b0 < kMatvecMaxBatch ? a.B - b0 : kMatvecMaxBatch;
     t.x = a.x + (size_t)b0 * a.N;
-    t.y = a.y + (size_t)b0 * 8 * a.M;
+    t.y = a.y + (size_t)b0 * a.ldy;
     const int rc = launch_matvec<KIND_E8D4>(t, s);
     if (rc) return rc;
   }

@@ -40,6 +40,16 @@ struct LinearArgs {
   int qb;
   int M, N, B;
   uint16_t* y;          // same element type as x
+  int ldy;              // elements between consecutive rows of y (>= 8M)
+};
+
+// Up to kMaxLayers layers that share x (e.g. q, k and v): one decode launch,
+// workgroups [start[l], start[l+1]) serve layer l.
+constexpr int kMaxLayers = 4;
+struct MultiArgs {
+  LinearArgs l[kMaxLayers];
+  int start[kMaxLayers + 1];
+  int n;
 };
 
 template <int KIND> int launch_dequant(const DequantArgs& a, hipStream_t s);
@@ -47,6 +57,9 @@ template <int KIND> int launch_matvec(const LinearArgs& a, hipStream_t s);
 int launch_gemm_e8d4(const LinearArgs& a, hipStream_t s);
 // Persistent E8-D4 decode (B <= 8); -1 when the layer/batch is outside its range.
 int launch_decode_e8d4(const LinearArgs& a, hipStream_t s);
+// Several layers sharing x (same N, B, table, dtypes) in one launch; -1 when
+// any of them is outside the decode kernel's range.
+int launch_decode_e8d4_multi(const LinearArgs* layers, int n, hipStream_t s);
 
 // Largest batch served by the decode matvec; larger batches take the GEMM.
 constexpr int kMatvecMaxBatch = 16;

@@ -228,7 +228,7 @@ __global__ __launch_bounds__(kThreads) void k_matvec(LinearArgs a) {
         const int row = 8 * m + k;
         s = s * (float)a.g[row];
         if (a.bias) s += (float)a.bias[row];
-        a.y[(size_t)b * (8 * a.M) + row] = Act<XT>::from_f32(s);
+        a.y[(size_t)b * a.ldy + row] = Act<XT>::from_f32(s);
       }
     }
   }

@@ -24,7 +24,8 @@ from . import _lib
 from ._lib import EPTQ_BF16, EPTQ_F16, EPTQ_F32, EptqError
 
 __all__ = ["e8_forward", "e8d4_forward", "e8_forward_grouped", "e8d4_forward_grouped",
-           "e8_dequant", "e8d4_dequant", "EptqError", "linear_forward", "dequant"]
+           "e8_dequant", "e8d4_dequant", "EptqError", "linear_forward", "linear_forward_multi",
+           "dequant"]
 
 
 def _ptr(t: Optional[torch.Tensor]):
@@ -92,6 +93,42 @@ def linear_forward(kind: str, Q, codes, g, h, x, O_vals, O_col, O_row_ptr, bias=
                 _ptr(O_vals), _ptr(O_col), _ptr(O_row_ptr), _ptr(bias), _ptr(S_group), n_groups,
                 M, N, B, _ptr(y), stream)
     _lib.check(rc, fn.__name__)
+    return y
+
+
+def linear_forward_multi(layers, codes, x) -> torch.Tensor:
+    """E8-D4 layers sharing ``x`` (B, N) -> (B, Σ out) with the layers' outputs
+    side by side, in one decode launch when the kernel takes them all.
+    ``layers``: dicts with Q, g, h, O_vals, O_col, O_row_ptr and optional
+    bias, S_group (the EPTQLinear buffers)."""
+    _require(len(layers) > 0, "no layers")
+    _require(x.dim() == 2 and x.dtype in (torch.float16, torch.bfloat16) and x.is_contiguous(),
+             "x must be a contiguous 2-D fp16/bf16 tensor")
+    N = int(x.shape[1])
+    arr = (_lib.EptqLayer * len(layers))()
+    off = 0
+    keep = []
+    for i, L in enumerate(layers):
+        M, n2, n_groups = _check_layer("e8_d4", L["Q"], codes, L["g"], L["h"], L["O_vals"], L["O_col"],
+                                       L["O_row_ptr"], L.get("S_group"))
+        _require(n2 == N and L["Q"].device == x.device, "layers must take x's in_features on x's device")
+        b = L.get("bias")
+        arr[i] = _lib.EptqLayer(_ptr(L["Q"]), _ptr(L["g"]), _ptr(L["h"]), _ptr(L["O_vals"]), _ptr(L["O_col"]),
+                                _ptr(L["O_row_ptr"]), _ptr(b), _ptr(L.get("S_group")), n_groups, M, off)
+        off += 8 * M
+        keep.append(L)
+    B = int(x.shape[0])
+    y = torch.empty((B, off), dtype=x.dtype, device=x.device)
+    if B == 0:
+        return y
+    lib = _lib.load()
+    with torch.cuda.device(x.device):
+        stream = torch.cuda.current_stream().cuda_stream
+        rc = lib.eptq_e8d4_forward_multi(len(layers), arr, _ptr(codes),
+                                         EPTQ_F32 if codes.dtype == torch.float32 else EPTQ_F16, _ptr(x),
+                                         EPTQ_BF16 if x.dtype == torch.bfloat16 else EPTQ_F16, N, B,
+                                         _ptr(y), off, stream)
+    _lib.check(rc, "eptq_e8d4_forward_multi")
     return y
 
 

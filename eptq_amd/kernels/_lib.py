@@ -23,8 +23,23 @@ SIGNATURES = {
     "eptq_last_error": ([], ctypes.c_char_p),
     "eptq_e8d4_forward": ([_P, _P, _I, _P, _P, _P, _I, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _P], _I),
     "eptq_e8_forward": ([_P, _P, _I, _P, _P, _P, _I, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _P], _I),
+    "eptq_e8d4_forward_multi": ([_I, _P, _P, _I, _P, _I, _I, _I, _P, _I, _P], _I),
     "eptq_e8d4_dequant": ([_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _P, _P], _I),
     "eptq_e8_dequant": ([_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _P, _P], _I),
+}
+
+class EptqLayer(ctypes.Structure):
+    """``eptq_layer`` of include/eptq_hip.h."""
+    _fields_ = [("Q", _P), ("g", _P), ("h", _P), ("O_vals", _P), ("O_col", _P), ("O_row_ptr", _P),
+                ("bias", _P), ("S_group", _P), ("n_groups", _I), ("M", _I), ("y_offset", ctypes.c_longlong)]
+
+
+# Fused decode-step operators of the Llama harness (include/eptq_llama.h).
+_F = ctypes.c_float
+LLAMA_SIGNATURES = {
+    "eptq_llama_rmsnorm": ([_P, _P, _P, _P, _I, _I, _F, _P], _I),
+    "eptq_llama_rope_attn": ([_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P], _I),
+    "eptq_llama_silu_mul": ([_P, _P, _I, _I, _P], _I),
 }
 
 _lib = None
@@ -45,7 +60,7 @@ def load(path: os.PathLike | None = None) -> ctypes.CDLL:
             f"EPTQ HIP library not built: {p} is missing "
             "(run __graft_entry__.build() or `python -m eptq_amd.build`)")
     lib = ctypes.CDLL(str(p))
-    for name, (args, res) in SIGNATURES.items():
+    for name, (args, res) in {**SIGNATURES, **LLAMA_SIGNATURES}.items():
         fn = getattr(lib, name)
         fn.argtypes = args
         fn.restype = res

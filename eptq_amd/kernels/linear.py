@@ -28,7 +28,7 @@ import torch
 import torch.nn as nn
 
 from . import dequant as _dequant
-from . import linear_forward
+from . import linear_forward, linear_forward_multi
 
 _KINDS = ("e8_lattice", "e8_d4")
 
@@ -155,3 +155,35 @@ class EPTQLinear(nn.Module):
 
 
 QuantizedLinear = EPTQLinear
+
+
+class EPTQMultiLinear(nn.Module):
+    """Several E8-D4 ``EPTQLinear`` layers applied to the same input, outputs
+    side by side (e.g. q|k|v or gate|up): one kernel launch per call where the
+    decode kernel takes them all.  Each layer keeps its own scales and
+    critical blocks; no weights are merged."""
+
+    def __init__(self, linears):
+        super().__init__()
+        ls = list(linears)
+        if not ls or any(l.quantizer_type != "e8_d4" for l in ls):
+            raise ValueError("EPTQMultiLinear takes one or more E8-D4 layers")
+        if len({l.in_features for l in ls}) != 1 or any(not torch.equal(l._table_f32, ls[0]._table_f32)
+                                                        for l in ls[1:]):
+            raise ValueError("layers must share in_features and the codebook table")
+        self.parts = nn.ModuleList(ls)
+        self.in_features = ls[0].in_features
+        self.out_features = sum(l.out_features for l in ls)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        shape, out_dtype = x.shape, x.dtype
+        x2 = x.reshape(-1, self.in_features)
+        if x2.dtype not in (torch.float16, torch.bfloat16):
+            x2 = x2.half()
+        x2 = x2.contiguous()
+        layers = [dict(Q=l.Q, g=l.g, h=l.h, O_vals=l.O_vals, O_col=l.O_col, O_row_ptr=l.O_row_ptr,
+                       bias=l.bias, S_group=l.S_group) for l in self.parts]
+        y = linear_forward_multi(layers, self.parts[0]._codebook, x2)
+        if y.dtype != out_dtype:
+            y = y.to(out_dtype)
+        return y.reshape(*shape[:-1], self.out_features)

@@ -7,9 +7,13 @@ every decoder Linear (q/k/v/o, gate/up/down) a synthetic E8-D4
 ``QuantizedLayerData`` and the embedding, norms and ``lm_head`` random fp16
 (the reference keeps ``lm_head`` unquantized, ``quantize.py:86-90``).
 
-The decode step has static shapes (the KV cache is preallocated and the
-current position lives in a device tensor), so it is captured once in a HIP
-graph and replayed per token.  Greedy decoding.
+Decode step (one token per sequence), 8 launches per layer:
+RMSNorm(+residual) -> q|k|v (one multi-layer decode launch) -> rotary + cache
+write + attention (one kernel) -> o -> RMSNorm(+residual) -> gate|up (one
+launch) -> SiLU·up -> down.  Shapes are static (preallocated cache, position in
+a device tensor), so the step is captured once in a HIP graph and replayed.
+Prefill (many tokens) runs the same Linears (MFMA GEMM) and PyTorch attention.
+Greedy decoding.
 """
 
 from __future__ import annotations
@@ -22,7 +26,8 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from .kernels.linear import EPTQLinear
+from .kernels import _lib
+from .kernels.linear import EPTQLinear, EPTQMultiLinear
 from .quantizers import E8D4Quantizer
 from .synthetic import make_layer
 
@@ -46,6 +51,28 @@ class LlamaConfig:
 LLAMA2_7B = LlamaConfig()
 
 
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def rmsnorm_(x: torch.Tensor, delta: Optional[torch.Tensor], w: torch.Tensor, eps: float) -> torch.Tensor:
+    """x += delta (in place, if given); returns w ⊙ x / rms(x) (HIP kernel)."""
+    B, H = x.shape
+    y = torch.empty_like(x)
+    rc = _lib.load().eptq_llama_rmsnorm(x.data_ptr(), None if delta is None else delta.data_ptr(),
+                                        w.data_ptr(), y.data_ptr(), B, H, eps, _stream(x))
+    _lib.check(rc, "eptq_llama_rmsnorm")
+    return y
+
+
+def silu_mul(gu: torch.Tensor) -> torch.Tensor:
+    B, F2 = gu.shape
+    a = torch.empty((B, F2 // 2), dtype=gu.dtype, device=gu.device)
+    _lib.check(_lib.load().eptq_llama_silu_mul(gu.data_ptr(), a.data_ptr(), B, F2 // 2, _stream(gu)),
+               "eptq_llama_silu_mul")
+    return a
+
+
 class RMSNorm(nn.Module):
     def __init__(self, dim: int, eps: float):
         super().__init__()
@@ -67,43 +94,43 @@ def _rope(x, cos, sin):
 
 
 class DecoderLayer(nn.Module):
-    def __init__(self, cfg: LlamaConfig, linears: dict):
+    def __init__(self, cfg: LlamaConfig, lin: dict):
         super().__init__()
         self.cfg = cfg
         self.input_layernorm = RMSNorm(cfg.hidden, cfg.eps)
         self.post_attention_layernorm = RMSNorm(cfg.hidden, cfg.eps)
-        for name, mod in linears.items():
-            setattr(self, name, mod)
+        self.qkv_proj = EPTQMultiLinear([lin["q_proj"], lin["k_proj"], lin["v_proj"]])
+        self.o_proj = lin["o_proj"]
+        self.gate_up_proj = EPTQMultiLinear([lin["gate_proj"], lin["up_proj"]])
+        self.down_proj = lin["down_proj"]
 
     def forward(self, x, cos, sin, kc, vc, pos, mask):
-        """x: (B, T, hidden); kc: (B, Hkv, D, L) and vc: (B, Hkv, L, D) cache; pos: (T,) positions;
-        mask: (T, L) additive attention mask."""
+        """Prefill (T tokens): x (B, T, hidden); caches (B, Hkv, L, D); pos (T,)
+        positions; mask (T, L) additive.  PyTorch attention."""
         cfg = self.cfg
         B, T, _ = x.shape
         H, Hk, D = cfg.heads, cfg.kv_heads, cfg.head_dim
         h = self.input_layernorm(x)
-        q = self.q_proj(h).view(B, T, H, D).transpose(1, 2)
-        k = self.k_proj(h).view(B, T, Hk, D).transpose(1, 2)
-        v = self.v_proj(h).view(B, T, Hk, D).transpose(1, 2)
-        q = _rope(q, cos, sin).contiguous()
-        k = _rope(k, cos, sin)
-        # K is cached transposed, (B, Hkv, D, L), so both attention products
-        # take contiguous operands.
-        kc.index_copy_(3, pos, k.transpose(2, 3))
+        qkv = self.qkv_proj(h)
+        q, k, v = qkv.split([H * D, Hk * D, Hk * D], dim=-1)
+        q = _rope(q.reshape(B, T, H, D).transpose(1, 2), cos, sin).contiguous()
+        k = _rope(k.reshape(B, T, Hk, D).transpose(1, 2), cos, sin)
+        v = v.reshape(B, T, Hk, D).transpose(1, 2)
+        kc.index_copy_(2, pos, k)
         vc.index_copy_(2, pos, v)
         kk, vv = kc, vc
         if Hk != H:
             kk = kk.repeat_interleave(H // Hk, dim=1)
             vv = vv.repeat_interleave(H // Hk, dim=1)
-        s = torch.matmul(q, kk).float() * (1.0 / math.sqrt(D)) + mask
-        p = torch.softmax(s, dim=-1).to(x.dtype)
-        o = torch.matmul(p, vv)
+        s = torch.matmul(q.float(), kk.float().transpose(-1, -2).contiguous()) * (1.0 / math.sqrt(D)) + mask
+        p = torch.softmax(s, dim=-1)
+        o = torch.matmul(p, vv.float()).to(x.dtype)
         o = o.transpose(1, 2).reshape(B, T, H * D)
         x = x + self.o_proj(o)
         h = self.post_attention_layernorm(x)
-        a = F.silu(self.gate_proj(h).float()) * self.up_proj(h).float()
-        x = x + self.down_proj(a.to(x.dtype))
-        return x
+        gu = self.gate_up_proj(h).float()
+        a = F.silu(gu[..., :cfg.ffn]) * gu[..., cfg.ffn:]
+        return x + self.down_proj(a.to(x.dtype))
 
 
 class QuantLlama(nn.Module):
@@ -120,16 +147,15 @@ class QuantLlama(nn.Module):
 
     def alloc_cache(self, batch: int, max_len: int, device):
         cfg = self.cfg
-        kshape = (batch, cfg.kv_heads, cfg.head_dim, max_len)
-        vshape = (batch, cfg.kv_heads, max_len, cfg.head_dim)
-        self.kc = [torch.zeros(kshape, dtype=torch.float16, device=device) for _ in self.layers]
-        self.vc = [torch.zeros(vshape, dtype=torch.float16, device=device) for _ in self.layers]
+        shape = (batch, cfg.kv_heads, max_len, cfg.head_dim)
+        self.kc = [torch.zeros(shape, dtype=torch.float16, device=device) for _ in self.layers]
+        self.vc = [torch.zeros(shape, dtype=torch.float16, device=device) for _ in self.layers]
         self.max_len = max_len
         inv = 1.0 / (cfg.rope_theta ** (torch.arange(0, cfg.head_dim, 2, device=device).float() / cfg.head_dim))
         t = torch.arange(max_len, device=device).float()
         f = torch.outer(t, inv)
         emb = torch.cat((f, f), dim=-1)
-        self.cos_tab, self.sin_tab = emb.cos(), emb.sin()
+        self.cos_tab, self.sin_tab = emb.cos().contiguous(), emb.sin().contiguous()
 
     def forward_tokens(self, ids, pos):
         """ids: (B, T) int64, pos: (T,) int64 positions -> logits (B, T, vocab)."""
@@ -144,6 +170,30 @@ class QuantLlama(nn.Module):
             x = layer(x, cos, sin, self.kc[i], self.vc[i], pos, mask)
         x = self.norm(x)
         return self.lm_head(x)
+
+    def decode_tokens(self, tok, pos):
+        """One token per sequence: tok (B, 1) int64, pos (1,) int64 on the device
+        -> logits (B, vocab).  Fused HIP kernels for everything but the
+        embedding, lm_head and argmax."""
+        cfg = self.cfg
+        H, Hk, D = cfg.heads, cfg.kv_heads, cfg.head_dim
+        x = self.embed_tokens(tok[:, 0])                    # (B, hidden), the residual stream
+        B = x.shape[0]
+        lib = _lib.load()
+        delta = None
+        for i, layer in enumerate(self.layers):
+            h = rmsnorm_(x, delta, layer.input_layernorm.weight, cfg.eps)
+            qkv = layer.qkv_proj(h)
+            att = torch.empty((B, H * D), dtype=x.dtype, device=x.device)
+            rc = lib.eptq_llama_rope_attn(qkv.data_ptr(), pos.data_ptr(), self.cos_tab.data_ptr(),
+                                          self.sin_tab.data_ptr(), self.kc[i].data_ptr(), self.vc[i].data_ptr(),
+                                          att.data_ptr(), B, H, Hk, D, self.max_len, _stream(x))
+            _lib.check(rc, "eptq_llama_rope_attn")
+            o = layer.o_proj(att)
+            h = rmsnorm_(x, o, layer.post_attention_layernorm.weight, cfg.eps)
+            delta = layer.down_proj(silu_mul(layer.gate_up_proj(h)))
+        h = rmsnorm_(x, delta, self.norm.weight, cfg.eps)
+        return self.lm_head(h)
 
 
 def build_synthetic(cfg: LlamaConfig = LLAMA2_7B, device="cuda", seed: int = 4000,
@@ -181,11 +231,16 @@ def build_synthetic(cfg: LlamaConfig = LLAMA2_7B, device="cuda", seed: int = 400
 
 
 class GraphDecoder:
-    """Greedy decode with the per-token step captured in a HIP graph."""
+    """Greedy decode with the per-token step captured in a HIP graph.
 
-    def __init__(self, model: QuantLlama, batch: int, max_len: int, device="cuda"):
+    ``fused=True`` runs the step on the fused decode kernels
+    (``QuantLlama.decode_tokens``); ``fused=False`` on the PyTorch-attention
+    path used for prefill (``forward_tokens``), kept as a cross-check."""
+
+    def __init__(self, model: QuantLlama, batch: int, max_len: int, device="cuda", fused: bool = True):
         self.model = model
         self.batch = batch
+        self.fused = fused
         self.device = torch.device(device)
         model.alloc_cache(batch, max_len, self.device)
         self.tok = torch.zeros((batch, 1), dtype=torch.long, device=self.device)
@@ -204,8 +259,11 @@ class GraphDecoder:
 
     @torch.no_grad()
     def _step(self):
-        logits = self.model.forward_tokens(self.tok, self.pos)
-        self.tok.copy_(logits[:, -1].argmax(-1, keepdim=True))
+        if self.fused:
+            logits = self.model.decode_tokens(self.tok, self.pos)
+        else:
+            logits = self.model.forward_tokens(self.tok, self.pos)[:, -1]
+        self.tok.copy_(logits.argmax(-1, keepdim=True))
         self.pos.add_(1)
 
     @torch.no_grad()

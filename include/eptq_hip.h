@@ -62,6 +62,37 @@ int eptq_e8d4_forward(const void* Q, const void* codes, int codes_dtype,
                       const void* bias, const void* S_group, int n_groups,
                       int M, int N, int B, void* y, void* stream);
 
+/* Per-layer operands of eptq_e8d4_forward_multi (meaning as in
+ * eptq_e8d4_forward); the layer writes columns [y_offset, y_offset + 8M) of
+ * every row of y. */
+typedef struct {
+  const void* Q;
+  const void* g;
+  const void* h;
+  const void* O_vals;
+  const void* O_col;
+  const void* O_row_ptr;
+  const void* bias;      /* or NULL */
+  const void* S_group;   /* or NULL */
+  int n_groups;
+  int M;
+  long long y_offset;    /* multiple of 4 */
+} eptq_layer;
+
+/*
+ * Several E8-D4 layers that read the same activations x (B, N) — e.g. q, k
+ * and v, or gate and up — into one output y (B, ldy), in one launch of the
+ * decode matvec when it takes them all (up to 4 layers, B <= 8, fp16 table),
+ * otherwise one launch per layer.  Each layer keeps its own h, g, CSR, bias
+ * and S_group, so unlike a concatenated weight it needs no shared column
+ * scales.  No counterpart in the reference, whose decoder calls one
+ * EPTQLinear per projection (kernels/linear.py:154-212); its callers are
+ * decode steps that want fewer launches per token.
+ */
+int eptq_e8d4_forward_multi(int n_layers, const eptq_layer* layers, const void* codes,
+                            int codes_dtype, const void* x, int x_dtype, int N, int B, void* y,
+                            int ldy, void* stream);
+
 /*
  * Fused E8-lattice quantized Linear (same math, 8-vector = codes[u]).
  * Replaces e8_forward (reference csrc/eptq_kernels.h:15-25,

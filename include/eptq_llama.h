@@ -1,0 +1,40 @@
+/*
+ * eptq_llama.h — fused decode-step operators of the synthetic Llama harness
+ * (eptq_amd/llama.py), in the same library as eptq_hip.h.
+ *
+ * No counterpart in the reference's kernel API: the reference runs these
+ * parts of a decoder layer as HuggingFace/PyTorch ops (LlamaRMSNorm, rotary
+ * embedding, attention over a StaticCache, SiLU gating) driven by
+ * bench_decode.py:44-71.  Same conventions as eptq_hip.h: device pointers,
+ * fp16 data, asynchronous on `stream`, no allocation; 0 = ok, 1 = invalid
+ * argument, 3 = HIP launch error.
+ */
+#ifndef EPTQ_LLAMA_H
+#define EPTQ_LLAMA_H
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* x (B, H) += delta (B, H) when delta is not NULL (the residual add), then
+ * y (B, H) = w ⊙ x · rsqrt(mean(x²) + eps).  H % 8 == 0, H <= 16384. */
+int eptq_llama_rmsnorm(void* x, const void* delta, const void* w, void* y, int B, int H, float eps,
+                       void* stream);
+
+/* Decode attention at position *pos (int64 on the device) for every (head,
+ * batch row): rotary on q and k (cos/sin (L, D) fp32 tables), k and v written
+ * to the caches (B, Hk, L, D) at pos, out (B, H·D) = softmax(q·Kᵀ/√D)·V over
+ * positions 0..pos.  qkv is (B, (H + 2 Hk)·D): [q heads | k heads | v heads].
+ * D == 128, H % Hk == 0, L <= 1024. */
+int eptq_llama_rope_attn(const void* qkv, const void* pos, const void* cos_tab, const void* sin_tab,
+                         void* k_cache, void* v_cache, void* out, int B, int H, int Hk, int D, int L,
+                         void* stream);
+
+/* out (B, F) = silu(gate) ⊙ up with gate_up (B, 2F) = [gate | up].  F % 8 == 0. */
+int eptq_llama_silu_mul(const void* gate_up, void* out, int B, int F, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* EPTQ_LLAMA_H */

@@ -16,8 +16,8 @@ from eptq_amd.kernels import _lib
 HEADER = Path(__file__).resolve().parent.parent / "include" / "eptq_hip.h"
 
 
-def header_functions():
-    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+def header_functions(path=HEADER):
+    text = re.sub(r"/\*.*?\*/", "", path.read_text(), flags=re.S)
     return re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(eptq_\w+)\s*\(", text, flags=re.M)
 
 
@@ -32,10 +32,12 @@ def test_header_declares_the_bound_functions():
     names = header_functions()
     assert len(names) == len(set(names))
     assert set(names) == set(_lib.SIGNATURES)
+    llama = header_functions(HEADER.parent / "eptq_llama.h")
+    assert set(llama) == set(_lib.LLAMA_SIGNATURES)
 
 
 def test_every_declared_symbol_is_exported(lib):
-    for name in header_functions():
+    for name in header_functions() + header_functions(HEADER.parent / "eptq_llama.h"):
         assert hasattr(lib, name), name
         assert isinstance(getattr(lib, name), ctypes._CFuncPtr)
 
@@ -101,3 +103,27 @@ def test_python_wrapper_raises_on_error_codes(lib):
 def test_missing_library_fails_loudly(tmp_path):
     with pytest.raises(_lib.EptqError, match="not built"):
         _lib.load(tmp_path / "missing.so")
+
+
+def test_multi_entry_point_validates_every_layer(lib):
+    L = _lib.EptqLayer
+    good = L(16, 16, 16, None, None, 16, None, None, 0, 4, 0)
+    arr = (L * 2)(good, L(16, 16, 16, None, None, 16, None, None, 0, 4, 32))
+    f = lib.eptq_e8d4_forward_multi
+    assert f(0, arr, 16, 0, 16, 0, 64, 1, 16, 64, None) == _lib.EPTQ_EINVAL
+    assert f(2, arr, 16, 0, 16, 0, 64, 1, 16, 48, None) == _lib.EPTQ_EINVAL   # 2nd layer past ldy
+    assert "outside a y row" in lib.eptq_last_error().decode()
+    bad = (L * 2)(good, L(None, 16, 16, None, None, 16, None, None, 0, 4, 32))
+    assert f(2, bad, 16, 0, 16, 0, 64, 1, 16, 64, None) == _lib.EPTQ_EINVAL
+    odd = (L * 2)(good, L(16, 16, 16, None, None, 16, None, None, 0, 4, 34))
+    assert f(2, odd, 16, 0, 16, 0, 64, 1, 16, 72, None) == _lib.EPTQ_EINVAL
+    assert f(2, arr, 16, 0, None, 0, 64, 0, None, 64, None) == _lib.EPTQ_OK   # B = 0
+
+
+def test_llama_ops_reject_invalid_arguments(lib):
+    assert lib.eptq_llama_rmsnorm(None, None, 16, 16, 1, 64, 1e-5, None) == 1
+    assert lib.eptq_llama_rmsnorm(16, None, 16, 16, 1, 60, 1e-5, None) == 1
+    assert lib.eptq_llama_rope_attn(16, 16, 16, 16, 16, 16, 16, 1, 4, 3, 128, 64, None) == 1   # H % Hk
+    assert lib.eptq_llama_rope_attn(16, 16, 16, 16, 16, 16, 16, 1, 4, 4, 64, 64, None) == 1    # D != 128
+    assert lib.eptq_llama_rope_attn(16, 16, 16, 16, 16, 16, 16, 1, 4, 4, 128, 2048, None) == 1  # L
+    assert lib.eptq_llama_silu_mul(16, 16, 1, 12, None) == 1

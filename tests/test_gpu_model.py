@@ -65,7 +65,7 @@ def test_load_quantized_model_logits_match_dense_reconstruction(tiny_dir):
 def test_llama_graph_decode_matches_eager():
     from eptq_amd.llama import GraphDecoder, LlamaConfig, build_synthetic
     print("synthetic llama: graph vs eager decode", flush=True)
-    cfg = LlamaConfig(hidden=256, ffn=512, layers=2, heads=4, kv_heads=4, vocab=512)
+    cfg = LlamaConfig(hidden=512, ffn=1024, layers=2, heads=4, kv_heads=4, vocab=512)
     model = build_synthetic(cfg, device="cuda", seed=9)
     dec = GraphDecoder(model, 2, 48, device="cuda")
     prompt = torch.randint(0, cfg.vocab, (2, 16), device="cuda", generator=torch.Generator("cuda").manual_seed(1))
@@ -80,3 +80,53 @@ def test_llama_graph_decode_matches_eager():
         dec.step()
         torch.cuda.synchronize()
         assert torch.equal(dec.tok, eager[i]), f"token {i}"
+
+
+def test_fused_decode_step_matches_pytorch_path():
+    """The fused decode kernels (RMSNorm, rotary + cache + attention, SiLU,
+    multi-layer q|k|v and gate|up launches) against the PyTorch path on the
+    same caches: logits and the cache entries written at the position."""
+    from eptq_amd.llama import LlamaConfig, build_synthetic
+    print("synthetic llama: fused decode step vs pytorch path", flush=True)
+    for kv in (4, 2):
+        cfg = LlamaConfig(hidden=512, ffn=1024, layers=2, heads=4, kv_heads=kv, vocab=256)
+        model = build_synthetic(cfg, device="cuda", seed=11)
+        for B in (1, 3):
+            model.alloc_cache(B, 64, "cuda")
+            prompt = torch.randint(0, cfg.vocab, (B, 20), device="cuda",
+                                   generator=torch.Generator("cuda").manual_seed(B))
+            with torch.no_grad():
+                model.forward_tokens(prompt, torch.arange(20, device="cuda"))
+                kc0 = [k.clone() for k in model.kc]
+                vc0 = [v.clone() for v in model.vc]
+                tok = torch.randint(0, cfg.vocab, (B, 1), device="cuda")
+                pos = torch.tensor([20], device="cuda")
+                ref = model.forward_tokens(tok, pos)[:, -1].float()
+                kref = [k[:, :, 20].clone() for k in model.kc]
+                for i in range(cfg.layers):
+                    model.kc[i].copy_(kc0[i])
+                    model.vc[i].copy_(vc0[i])
+                got = model.decode_tokens(tok, pos).float()
+            assert rel_l2(got.cpu().numpy(), ref.cpu().numpy()) < 1e-2, (kv, B)
+            for i in range(cfg.layers):
+                assert rel_l2(model.kc[i][:, :, 20].float().cpu().numpy(), kref[i].float().cpu().numpy()) < 1e-2
+
+
+def test_multi_linear_matches_separate_layers():
+    from eptq_amd.kernels.linear import EPTQLinear, EPTQMultiLinear
+    from eptq_amd.quantizers import E8D4Quantizer
+    from eptq_amd.synthetic import make_layer
+    print("multi-layer launch vs separate layers", flush=True)
+    q = E8D4Quantizer(radius=1.75)
+    for shapes, bias, qb in ((((512, 256), (128, 256), (128, 256)), False, None),
+                             (((1024, 512), (1024, 512)), True, None),
+                             (((256, 128), (256, 128), (512, 128), (128, 128)), False, 64)):
+        ls = [EPTQLinear.from_quantized_data(make_layer(o, i, seed=o + 7 * k, percmask=0.01, bias=bias,
+                                                        qb_size=qb), q, "e8_d4").cuda()
+              for k, (o, i) in enumerate(shapes)]
+        multi = EPTQMultiLinear(ls)
+        for B in (1, 2, 5, 8, 12, 40):
+            x = torch.randn(B, shapes[0][1], device="cuda").half()
+            want = torch.cat([l(x) for l in ls], dim=1).float().cpu().numpy()
+            got = multi(x).float().cpu().numpy()
+            assert rel_l2(got, want) < 2e-3, (shapes, B)
