@@ -13,11 +13,11 @@ from pathlib import Path
 
 ROOT = Path(__file__).resolve().parent
 REPO = ROOT.parent
-SOURCES = ["abi.hip", "dequant.hip", "matvec.hip", "decode.hip", "gemm.hip", "llama_ops.hip"]
+SOURCES = ["abi.hip", "dequant.hip", "matvec.hip", "decode.hip", "chain.hip", "gemm.hip", "llama_ops.hip"]
 OUT = ROOT / "_lib" / "libeptq_hip.so"
 
 HIPCC_FLAGS = [
-    "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",
+    "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",
     # IEEE fp32 everywhere: no multiply-add contraction (bit-exact dequant).
     "-ffp-contract=off",
     # Keep the compiler from emitting packed fp32 VALU ops.
@@ -32,18 +32,37 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found")
 
 
-def build(verbose: bool = False) -> Path:
-    OUT.parent.mkdir(parents=True, exist_ok=True)
-    tmp = OUT.with_suffix(".so.tmp")
-    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{REPO / 'include'}", f"-I{ROOT / 'csrc'}",
-           *[str(ROOT / "csrc" / s) for s in SOURCES], "-o", str(tmp)]
+def _run(cmd, verbose):
     if verbose:
         print(" ".join(cmd), flush=True)
-    res = subprocess.run(cmd, capture_output=True, text=True)
-    errs = "\n".join(l for l in res.stderr.splitlines() if "packed-fp32-ops" not in l)
-    if res.returncode != 0:
-        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{errs}")
+    return subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True)
+
+
+def _finish(proc, what):
+    _, err = proc.communicate()
+    errs = "\n".join(l for l in err.splitlines() if "packed-fp32-ops" not in l)
+    if proc.returncode != 0:
+        raise RuntimeError(f"hipcc failed on {what} ({proc.returncode}):\n{errs}")
+
+
+def build(verbose: bool = False) -> Path:
+    """Compile the sources in parallel (one object each), then link."""
+    OUT.parent.mkdir(parents=True, exist_ok=True)
+    objdir = OUT.parent / "obj"
+    objdir.mkdir(exist_ok=True)
+    inc = [f"-I{REPO / 'include'}", f"-I{ROOT / 'csrc'}"]
+    objs, procs = [], []
+    for src in SOURCES:
+        obj = objdir / (Path(src).stem + ".o")
+        objs.append(str(obj))
+        procs.append((_run([hipcc(), *HIPCC_FLAGS, *inc, "-c", str(ROOT / "csrc" / src), "-o", str(obj)],
+                           verbose), src))
+    for proc, src in procs:
+        _finish(proc, src)
+    tmp = OUT.with_suffix(".so.tmp")
+    _finish(_run([hipcc(), *HIPCC_FLAGS, "-shared", *objs, "-o", str(tmp)], verbose), "link")
     os.replace(tmp, OUT)
+    shutil.rmtree(objdir, ignore_errors=True)
     return OUT
 
 

@@ -10,6 +10,7 @@
 #include <string.h>
 
 #include "eptq_hip.h"
+#include "chain.h"
 #include "kernels.h"
 
 namespace {
@@ -239,6 +240,82 @@ int eptq_e8d4_forward_multi(int n_layers, const eptq_layer* layers, const void* 
   }
   return check_launch(fn);
 }
+
+int eptq_e8d4_chain_create(int n_stages, const eptq_stage* stages, const void* codes,
+                           int codes_dtype, eptq_chain** chain) {
+  const char* fn = "eptq_e8d4_chain_create";
+  if (!chain) return fail(EPTQ_EINVAL, "%s: null chain", fn);
+  *chain = nullptr;
+  if (n_stages <= 0 || !stages) return fail(EPTQ_EINVAL, "%s: n_stages=%d", fn, n_stages);
+  if (codes_dtype != EPTQ_F16) return fail(EPTQ_EUNSUPPORTED, "%s: the chain takes the fp16 table", fn);
+  eptq::ChainStage* cs = new eptq::ChainStage[n_stages];
+  bool has_s = false;
+  for (int s = 0; s < n_stages; ++s) {
+    const eptq_stage& S = stages[s];
+    eptq::ChainStage& c = cs[s];
+    c = eptq::ChainStage();
+    if (S.n_layers < 1 || S.n_layers > eptq::kMaxLayers || !S.layers) {
+      delete[] cs;
+      return fail(EPTQ_EINVAL, "%s: stage %d has %d layers (1..%d)", fn, s, S.n_layers, eptq::kMaxLayers);
+    }
+    if (!S.x || !S.y) {
+      delete[] cs;
+      return fail(EPTQ_EINVAL, "%s: stage %d: null x/y", fn, s);
+    }
+    c.n = S.n_layers;
+    c.wait = S.wait != 0;
+    for (int l = 0; l < S.n_layers; ++l) {
+      const eptq_layer& L = S.layers[l];
+      eptq::LinearArgs t;
+      int rc = layer_args(fn, eptq::KIND_E8D4, L.Q, codes, codes_dtype, L.g, L.h, S.x, EPTQ_F16, L.O_vals,
+                          L.O_col, L.O_row_ptr, L.bias, L.S_group, L.n_groups, L.M, S.N, 1, &t);
+      if (rc) {
+        delete[] cs;
+        return rc;
+      }
+      if (L.y_offset < 0 || L.y_offset + 8LL * L.M > (long long)S.ldy || (L.y_offset & 3)) {
+        delete[] cs;
+        return fail(EPTQ_EINVAL, "%s: stage %d layer %d columns [%lld, %lld) outside a y row of %d (offset %% 4 == 0)",
+                    fn, s, l, L.y_offset, L.y_offset + 8LL * L.M, S.ldy);
+      }
+      if (s == 0 && l == 0) has_s = L.S_group != nullptr;
+      if ((L.S_group != nullptr) != has_s) {
+        delete[] cs;
+        return fail(EPTQ_EUNSUPPORTED, "%s: all layers of a chain must have S_group or none", fn);
+      }
+      t.y = (uint16_t*)S.y + L.y_offset;
+      t.ldy = S.ldy;
+      c.l[l] = t;
+    }
+  }
+  eptq::ChainPlan* plan = nullptr;
+  const int rc = eptq::chain_create(cs, n_stages, &plan);
+  delete[] cs;
+  if (rc == -1) return fail(EPTQ_EUNSUPPORTED, "%s: a stage is outside the decode kernel's range", fn);
+  if (rc) return fail(EPTQ_EHIP, "%s: %s", fn, hipGetErrorString(hipGetLastError()));
+  *chain = (eptq_chain*)plan;
+  return EPTQ_OK;
+}
+
+int eptq_e8d4_chain_run(const eptq_chain* chain, void* stream) {
+  if (!chain) return fail(EPTQ_EINVAL, "eptq_e8d4_chain_run: null chain");
+  eptq::chain_run((const eptq::ChainPlan*)chain, (hipStream_t)stream);
+  return check_launch("eptq_e8d4_chain_run");
+}
+
+int eptq_e8d4_chain_check(eptq_chain* chain) {
+  if (!chain) return fail(EPTQ_EINVAL, "eptq_e8d4_chain_check: null chain");
+  const int rc = eptq::chain_check((eptq::ChainPlan*)chain);
+  if (rc == 1) return fail(EPTQ_ETIMEOUT, "eptq_e8d4_chain_check: a stage wait timed out; results are invalid");
+  if (rc) return fail(EPTQ_EHIP, "eptq_e8d4_chain_check: %s", hipGetErrorString(hipGetLastError()));
+  return EPTQ_OK;
+}
+
+int eptq_e8d4_chain_grid(const eptq_chain* chain) {
+  return chain ? eptq::chain_grid((const eptq::ChainPlan*)chain) : 0;
+}
+
+void eptq_e8d4_chain_destroy(eptq_chain* chain) { eptq::chain_destroy((eptq::ChainPlan*)chain); }
 
 int eptq_e8d4_dequant(const void* Q, const void* codes_f32, const void* g, const void* h,
                       const void* O_vals, const void* O_col, const void* O_row_ptr,

@@ -1,0 +1,580 @@
+// One layer of the E8-D4 decode matvec (batch 1..8) as seen by one workgroup:
+// shared by the one-launch-per-layer kernel (decode.hip) and the persistent
+// chain kernel (chain.hip).
+//
+// Same result as the reference decode kernels (csrc/eptq_kernels.cu:161-292,
+// kernels/triton_e8d4.py:47-157): y = g ⊙ (decode(Q)·(h ⊙ S ⊙ x)ᵀ + CSR(O)) + bias.
+//
+// Work split.  A workgroup is 4 waves; S waves (1, 2 or 4) share a Q-row, so
+// a workgroup works on R = 4/S adjacent rows at a time and walks row groups
+// wg, wg+G, wg+2G, ...  Lane `lane` of segment wave `seg` owns the 16-byte
+// column chunks c = seg·64 + lane + 64·S·j (j < J) of every row, so the
+// activation side (x·h) is prepared once per workgroup in LDS and the E8-D4
+// table is staged in LDS once.  Whole-row waves (S = 1) need no cross-wave
+// reduction and no barrier; S > 1 combines the S partial sums through LDS
+// with one barrier per row group.  The index chunks of the next P row groups
+// are kept in flight in a register ring of 8 chunks (128 bytes per lane) so
+// HBM latency is covered.
+//
+// Arithmetic:
+//  * B = 1: x·h is formed in fp32 and stored in fp16 scaled per chunk of 8
+//    columns by a power of two 2^-e with max|x·h|·2^-e in [0.5, 1); packed
+//    fp16 FMAs accumulate a chunk (two rows per op), and one mixed-precision
+//    FMA per row moves the chunk sum into fp32 times 2^e.
+//  * B >= 2: the two indices of a 32-bit word (adjacent columns) are paired:
+//    byte permutes turn their two table vectors into (c_k(n), c_k(n+1)) fp16
+//    pairs and one v_dot2_f32_f16 per (k, b) accumulates both columns in
+//    fp32.  The activation pairs x·h are rounded to fp16 after scaling h by a
+//    workgroup-uniform power of two 2^-e with max|h|·2^-e <= 1, so |x·h·2^-e|
+//    <= |x| cannot overflow; 2^e is restored in fp32 at the output.  With
+//    S_group the pairs are multiplied by the row group's scales in fp16.
+//
+// Index decode from the raw int16 bits v, with the LDS table stored at
+// position e ^ 0x100 for table row e (u = v ^ 0x8000 needs no fix-up):
+//   rows 0..3 of the block: byte address (v >> 4) & 0xFF8
+//   rows 4..7:              same bits 10-11, bits 3-9 = (v & 127) << 3.
+// Critical blocks (v = 32767) decode as table row 511 in both halves; the
+// CSR pass adds O·(h x) minus exactly what the main loop accumulated for them.
+//
+// COH (chain kernel): x is read and y written with device-coherent (sc1)
+// accesses, because x may be the output of another workgroup earlier in the
+// same launch, on another XCD, whose L2 is not coherent with this one.
+#pragma once
+
+#include "common.h"
+#include "kernels.h"
+
+namespace eptq {
+namespace dec {
+
+constexpr int kT = 256;                    // threads per workgroup
+constexpr int kW = kT / 64;                // waves per workgroup
+constexpr int kBufferWord3 = 0x00020000;   // buffer resource word 3 (gfx9 family)
+constexpr int kNonTemporal = 2;            // buffer load cache policy: nt
+constexpr int kCoherent = 16;              // buffer load cache policy: sc1 (device scope)
+constexpr int kRing = 8;                   // index chunks in flight per lane
+
+typedef f16 h2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint32_t perm(uint32_t hi_src, uint32_t lo_src, uint32_t sel) {
+  return __builtin_amdgcn_perm(hi_src, lo_src, sel);
+}
+
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, a), __builtin_bit_cast(h2, b), c, false);
+}
+
+// By value: __builtin_bit_cast applied directly to a vector-element lvalue
+// (v[1], v.y) reads element 0 with this compiler.
+__device__ __forceinline__ h2 as_h2(uint32_t v) { return __builtin_bit_cast(h2, v); }
+
+// acc + (float)(lo or hi half of a packed fp16 pair) · s, one mixed-precision FMA.
+__device__ __forceinline__ float fma_lo(uint32_t p, float s, float acc) {
+  float r;
+  asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(p), "v"(s), "v"(acc));
+  return r;
+}
+__device__ __forceinline__ float fma_hi(uint32_t p, float s, float acc) {
+  float r;
+  asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(p), "v"(s), "v"(acc));
+  return r;
+}
+
+__device__ __forceinline__ uint32_t pk_mul(uint32_t a, uint32_t b) {
+  return __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, a) * __builtin_bit_cast(h2, b));
+}
+
+// A layer pointer as a global-memory pointer.  Pointers that reach a kernel
+// through memory other than its argument segment (the chain kernel's stage
+// descriptors) are generic to the compiler, which would access them with
+// flat instructions; those count on both vmcnt and lgkmcnt and make every
+// wait a full one.
+template <typename T>
+__device__ __forceinline__ __attribute__((address_space(1))) T* gp(T* p) {
+  return (__attribute__((address_space(1))) T*)p;
+}
+
+template <bool COH>
+__device__ __forceinline__ void store_y(uint16_t* p, uint16_t v) {
+  if constexpr (COH) __hip_atomic_store(gp(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  else *gp(p) = v;
+}
+
+// Dynamic LDS of the activation side: BT padded fp16 rows, plus the per-chunk
+// scales for B = 1.
+__host__ __device__ inline size_t act_lds_bytes(int N, int BT) {
+  return (size_t)BT * (N + 8) * 2 + (BT == 1 ? (size_t)((N >> 3) + 1) * 4 : 0);
+}
+
+// Host side of the launch shape.
+int cu_count();   // compute units of the current device
+
+// Chunks per lane for a row split S ways (0 if beyond the kernel's range).
+inline int chunks_for(int nch, int S) {
+  const int j = (nch + 64 * S - 1) / (64 * S);
+  if (j <= 2) return 2;
+  if (j <= 4) return 4;
+  if (j <= 8) return 8;
+  return 0;
+}
+
+constexpr size_t kActLdsMax = 64 * 1024;   // activation table limit per workgroup
+constexpr size_t kLdsPerCu = 160 * 1024;
+
+inline bool fits(int J, int N, int BT) { return J > 0 && act_lds_bytes(N, BT) <= kActLdsMax; }
+
+// LDS shared by the layer code of one workgroup.
+template <int BT>
+struct Smem {
+  f16x4* tab;                  // [512], row e at e ^ 0x100
+  float (*red)[kW][BT * 8];    // [2][kW][V] cross-wave partial sums (S > 1)
+  float* wmax;                 // [kW]
+  uint16_t* xs;                // [BT][N + 8] activation table
+  float* csc;                  // [N/8 + 1] chunk scales (B = 1)
+};
+
+// State a workgroup carries from the prefetch of its first row groups into
+// the row loop: the index ring (slot p·K + j = chunk j of the p-th row group
+// ahead), critical-block entry ranges of this and the next row group, this
+// lane's first-pass entry and the epilogue operands of this thread's output.
+struct RowState {
+  u32x4 ring[kRing];
+  int crb, cre, nrb, nre;
+  int ecol;
+  u32x4 eo;
+  f16 og, ob;
+};
+
+// Where one workgroup's work lies in a layer split S ways with J chunks per
+// lane: the row groups wg, wg + G, ...  Runtime form of the layout, so a
+// persistent kernel can prefetch a stage of any split; with compile-time
+// S and J the arithmetic folds away.
+struct Walk {
+  const LinearArgs& a;
+  int wg, G, S, J, K, R, slot, seg, lane, tid, V;
+
+  __device__ __forceinline__ Walk(const LinearArgs& a_, int wg_, int G_, int S_, int J_, int V_)
+      : a(a_), wg(wg_), G(G_), S(S_), J(J_), K(J_ > 4 ? 4 : J_), R(kW / S_),
+        slot(__builtin_amdgcn_readfirstlane(threadIdx.x >> 6) / S_),
+        seg(__builtin_amdgcn_readfirstlane(threadIdx.x >> 6) % S_), lane(threadIdx.x & 63),
+        tid(threadIdx.x), V(V_) {}
+
+  __device__ __forceinline__ int chunk(int j) const { return seg * 64 + lane + 64 * S * j; }
+
+  // Critical-block rows [rb, re) of O_col/O for this wave's row of row group
+  // rg; rows past the end give an empty range.  Vector loads (the values are
+  // wave-uniform): a scalar load would share lgkmcnt with the LDS lookups,
+  // and since scalar loads complete out of order every LDS wait would also
+  // wait for it.
+  __device__ __forceinline__ void row_range(int rg, int& rb, int& re) const {
+    const int M = a.M;
+    const int row = rg * R + slot;             // wave-uniform
+    const int rr = row < M ? row : M;
+    const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)a.O_row_ptr, (short)0, (M + 1) * 4, kBufferWord3);
+    rb = (int)__builtin_amdgcn_raw_buffer_load_b32(rp, rr * 4, 0, 0);
+    re = (int)__builtin_amdgcn_raw_buffer_load_b32(rp, (row < M ? rr + 1 : rr) * 4, 0, 0);
+  }
+
+  // Index chunks are read through a buffer resource spanning one row (an
+  // empty one past the last row): out-of-range chunks read as zero, so the
+  // loads need no branches or clamps, and the compiler can wait for exactly
+  // the load it needs (vmcnt counts loads in issue order).
+  __device__ __forceinline__ void load_chunk(u32x4& dst, int rg, int j) const {
+    const int M = a.M, N = a.N;
+    const int row = rg * R + slot;            // wave-uniform
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(a.Q + (size_t)(row < M ? row : 0) * N), (short)0, row < M ? N * 2 : 0, kBufferWord3);
+    dst = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, chunk(j) * 16, 0, kNonTemporal));
+  }
+
+  // Critical blocks, first 64·S entries of a row: lane `ent` of the row's S
+  // waves holds entry rb + ent (its column and O vector).  Buffer resources
+  // span exactly the row's entries, so lanes past the end read zeros.
+  __device__ __forceinline__ void load_entries(RowState& st, int rb_v, int re_v) const {
+    const int ent = seg * 64 + lane;
+    const int rb = __builtin_amdgcn_readfirstlane(rb_v);
+    const int cnt = __builtin_amdgcn_readfirstlane(re_v) - rb;
+    const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(a.O_col + rb), (short)0, cnt * 4, kBufferWord3);
+    const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(a.O + (size_t)rb * 8), (short)0, cnt * 16, kBufferWord3);
+    st.ecol = (int)__builtin_amdgcn_raw_buffer_load_b32(rc, ent * 4, 0, 0);
+    st.eo = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(ro, ent * 16, 0, 0));
+  }
+
+  // The output row this thread writes for row group rg, and its (batch row,
+  // row-in-block) position.
+  __device__ __forceinline__ int out_row(int rg) const {
+    return S == 1 ? rg * R + slot : rg * R + (tid < R * V ? tid / V : 0);
+  }
+  template <int VV>
+  __device__ __forceinline__ int wbase() const {
+    return S == 1 ? reduce_base<VV>(lane) : (tid < R * VV ? tid % VV : 0);
+  }
+  // g and bias of this thread's output in row group rg (rows past the end
+  // read the last row; bias through a resource that is empty when null).
+  template <int VV>
+  __device__ __forceinline__ void load_epilogue(int rg, f16& og, f16& ob) const {
+    const int M = a.M;
+    const int orow = out_row(rg);
+    const int oidx = 8 * (orow < M ? orow : M - 1) + (wbase<VV>() & 7);
+    const __amdgpu_buffer_rsrc_t rbias = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)a.bias, (short)0, a.bias ? 16 * M : 0, kBufferWord3);
+    og = gp(a.g)[oidx];
+    ob = __builtin_bit_cast(f16, (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(rbias, oidx * 2, 0, 0));
+  }
+
+  // Entry ranges of the first two row groups (issued early: the entry loads
+  // need them).
+  __device__ __forceinline__ void rows_first(RowState& st) const {
+    row_range(wg, st.crb, st.cre);
+    row_range(wg + G, st.nrb, st.nre);
+  }
+
+  // Index chunks in flight: K of each of the kRing/K row groups of the ring,
+  // then the first row group's critical-block entries and epilogue operands.
+  template <int VV>
+  __device__ __forceinline__ void issue_ring(RowState& st) const {
+#pragma unroll
+    for (int k = 0; k < kRing; ++k) {
+      const int p = K == 4 ? k >> 2 : K == 2 ? k >> 1 : k;
+      const int j = k - p * K;
+      load_chunk(st.ring[k], wg + p * G, j);
+    }
+    load_entries(st, st.crb, st.cre);
+    load_epilogue<VV>(wg, st.og, st.ob);
+  }
+};
+
+template <int BT, int J, int P, int S, bool HAS_S, typename XT, bool COH>
+struct Layer {
+  static constexpr int V = BT * 8;
+  static constexpr int R = kW / S;                        // rows per row group
+  static constexpr int K = J > 4 ? 4 : J;                 // chunks of a row in flight
+  static_assert(P * K == kRing, "the ring holds kRing chunks");
+  static_assert(J % K == 0, "chunks per row must be a multiple of the chunks in flight");
+  static_assert(V <= 64 && R * V <= kT, "one output per thread after the reduction");
+  // Activation chunks per thread (>= ceil(nch / kT)), the first CAP loaded together.
+  static constexpr int CA = (J * S) / 4 < 1 ? 1 : (J * S) / 4;
+  static constexpr int CAP = CA < 18 / (BT + 1) ? CA : 18 / (BT + 1);
+
+  using State = RowState;
+
+  const LinearArgs& a;
+  const int wg, G;
+  const int tid, lane, wave, slot, seg;
+  const int N, M, B, nch, NP, RG;
+  const Walk w;
+
+  __device__ __forceinline__ Layer(const LinearArgs& a_, int wg_, int G_)
+      : a(a_), wg(wg_), G(G_), tid(threadIdx.x), lane(threadIdx.x & 63),
+        wave(__builtin_amdgcn_readfirstlane(threadIdx.x >> 6)), slot(wave / S), seg(wave % S),
+        N(a_.N), M(a_.M), B(a_.B), nch(a_.N >> 3), NP(a_.N + 8), RG((a_.M + R - 1) / R),
+        w(a_, wg_, G_, S, J, V) {}
+
+  __device__ __forceinline__ int chunk(int j) const { return w.chunk(j); }
+  __device__ __forceinline__ void rows_first(State& st) const { w.rows_first(st); }
+  __device__ __forceinline__ void issue_ring(State& st) const { w.issue_ring<V>(st); }
+
+  // The activation table x·h (scaled) into LDS; returns the output scale.
+  // The loads are issued first (h and x rows through buffer resources whose
+  // offsets past the end read zero), then the LDS table is written.  Needs a
+  // barrier before the row loop reads it.
+  __device__ __forceinline__ float build_act(const Smem<BT>& sm) const {
+    uint16_t* __restrict__ xs = sm.xs;
+    float* __restrict__ csc = sm.csc;
+    const __amdgpu_buffer_rsrc_t rh = __builtin_amdgcn_make_buffer_rsrc((void*)a.h, (short)0, N * 2, kBufferWord3);
+    const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void*)a.x, (short)0, B * N * 2, kBufferWord3);
+    auto load_hx = [&](int c, u32x4& hw, u32x4 (&xw)[BT]) {
+      const bool cv = c < nch;
+      hw = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rh, cv ? c * 16 : N * 2, 0, 0));
+#pragma unroll
+      for (int b = 0; b < BT; ++b)
+        xw[b] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+            rx, cv && b < B ? b * N * 2 + c * 16 : B * N * 2, 0, COH ? kCoherent : 0));
+    };
+    u32x4 hpre[CAP], xpre[CAP][BT];
+#pragma unroll
+    for (int k = 0; k < CAP; ++k) load_hx(tid + kT * k, hpre[k], xpre[k]);
+
+    float out_scale = 1.0f;
+    if (tid == 0) {   // the zero chunk past the end of every row
+#pragma unroll
+      for (int b = 0; b < BT; ++b) *(u32x4*)(xs + b * NP + nch * 8) = (u32x4){0u, 0u, 0u, 0u};
+      if (BT == 1) csc[nch] = 1.0f;
+    }
+    if constexpr (BT == 1) {
+      // Per chunk of 8 columns: xs = fp16(x·h·2^-e), csc = 2^e with
+      // max|x·h|·2^-e in [0.5, 1), so the fp16 accumulation of a chunk (|c| < 2,
+      // 8 columns) cannot overflow; the main loop applies 2^e in fp32.
+      auto prep = [&](int c, const u32x4 hw, const u32x4 xw) {
+        const f16x8 hv = __builtin_bit_cast(f16x8, hw);
+        const u16x8 xv = __builtin_bit_cast(u16x8, xw);
+        float xf[8], mx = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          xf[e] = Act<XT>::mul_f16(xv[e], hv[e]);
+          mx = fmaxf(mx, fabsf(xf[e]));
+        }
+        const int ex = mx > 0.0f ? (int)((__builtin_bit_cast(uint32_t, mx) >> 23) & 0xff) - 126 : 0;
+        const float down = __builtin_ldexpf(1.0f, -ex);
+        u32x4 w;
+#pragma unroll
+        for (int d = 0; d < 4; ++d)
+          w[d] = __builtin_bit_cast(uint32_t, (h2){(f16)(xf[2 * d] * down), (f16)(xf[2 * d + 1] * down)});
+        if (c < nch) {
+          *(u32x4*)(xs + c * 8) = w;
+          csc[c] = __builtin_ldexpf(1.0f, ex);
+        }
+      };
+#pragma unroll
+      for (int k = 0; k < CAP; ++k) prep(tid + kT * k, hpre[k], xpre[k][0]);
+      for (int c = tid + kT * CAP; c < nch; c += kT) {
+        u32x4 hw, xw[BT];
+        load_hx(c, hw, xw);
+        prep(c, hw, xw[0]);
+      }
+    } else {
+      // Workgroup-uniform power-of-two scale with max|h|·2^-e <= 1, so the fp16
+      // pairs |x·h·2^-e| <= |x| cannot overflow (dot2 accumulates in fp32).
+      float mx = 0.0f;
+      auto hmax = [&](const u32x4 hw) {
+        const f16x8 hv = __builtin_bit_cast(f16x8, hw);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) mx = fmaxf(mx, fabsf((float)hv[e]));
+      };
+#pragma unroll
+      for (int k = 0; k < CAP; ++k) hmax(hpre[k]);
+      for (int c = tid + kT * CAP; c < nch; c += kT)
+        hmax(__builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rh, c * 16, 0, 0)));
+      mx = fmaxf(mx, partner<1>(mx));
+      mx = fmaxf(mx, partner<2>(mx));
+      mx = fmaxf(mx, partner<4>(mx));
+      mx = fmaxf(mx, partner<8>(mx));
+      mx = fmaxf(mx, partner<16>(mx));
+      mx = fmaxf(mx, partner<32>(mx));
+      if (lane == 0) sm.wmax[wave] = mx;
+      __syncthreads();
+      mx = fmaxf(fmaxf(sm.wmax[0], sm.wmax[1]), fmaxf(sm.wmax[2], sm.wmax[3]));
+      int ex = 0;
+      if (mx > 1.0f) ex = (int)((__builtin_bit_cast(uint32_t, mx) >> 23) & 0xff) - 126;  // 2^ex >= mx
+      out_scale = __builtin_ldexpf(1.0f, ex);
+      const f16 down = (f16)__builtin_ldexpf(1.0f, -ex);
+      const uint32_t down2 = __builtin_bit_cast(uint32_t, (h2){down, down});
+      auto prep = [&](int c, const u32x4 hw, const u32x4 (&xw)[BT]) {
+        if (c < nch) {
+#pragma unroll
+          for (int b = 0; b < BT; ++b) {
+            u32x4 w;
+#pragma unroll
+            for (int d = 0; d < 4; ++d) w[d] = pk_mul(xw[b][d], pk_mul(hw[d], down2));
+            *(u32x4*)(xs + b * NP + c * 8) = w;
+          }
+        }
+      };
+#pragma unroll
+      for (int k = 0; k < CAP; ++k) prep(tid + kT * k, hpre[k], xpre[k]);
+      for (int c = tid + kT * CAP; c < nch; c += kT) {
+        u32x4 hw, xw[BT];
+        load_hx(c, hw, xw);
+        prep(c, hw, xw);
+      }
+    }
+    return out_scale;
+  }
+
+  // The row groups of this workgroup, starting from the state the ring and
+  // entry prefetch left.  The LDS table and activation table must be ready.
+  __device__ __forceinline__ void rows(State& st, const Smem<BT>& sm, float out_scale) const {
+    const char* __restrict__ tabB = (const char*)sm.tab;
+    const uint16_t* __restrict__ xs = sm.xs;
+    const float* __restrict__ csc = sm.csc;
+    const int ent = seg * 64 + lane;
+    // Marker vector as the main loop sees it.
+    const f16x4 t5 = sm.tab[511 ^ 0x100];
+    // The output (batch row, block row) this thread writes after the reduction.
+    const int wbase = w.wbase<V>();
+    const int wb = wbase >> 3, wk = wbase & 7;
+
+    int par = 0;
+    for (int rg0 = wg; rg0 < RG; rg0 += P * G) {
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+      const int rg = rg0 + p * G;
+      if (rg >= RG) break;                       // uniform across the workgroup
+      const int m = rg * R + slot;
+      const bool row_ok = m < M;
+      const int grp = HAS_S ? (8 * (row_ok ? m : 0)) / a.qb : 0;
+
+      // Epilogue operands: this row group's (loaded a row group ago), and the
+      // next one's.
+      const int orow = w.out_row(rg);
+      const f16 og = st.og, ob = st.ob;
+      w.load_epilogue<V>(rg + G, st.og, st.ob);
+      // Row pointers two row groups ahead (their entries are loaded next).
+      int frb, fre;
+      w.row_range(rg + 2 * G, frb, fre);
+      // S at the critical blocks' columns (grouped layers), issued part-way
+      // through the chunk loop once the entry columns have arrived.
+      f16 gs = (f16)1.0f;
+      auto load_gather = [&]() {
+        if constexpr (HAS_S) {
+          const int col = (unsigned)st.ecol < (unsigned)N ? st.ecol : 0;
+          gs = gp(a.S)[(size_t)grp * N + col];
+        }
+      };
+
+      float acc[V];
+#pragma unroll
+      for (int i = 0; i < V; ++i) acc[i] = 0.0f;
+
+#pragma unroll
+      for (int j = 0; j < J; ++j) {
+        const bool live = seg * 64 + 64 * S * j < nch;   // uniform: some lane has this chunk
+        if (j == J / 2) load_gather();
+        const int cj = chunk(j) < nch ? chunk(j) : nch;   // past the end: the zero chunk
+        f16x8 sv;
+        u32x4 xw[BT];
+        // All 16 table lookups of the chunk first, then the arithmetic, so the
+        // LDS latency is paid once per chunk rather than once per word.
+        u32x2 t1l[4], t2l[4], t1h[4], t2h[4];
+        if (live) {
+          if (HAS_S) sv = *gp((const f16x8*)(a.S + (size_t)grp * N + ((cj < nch ? cj : 0) << 3)));
+#pragma unroll
+          for (int b = 0; b < BT; ++b) xw[b] = *(const u32x4*)(xs + b * NP + cj * 8);
+#pragma unroll
+          for (int d = 0; d < 4; ++d) {
+            const uint32_t q = st.ring[p * K + j % K][d];
+            const uint32_t a1lo = (q >> 4) & 0xFF8u;
+            const uint32_t a1hi = (q >> 20) & 0xFF8u;
+            const uint32_t a2lo = bfi(0x3F8u, q << 3, a1lo);
+            const uint32_t a2hi = bfi(0x3F8u, q >> 13, a1hi);
+            t1l[d] = *(const u32x2*)(tabB + a1lo);
+            t2l[d] = *(const u32x2*)(tabB + a2lo);
+            t1h[d] = *(const u32x2*)(tabB + a1hi);
+            t2h[d] = *(const u32x2*)(tabB + a2hi);
+          }
+        }
+        // Refill this chunk's ring slot: the chunk K ahead in the same row,
+        // else the matching chunk of the row group P·G ahead.
+        if (j + K < J) w.load_chunk(st.ring[p * K + j % K], rg, j + K);
+        else w.load_chunk(st.ring[p * K + j % K], rg + P * G, j + K - J);
+        if (!live) continue;
+        if constexpr (BT == 1) {
+          const float sc = csc[cj];
+          h2 acc16[4];   // rows (0,1) (2,3) (4,5) (6,7) of this chunk, fp16
+#pragma unroll
+          for (int d = 0; d < 4; ++d) {
+            // Packed fp16 FMAs, two rows per op, both columns of the word.
+            const uint32_t xp = HAS_S ? pk_mul(xw[0][d], __builtin_bit_cast(u32x4, sv)[d]) : xw[0][d];
+            const h2 xx = __builtin_bit_cast(h2, xp);
+            const h2 xl = {xx.x, xx.x}, xh = {xx.y, xx.y};
+            const h2 c[8] = {as_h2(t1l[d][0]), as_h2(t1l[d][1]), as_h2(t2l[d][0]), as_h2(t2l[d][1]),
+                             as_h2(t1h[d][0]), as_h2(t1h[d][1]), as_h2(t2h[d][0]), as_h2(t2h[d][1])};
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              acc16[q] = d == 0 ? c[q] * xl : __builtin_elementwise_fma(c[q], xl, acc16[q]);
+              acc16[q] = __builtin_elementwise_fma(c[q + 4], xh, acc16[q]);
+            }
+          }
+          // Chunk partial sums (8 columns) into the fp32 accumulators, times 2^e.
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const uint32_t pq = __builtin_bit_cast(uint32_t, acc16[q]);
+            acc[2 * q] = fma_lo(pq, sc, acc[2 * q]);
+            acc[2 * q + 1] = fma_hi(pq, sc, acc[2 * q + 1]);
+          }
+        } else {
+#pragma unroll
+          for (int d = 0; d < 4; ++d) {
+            // (c_k(lo), c_k(hi)) fp16 pairs for k = 0..7
+            uint32_t pr[8];
+            pr[0] = perm(t1h[d][0], t1l[d][0], 0x05040100u);
+            pr[1] = perm(t1h[d][0], t1l[d][0], 0x07060302u);
+            pr[2] = perm(t1h[d][1], t1l[d][1], 0x05040100u);
+            pr[3] = perm(t1h[d][1], t1l[d][1], 0x07060302u);
+            pr[4] = perm(t2h[d][0], t2l[d][0], 0x05040100u);
+            pr[5] = perm(t2h[d][0], t2l[d][0], 0x07060302u);
+            pr[6] = perm(t2h[d][1], t2l[d][1], 0x05040100u);
+            pr[7] = perm(t2h[d][1], t2l[d][1], 0x07060302u);
+            uint32_t sp = 0;
+            if (HAS_S) sp = __builtin_bit_cast(u32x4, sv)[d];
+#pragma unroll
+            for (int b = 0; b < BT; ++b) {
+              const uint32_t xp = HAS_S ? pk_mul(xw[b][d], sp) : xw[b][d];
+#pragma unroll
+              for (int k = 0; k < 8; ++k) acc[b * 8 + k] = dot2(pr[k], xp, acc[b * 8 + k]);
+            }
+          }
+        }
+      }
+
+      // Critical blocks: add O·(x h) in the accumulator's units, minus what the
+      // marker index contributed in the main loop (table row 511 against the
+      // same activation operand).  x·h for O is the activation table's value.
+      auto correct = [&](const f16x8 o, int col, float sc) {
+        const float csx = BT == 1 ? csc[col >> 3] : 1.0f;
+#pragma unroll
+        for (int b = 0; b < BT; ++b) {
+          if (b < B) {
+            const f16 x16 = __builtin_bit_cast(f16, xs[b * NP + col]);
+            const float xo = (float)x16 * csx;
+            const float xm = HAS_S ? (float)(f16)((float)x16 * sc) * csx : xo;
+#pragma unroll
+            for (int k = 0; k < 8; ++k)
+              acc[b * 8 + k] += (float)o[k] * xo - (float)t5[k & 3] * xm;
+          }
+        }
+      };
+      if (row_ok && ent < st.cre - st.crb)
+        correct(__builtin_bit_cast(f16x8, st.eo), (unsigned)st.ecol < (unsigned)N ? st.ecol : 0, (float)gs);
+      // Rows with more than 64·S critical blocks: the rest, synchronously.
+      if (row_ok) {
+        for (int i = st.crb + 64 * S + ent; i < st.cre; i += 64 * S) {
+          const int col = gp(a.O_col)[i];
+          const float sc = HAS_S ? (float)gp(a.S)[(size_t)grp * N + col] : 1.0f;
+          correct(*gp((const f16x8*)(a.O + (size_t)i * 8)), col, sc);
+        }
+      }
+
+      // Next row group's entries.
+      w.load_entries(st, st.nrb, st.nre);
+      st.crb = st.nrb; st.cre = st.nre;
+      st.nrb = frb; st.nre = fre;
+
+      const int base = wave_reduce_halving<V>(acc);
+      if constexpr (S == 1) {
+        // The wave owns the row: write straight from the reducing lanes.
+        (void)base;
+        if (row_ok && WaveReduceOut<V>::writer(lane) && wb < B) {
+          const float sum = acc[0] * out_scale * (float)og + (float)ob;
+          store_y<COH>(a.y + (size_t)wb * a.ldy + 8 * m + wk, Act<XT>::from_f32(sum));
+        }
+      } else {
+        if (WaveReduceOut<V>::writer(lane)) {
+#pragma unroll
+          for (int i = 0; i < WaveReduceOut<V>::per_lane; ++i) sm.red[par][wave][base + i] = acc[i];
+        }
+        // One barrier per row group: red[] alternates, and the next barrier
+        // orders these reads of red[par] before its reuse two groups later.
+        __syncthreads();
+        if (tid < R * V) {
+          const int sl = tid / V;
+          if (orow < M && wb < B) {
+            float sum = 0.0f;
+#pragma unroll
+            for (int w = 0; w < S; ++w) sum += sm.red[par][sl * S + w][wbase];
+            sum = sum * out_scale * (float)og + (float)ob;
+            store_y<COH>(a.y + (size_t)wb * a.ldy + 8 * orow + wk, Act<XT>::from_f32(sum));
+          }
+        }
+        par ^= 1;
+      }
+    }
+    }
+  }
+};
+
+}  // namespace dec
+}  // namespace eptq

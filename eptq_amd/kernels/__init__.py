@@ -16,6 +16,8 @@ and ``eptq::e8d4_dequant`` / ``eptq::e8_dequant`` produce the bit-exact fp16 W o
 
 from __future__ import annotations
 
+import ctypes
+
 from typing import Optional
 
 import torch
@@ -130,6 +132,78 @@ def linear_forward_multi(layers, codes, x) -> torch.Tensor:
                                          _ptr(y), off, stream)
     _lib.check(rc, "eptq_e8d4_forward_multi")
     return y
+
+
+class DecodeChain:
+    """A plan for ``eptq_e8d4_chain_*``: batch-1 E8-D4 stages run in order by
+    one persistent launch (a decode step's q|k|v, o, gate|up, down stages).
+
+    ``stages``: list of dicts with ``layers`` (1..4 dicts of EPTQLinear
+    buffers as for ``linear_forward_multi``), ``x`` (1, N) fp16, ``y`` (1, ldy)
+    fp16 with the layers' outputs side by side from column 0, and ``wait``
+    (read x only after every earlier stage has written its y; x may then be a
+    prefix of an earlier stage's y).  The plan keeps references to every
+    tensor; ``run`` launches on the current stream and allocates nothing."""
+
+    def __init__(self, stages, codes):
+        _require(len(stages) > 0, "no stages")
+        _require(codes.dtype == torch.float16, "the chain takes the fp16 table")
+        lib = _lib.load()
+        self._keep = [codes]
+        self._arrs = []
+        st = (_lib.EptqStage * len(stages))()
+        device = codes.device
+        for i, S in enumerate(stages):
+            x, y = S["x"], S["y"]
+            _require(x.dtype == torch.float16 and y.dtype == torch.float16 and x.is_contiguous()
+                     and y.is_contiguous() and x.shape[0] == 1 and y.shape[0] == 1,
+                     "chain x and y must be contiguous (1, n) fp16 tensors")
+            N = int(x.shape[1])
+            arr = (_lib.EptqLayer * len(S["layers"]))()
+            off = 0
+            for k, L in enumerate(S["layers"]):
+                M, n2, n_groups = _check_layer("e8_d4", L["Q"], codes, L["g"], L["h"], L["O_vals"], L["O_col"],
+                                               L["O_row_ptr"], L.get("S_group"))
+                _require(n2 == N and L["Q"].device == device, "layers must take x's in_features on the table's device")
+                arr[k] = _lib.EptqLayer(_ptr(L["Q"]), _ptr(L["g"]), _ptr(L["h"]), _ptr(L["O_vals"]),
+                                        _ptr(L["O_col"]), _ptr(L["O_row_ptr"]), _ptr(L.get("bias")),
+                                        _ptr(L.get("S_group")), n_groups, M, off)
+                off += 8 * M
+                self._keep.append(L)
+            _require(off <= y.shape[1], "stage outputs exceed y's width")
+            self._keep += [x, y]
+            self._arrs.append(arr)
+            st[i] = _lib.EptqStage(len(S["layers"]), ctypes.addressof(arr), _ptr(x), N, _ptr(y),
+                                   int(y.shape[1]), 1 if S.get("wait", True) else 0)
+        self._handle = ctypes.c_void_p()
+        self.device = device
+        with torch.cuda.device(device):
+            rc = lib.eptq_e8d4_chain_create(len(stages), st, _ptr(codes), EPTQ_F16, ctypes.byref(self._handle))
+        _lib.check(rc, "eptq_e8d4_chain_create")
+        self.n_stages = len(stages)
+        self.grid = lib.eptq_e8d4_chain_grid(self._handle)
+
+    def run(self) -> None:
+        with torch.cuda.device(self.device):
+            rc = _lib.load().eptq_e8d4_chain_run(self._handle, torch.cuda.current_stream().cuda_stream)
+        _lib.check(rc, "eptq_e8d4_chain_run")
+
+    def check(self) -> None:
+        """Raise if a stage wait timed out since the last check (synchronizes)."""
+        torch.cuda.synchronize(self.device)
+        _lib.check(_lib.load().eptq_e8d4_chain_check(self._handle), "eptq_e8d4_chain_check")
+
+    def close(self) -> None:
+        if getattr(self, "_handle", None) and self._handle.value:
+            torch.cuda.synchronize(self.device)
+            _lib.load().eptq_e8d4_chain_destroy(self._handle)
+            self._handle = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 def dequant(kind: str, Q, codes, g, h, O_vals, O_col, O_row_ptr, S_group=None) -> torch.Tensor:

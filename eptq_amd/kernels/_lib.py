@@ -13,7 +13,7 @@ from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent.parent / "_lib" / "libeptq_hip.so"
 
-EPTQ_OK, EPTQ_EINVAL, EPTQ_EUNSUPPORTED, EPTQ_EHIP = 0, 1, 2, 3
+EPTQ_OK, EPTQ_EINVAL, EPTQ_EUNSUPPORTED, EPTQ_EHIP, EPTQ_ETIMEOUT = 0, 1, 2, 3, 4
 EPTQ_F16, EPTQ_F32, EPTQ_BF16 = 0, 1, 2
 
 # Every symbol the header declares, with its ctypes signature.
@@ -24,6 +24,11 @@ SIGNATURES = {
     "eptq_e8d4_forward": ([_P, _P, _I, _P, _P, _P, _I, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _P], _I),
     "eptq_e8_forward": ([_P, _P, _I, _P, _P, _P, _I, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _P], _I),
     "eptq_e8d4_forward_multi": ([_I, _P, _P, _I, _P, _I, _I, _I, _P, _I, _P], _I),
+    "eptq_e8d4_chain_create": ([_I, _P, _P, _I, ctypes.POINTER(_P)], _I),
+    "eptq_e8d4_chain_run": ([_P, _P], _I),
+    "eptq_e8d4_chain_check": ([_P], _I),
+    "eptq_e8d4_chain_grid": ([_P], _I),
+    "eptq_e8d4_chain_destroy": ([_P], None),
     "eptq_e8d4_dequant": ([_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _P, _P], _I),
     "eptq_e8_dequant": ([_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _P, _P], _I),
 }
@@ -32,6 +37,12 @@ class EptqLayer(ctypes.Structure):
     """``eptq_layer`` of include/eptq_hip.h."""
     _fields_ = [("Q", _P), ("g", _P), ("h", _P), ("O_vals", _P), ("O_col", _P), ("O_row_ptr", _P),
                 ("bias", _P), ("S_group", _P), ("n_groups", _I), ("M", _I), ("y_offset", ctypes.c_longlong)]
+
+
+class EptqStage(ctypes.Structure):
+    """``eptq_stage`` of include/eptq_hip.h."""
+    _fields_ = [("n_layers", _I), ("layers", _P), ("x", _P), ("N", _I), ("y", _P), ("ldy", _I),
+                ("wait", _I)]
 
 
 # Fused decode-step operators of the Llama harness (include/eptq_llama.h).

@@ -36,7 +36,8 @@ enum {
   EPTQ_OK = 0,
   EPTQ_EINVAL = 1,        /* null pointer / negative size / inconsistent args */
   EPTQ_EUNSUPPORTED = 2,  /* shape or alignment outside what the kernels take */
-  EPTQ_EHIP = 3           /* HIP runtime reported an error at launch */
+  EPTQ_EHIP = 3,          /* HIP runtime reported an error at launch */
+  EPTQ_ETIMEOUT = 4       /* a decode chain's stage wait gave up (results invalid) */
 };
 
 enum { EPTQ_F16 = 0, EPTQ_F32 = 1, EPTQ_BF16 = 2 };
@@ -92,6 +93,48 @@ typedef struct {
 int eptq_e8d4_forward_multi(int n_layers, const eptq_layer* layers, const void* codes,
                             int codes_dtype, const void* x, int x_dtype, int N, int B, void* y,
                             int ldy, void* stream);
+
+/*
+ * Decode chain: a sequence of batch-1 E8-D4 stages run by one persistent
+ * launch.  A stage is up to 4 layers that read the same x (1, N) fp16 and
+ * write columns [y_offset, y_offset + 8M) of y (1, ldy) fp16, as in
+ * eptq_e8d4_forward_multi.  With `wait` set, the stage reads x only after
+ * every earlier stage of the chain has written its y, so x may be (a prefix
+ * of) an earlier stage's y: the stages of a decode step (q|k|v, o, gate|up,
+ * down per transformer layer) in one launch, with the index stream of a
+ * stage in flight before its input is ready.  No counterpart in the
+ * reference, which launches one kernel per Linear (kernels/linear.py:154-212)
+ * and captures a decode step in a CUDA graph (bench_decode.py:56-69).
+ *
+ * create validates every stage (fp16 table, the same table and S_group
+ * presence for all layers, N within the decode kernel's range), sizes the
+ * persistent grid from this device's occupancy, allocates the plan's device
+ * memory (stage table and synchronization counters) and copies the stages;
+ * it synchronizes the device.  The pointers in `stages` are kept by the plan.
+ * run launches the chain on `stream` and allocates nothing (it can be
+ * captured in a HIP graph); one plan must not run twice concurrently.
+ * check (after the stream is synchronized) returns EPTQ_ETIMEOUT if a stage
+ * wait gave up since the last check (e.g. another kernel held the CUs), else
+ * EPTQ_OK.  grid returns the plan's workgroup count.
+ */
+typedef struct {
+  int n_layers;               /* 1..4 */
+  const eptq_layer* layers;
+  const void* x;              /* (1, N) fp16 device */
+  int N;
+  void* y;                    /* (1, ldy) fp16 device */
+  int ldy;
+  int wait;                   /* nonzero: after every earlier stage */
+} eptq_stage;
+
+typedef struct eptq_chain eptq_chain;
+
+int eptq_e8d4_chain_create(int n_stages, const eptq_stage* stages, const void* codes,
+                           int codes_dtype, eptq_chain** chain);
+int eptq_e8d4_chain_run(const eptq_chain* chain, void* stream);
+int eptq_e8d4_chain_check(eptq_chain* chain);
+int eptq_e8d4_chain_grid(const eptq_chain* chain);
+void eptq_e8d4_chain_destroy(eptq_chain* chain);
 
 /*
  * Fused E8-lattice quantized Linear (same math, 8-vector = codes[u]).
