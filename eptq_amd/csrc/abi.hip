@@ -10,6 +10,7 @@
 #include <string.h>
 
 #include "eptq_hip.h"
+#include "eptq_llama.h"
 #include "chain.h"
 #include "kernels.h"
 
@@ -94,6 +95,12 @@ int layer_args(const char* fn, int kind, const void* Q, const void* codes, int c
   a->B = B;
   a->y = nullptr;
   a->ldy = 8 * M;
+  a->prep = 0;
+  a->ldx = N;
+  a->x2 = nullptr;
+  a->nw = nullptr;
+  a->xsum = nullptr;
+  a->eps = 0.0f;
   return EPTQ_OK;
 }
 
@@ -171,6 +178,50 @@ int dequant_common(int kind, const void* Q, const void* codes_f32, const void* g
   rc = kind == eptq::KIND_E8D4 ? eptq::launch_dequant<eptq::KIND_E8D4>(a, s)
                                : eptq::launch_dequant<eptq::KIND_E8>(a, s);
   if (rc) return fail(EPTQ_EUNSUPPORTED, "%s: layer too large (M=%d N=%d)", fn, M, N);
+  return check_launch(fn);
+}
+
+bool overlaps(const void* a, const void* b, size_t bytes) {
+  if (!a || !b) return false;
+  const uintptr_t x = (uintptr_t)a, y = (uintptr_t)b;
+  return x < y + bytes && y < x + bytes;
+}
+
+// Layers reading an activation that the decode kernel forms itself (prep 1:
+// residual add + RMSNorm); see LinearArgs.
+int fused_linear(const char* fn, int n, const eptq_layer* layers, const void* codes, const void* x,
+                 int ldx, int prep, const void* x2, const void* nw, float eps, void* xsum, int N, int B,
+                 void* y, int ldy, void* stream) {
+  if (n < 1 || n > eptq::kMaxLayers || !layers) return fail(EPTQ_EINVAL, "%s: n_layers=%d (1..%d)", fn, n, eptq::kMaxLayers);
+  if (B < 0 || B > 8) return fail(B < 0 ? EPTQ_EINVAL : EPTQ_EUNSUPPORTED, "%s: B=%d (0..8)", fn, B);
+  if (B > 0 && (!x || !y)) return fail(EPTQ_EINVAL, "%s: null input/y", fn);
+  if (prep == 1 && !nw) return fail(EPTQ_EINVAL, "%s: null norm weight", fn);
+  if ((x && !aligned16(x)) || (x2 && !aligned16(x2)) || (nw && !aligned16(nw)) || (xsum && !aligned16(xsum)))
+    return fail(EPTQ_EUNSUPPORTED, "%s: activation pointers must be 16-byte aligned", fn);
+  const size_t row_bytes = (size_t)B * N * 2;
+  if (overlaps(xsum, x, row_bytes) || overlaps(xsum, x2, row_bytes))
+    return fail(EPTQ_EINVAL, "%s: resid_out overlaps resid or delta", fn);
+  eptq::LinearArgs a[eptq::kMaxLayers];
+  for (int l = 0; l < n; ++l) {
+    const eptq_layer& L = layers[l];
+    int rc = layer_args(fn, eptq::KIND_E8D4, L.Q, codes, EPTQ_F16, L.g, L.h, x, EPTQ_F16, L.O_vals, L.O_col,
+                        L.O_row_ptr, L.bias, L.S_group, L.n_groups, L.M, N, B, &a[l]);
+    if (rc) return rc;
+    if (L.y_offset < 0 || L.y_offset + 8LL * L.M > (long long)ldy || (L.y_offset & 3))
+      return fail(EPTQ_EINVAL, "%s: layer %d columns [%lld, %lld) outside a y row of %d (offset %% 4 == 0)",
+                  fn, l, L.y_offset, L.y_offset + 8LL * L.M, ldy);
+    a[l].y = (uint16_t*)y + L.y_offset;
+    a[l].ldy = ldy;
+    a[l].prep = prep;
+    a[l].ldx = ldx;
+    a[l].x2 = (const uint16_t*)x2;
+    a[l].nw = (const eptq::f16*)nw;
+    a[l].eps = eps;
+    a[l].xsum = (uint16_t*)xsum;
+  }
+  if (B == 0) return EPTQ_OK;
+  if (eptq::launch_decode_e8d4_multi(a, n, (hipStream_t)stream) != 0)
+    return fail(EPTQ_EUNSUPPORTED, "%s: the decode kernel does not take N=%d B=%d here", fn, N, B);
   return check_launch(fn);
 }
 
@@ -316,6 +367,13 @@ int eptq_e8d4_chain_grid(const eptq_chain* chain) {
 }
 
 void eptq_e8d4_chain_destroy(eptq_chain* chain) { eptq::chain_destroy((eptq::ChainPlan*)chain); }
+
+int eptq_llama_norm_linear(int n_layers, const eptq_layer* layers, const void* codes,
+                           const void* resid, const void* delta, const void* w, float eps,
+                           void* resid_out, int N, int B, void* y, int ldy, void* stream) {
+  return fused_linear("eptq_llama_norm_linear", n_layers, layers, codes, resid, N, 1, delta, w, eps, resid_out,
+                      N, B, y, ldy, stream);
+}
 
 int eptq_e8d4_dequant(const void* Q, const void* codes_f32, const void* g, const void* h,
                       const void* O_vals, const void* O_col, const void* O_row_ptr,

@@ -90,7 +90,7 @@ __device__ __forceinline__ void wait_stage(int* sync, int s, int NG, int grp, in
 // A stage as one workgroup sees it, read from the stage descriptor that a
 // wave-wide vector load left in `d` (lane i holds bytes 16i..16i+15 of the
 // ChainStage): wave-uniform values via readlane, no scalar loads.
-static_assert(sizeof(LinearArgs) == 128, "layer arguments are 32 dwords");
+constexpr int kArgWords = sizeof(LinearArgs) / 4;   // a multiple of 4
 static_assert(sizeof(ChainStage) <= 64 * 16, "a stage descriptor fits one wave-wide load");
 static_assert(sizeof(ChainStage) % 16 == 0, "stage descriptors are 16-byte aligned");
 
@@ -128,9 +128,9 @@ __device__ __forceinline__ StageView view_stage(const u32x4& d) {
   v.wg = (int)blockIdx.x - s0;
   v.Gl = s1 - s0;
   v.active = v.wg < v.Gl;
-  uint32_t w[32];
+  uint32_t w[kArgWords];
 #pragma unroll
-  for (int k = 0; k < 32; ++k) w[k] = __builtin_amdgcn_readlane(d[k & 3], li * 8 + (k >> 2));
+  for (int k = 0; k < kArgWords; ++k) w[k] = __builtin_amdgcn_readlane(d[k & 3], li * (kArgWords / 4) + (k >> 2));
   __builtin_memcpy(&v.a, w, sizeof(LinearArgs));
   return v;
 }
@@ -172,7 +172,7 @@ __device__ __forceinline__ void run_stage(const LinearArgs& a, int wg, int G, bo
 }
 
 template <bool HAS_S>
-__global__ __launch_bounds__(kT, 3) void k_decode_chain(const ChainStage* __restrict__ prog, int n_stages,
+__global__ __launch_bounds__(kT) void k_decode_chain(const ChainStage* __restrict__ prog, int n_stages,
                                                         int* __restrict__ sync, int NG) {
   __shared__ f16x4 tab[512];
   __shared__ float red[2][kW][8];

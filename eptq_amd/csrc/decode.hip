@@ -68,11 +68,13 @@ int cu_count() {
 namespace {
 
 template <int BT, int J, int S, bool HAS_S, typename XT>
-void launch_k(const LinearArgs* layers, int n, hipStream_t s) {
+int launch_k(const LinearArgs* layers, int n, hipStream_t s) {
   // About 8 index chunks (128 bytes) per lane in flight: P row groups of
   // min(J, 4) chunks.
   constexpr int P = 8 / (J > 4 ? 4 : J);
   constexpr int R = kW / S;
+  // The fused RMSNorm keeps a whole row in the first CAP chunks per thread.
+  if (layers[0].prep == 1 && Layer<BT, J, P, S, HAS_S, XT, false>::CAP * kT * 8 < layers[0].N) return -1;
   auto kern = k_decode_e8d4<BT, J, P, S, HAS_S, XT>;
   // As many workgroups per CU as registers and LDS allow (one wave of each
   // workgroup per SIMD): occupancy hides the LDS lookup latency.
@@ -107,15 +109,16 @@ void launch_k(const LinearArgs* layers, int n, hipStream_t s) {
     }
   }
   kern<<<ma.start[n], kT, dyn, s>>>(ma);
+  return 0;
 }
 
 template <int BT, int S, bool HAS_S, typename XT>
 int launch_s(const LinearArgs* l, int n, hipStream_t s) {
   const int J = chunks_for(l[0].N >> 3, S);
   if (!fits(J, l[0].N, BT)) return -1;
-  if (J == 2) { launch_k<BT, 2, S, HAS_S, XT>(l, n, s); return 0; }
-  if (J == 4) { launch_k<BT, 4, S, HAS_S, XT>(l, n, s); return 0; }
-  if (J == 8) { launch_k<BT, 8, S, HAS_S, XT>(l, n, s); return 0; }
+  if (J == 2) return launch_k<BT, 2, S, HAS_S, XT>(l, n, s);
+  if (J == 4) return launch_k<BT, 4, S, HAS_S, XT>(l, n, s);
+  if (J == 8) return launch_k<BT, 8, S, HAS_S, XT>(l, n, s);
   return -1;
 }
 
@@ -158,8 +161,11 @@ int launch_decode_e8d4_multi(const LinearArgs* l, int n, hipStream_t s) {
   const LinearArgs& a = l[0];
   for (int i = 1; i < n; ++i)
     if (l[i].N != a.N || l[i].B != a.B || l[i].x != a.x || l[i].codes != a.codes ||
-        l[i].codes_f32 != a.codes_f32 || l[i].x_bf16 != a.x_bf16 || (l[i].S != nullptr) != (a.S != nullptr))
+        l[i].codes_f32 != a.codes_f32 || l[i].x_bf16 != a.x_bf16 || (l[i].S != nullptr) != (a.S != nullptr) ||
+        l[i].prep != a.prep || l[i].ldx != a.ldx || l[i].x2 != a.x2 || l[i].nw != a.nw ||
+        l[i].xsum != a.xsum || l[i].eps != a.eps)
       return -1;
+  if (a.prep != 0 && a.x_bf16) return -1;
   if (a.B < 1 || a.B > 8) return -1;
   if (a.codes_f32) return -1;  // fp32 tables take the generic kernel
   if (a.x_bf16) {

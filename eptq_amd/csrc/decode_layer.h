@@ -280,23 +280,106 @@ struct Layer {
   // The activation table x·h (scaled) into LDS; returns the output scale.
   // The loads are issued first (h and x rows through buffer resources whose
   // offsets past the end read zero), then the LDS table is written.  Needs a
-  // barrier before the row loop reads it.
+  // barrier before the row loop reads it.  With a.prep == 1 the Linear's
+  // input is formed here first: the RMSNorm of a residual sum (see
+  // LinearArgs).
   __device__ __forceinline__ float build_act(const Smem<BT>& sm) const {
     uint16_t* __restrict__ xs = sm.xs;
     float* __restrict__ csc = sm.csc;
+    const int prep = a.prep, ldx = a.ldx;
     const __amdgpu_buffer_rsrc_t rh = __builtin_amdgcn_make_buffer_rsrc((void*)a.h, (short)0, N * 2, kBufferWord3);
-    const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void*)a.x, (short)0, B * N * 2, kBufferWord3);
-    auto load_hx = [&](int c, u32x4& hw, u32x4 (&xw)[BT]) {
+    const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void*)a.x, (short)0, B * ldx * 2, kBufferWord3);
+    // The residual delta (prep 1; an empty resource when absent).
+    const __amdgpu_buffer_rsrc_t r2 = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)a.x2, (short)0, prep == 1 && a.x2 ? B * ldx * 2 : 0, kBufferWord3);
+    auto load_hx = [&](int c, u32x4& hw, u32x4 (&xw)[BT], u32x4 (&dw)[BT]) {
       const bool cv = c < nch;
       hw = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rh, cv ? c * 16 : N * 2, 0, 0));
 #pragma unroll
       for (int b = 0; b < BT; ++b)
         xw[b] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-            rx, cv && b < B ? b * N * 2 + c * 16 : B * N * 2, 0, COH ? kCoherent : 0));
-    };
-    u32x4 hpre[CAP], xpre[CAP][BT];
+            rx, cv && b < B ? b * ldx * 2 + c * 16 : B * ldx * 2, 0, COH ? kCoherent : 0));
+      if (prep != 0) {
 #pragma unroll
-    for (int k = 0; k < CAP; ++k) load_hx(tid + kT * k, hpre[k], xpre[k]);
+        for (int b = 0; b < BT; ++b)
+          dw[b] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+              r2, cv && b < B ? b * ldx * 2 + c * 16 : B * ldx * 2, 0, 0));
+      }
+    };
+    u32x4 hpre[CAP], xpre[CAP][BT], dpre[CAP][BT];
+#pragma unroll
+    for (int k = 0; k < CAP; ++k) load_hx(tid + kT * k, hpre[k], xpre[k], dpre[k]);
+    if (prep == 1) {
+      // r = fp16(x + x2) (every chunk is among the first CAP: the launch
+      // checks N <= CAP·kT·8), sum of squares per batch row, then
+      // fp16(r · rsqrt(mean + eps) · w).
+      const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc((void*)a.nw, (short)0, N * 2, kBufferWord3);
+      u32x4 wpre[CAP];
+#pragma unroll
+      for (int k = 0; k < CAP; ++k) {
+        const int c = tid + kT * k;
+        wpre[k] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, c < nch ? c * 16 : N * 2, 0, 0));
+      }
+      float ss[BT];
+#pragma unroll
+      for (int b = 0; b < BT; ++b) ss[b] = 0.0f;
+#pragma unroll
+      for (int k = 0; k < CAP; ++k) {
+        const int c = tid + kT * k;
+#pragma unroll
+        for (int b = 0; b < BT; ++b) {
+          const f16x8 xv = __builtin_bit_cast(f16x8, xpre[k][b]), dv = __builtin_bit_cast(f16x8, dpre[k][b]);
+          f16x8 r;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            r[e] = (f16)((float)xv[e] + (float)dv[e]);
+            ss[b] += (float)r[e] * (float)r[e];
+          }
+          xpre[k][b] = __builtin_bit_cast(u32x4, r);
+          if (blockIdx.x == 0 && a.xsum && c < nch && b < B)
+            *gp((u32x4*)(a.xsum + (size_t)b * N + c * 8)) = xpre[k][b];
+        }
+      }
+      // Workgroup sums of the BT rows (LDS partials of the 4 waves).
+#pragma unroll
+      for (int b = 0; b < BT; ++b) {
+        float v = ss[b];
+        v += partner<1>(v);
+        v += partner<2>(v);
+        v += partner<4>(v);
+        v += partner<8>(v);
+        v += partner<16>(v);
+        v += partner<32>(v);
+        if (lane == 0) sm.red[0][wave][b] = v;
+      }
+      __syncthreads();
+      float inv[BT];
+#pragma unroll
+      for (int b = 0; b < BT; ++b) {
+        float t = 0.0f;
+#pragma unroll
+        for (int w2 = 0; w2 < kW; ++w2) t += sm.red[0][w2][b];
+        inv[b] = rsqrtf(t / (float)N + a.eps);
+      }
+      __syncthreads();   // red[] is reused by the row loop
+#pragma unroll
+      for (int k = 0; k < CAP; ++k) {
+        const f16x8 wv = __builtin_bit_cast(f16x8, wpre[k]);
+#pragma unroll
+        for (int b = 0; b < BT; ++b) {
+          const f16x8 r = __builtin_bit_cast(f16x8, xpre[k][b]);
+          f16x8 o;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) o[e] = (f16)((float)r[e] * inv[b] * (float)wv[e]);
+          xpre[k][b] = __builtin_bit_cast(u32x4, o);
+        }
+      }
+    }
+    // Chunks past the first CAP (wide layers, prep 0), one at a time.
+    auto load_more = [&](int c, u32x4& hw, u32x4 (&xw)[BT]) {
+      u32x4 dw[BT];
+      load_hx(c, hw, xw, dw);
+    };
 
     float out_scale = 1.0f;
     if (tid == 0) {   // the zero chunk past the end of every row
@@ -332,7 +415,7 @@ struct Layer {
       for (int k = 0; k < CAP; ++k) prep(tid + kT * k, hpre[k], xpre[k][0]);
       for (int c = tid + kT * CAP; c < nch; c += kT) {
         u32x4 hw, xw[BT];
-        load_hx(c, hw, xw);
+        load_more(c, hw, xw);
         prep(c, hw, xw[0]);
       }
     } else {
@@ -377,7 +460,7 @@ struct Layer {
       for (int k = 0; k < CAP; ++k) prep(tid + kT * k, hpre[k], xpre[k]);
       for (int c = tid + kT * CAP; c < nch; c += kT) {
         u32x4 hw, xw[BT];
-        load_hx(c, hw, xw);
+        load_more(c, hw, xw);
         prep(c, hw, xw);
       }
     }

@@ -41,7 +41,20 @@ struct LinearArgs {
   int M, N, B;
   uint16_t* y;          // same element type as x
   int ldy;              // elements between consecutive rows of y (>= 8M)
+  // Activation preparation fused into the decode launch (fp16 x; decode
+  // kernel only): the Linear's input is
+  //   prep 0: x
+  //   prep 1: RMSNorm(x + x2) = nw ⊙ r / rms(r), r = fp16(x + x2) (x2 may be
+  //           null); the first workgroup writes r to xsum (if non-null)
+  int prep;
+  int ldx;              // elements between consecutive rows of x
+  const uint16_t* x2;
+  const f16* nw;
+  uint16_t* xsum;
+  float eps;
+  int pad_[3];
 };
+static_assert(sizeof(LinearArgs) % 16 == 0, "LinearArgs is a whole number of 16-byte words");
 
 // Up to kMaxLayers layers that share x (e.g. q, k and v): one decode launch,
 // workgroups [start[l], start[l+1]) serve layer l.

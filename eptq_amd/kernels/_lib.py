@@ -49,15 +49,21 @@ class EptqStage(ctypes.Structure):
 _F = ctypes.c_float
 LLAMA_SIGNATURES = {
     "eptq_llama_rmsnorm": ([_P, _P, _P, _P, _I, _I, _F, _P], _I),
-    "eptq_llama_rope_attn": ([_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P], _I),
+    "eptq_llama_rope_attn": ([_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _P], _I),
+    "eptq_llama_attn_work_bytes": ([_I, _I], ctypes.c_longlong),
     "eptq_llama_silu_mul": ([_P, _P, _I, _I, _P], _I),
+    "eptq_llama_norm_linear": ([_I, _P, _P, _P, _P, _P, _F, _P, _I, _I, _P, _I, _P], _I),
 }
 
 _lib = None
 
 
 class EptqError(RuntimeError):
-    """A C-ABI call returned an error code."""
+    """A C-ABI call returned an error code (``code``: EPTQ_*; 0 if none)."""
+
+    def __init__(self, msg: str, code: int = 0):
+        super().__init__(msg)
+        self.code = code
 
 
 def load(path: os.PathLike | None = None) -> ctypes.CDLL:
@@ -83,7 +89,7 @@ def load(path: os.PathLike | None = None) -> ctypes.CDLL:
 def check(rc: int, what: str) -> None:
     if rc != EPTQ_OK:
         msg = load().eptq_last_error().decode(errors="replace")
-        raise EptqError(f"{what} failed (code {rc}): {msg}")
+        raise EptqError(f"{what} failed (code {rc}): {msg}", rc)
 
 
 def forward_into(kind: str, Q, codes, g, h, x, O_vals, O_col, O_row_ptr, bias, S_group,

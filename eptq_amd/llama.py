@@ -7,11 +7,12 @@ every decoder Linear (q/k/v/o, gate/up/down) a synthetic E8-D4
 ``QuantizedLayerData`` and the embedding, norms and ``lm_head`` random fp16
 (the reference keeps ``lm_head`` unquantized, ``quantize.py:86-90``).
 
-Decode step (one token per sequence), 8 launches per layer:
-RMSNorm(+residual) -> q|k|v (one multi-layer decode launch) -> rotary + cache
-write + attention (one kernel) -> o -> RMSNorm(+residual) -> gate|up (one
-launch) -> SiLU·up -> down.  Shapes are static (preallocated cache, position in
-a device tensor), so the step is captured once in a HIP graph and replayed.
+Decode step (one token per sequence), 6 launches per layer: q|k|v with the
+residual add and RMSNorm formed inside the launch (one multi-layer decode
+launch) -> rotary + cache write + attention (one kernel) -> o -> gate|up with
+the residual add and RMSNorm inside -> SiLU·up -> down.  Shapes are
+static (preallocated cache, position in a device tensor), so the step is
+captured once in a HIP graph and replayed.
 Prefill (many tokens) runs the same Linears (MFMA GEMM) and PyTorch attention.
 Greedy decoding.
 """
@@ -71,6 +72,48 @@ def silu_mul(gu: torch.Tensor) -> torch.Tensor:
     _lib.check(_lib.load().eptq_llama_silu_mul(gu.data_ptr(), a.data_ptr(), B, F2 // 2, _stream(gu)),
                "eptq_llama_silu_mul")
     return a
+
+
+def _layer_array(lins):
+    """``eptq_layer`` array for E8-D4 ``EPTQLinear`` parts, outputs side by side."""
+    arr = (_lib.EptqLayer * len(lins))()
+    off = 0
+    for k, l in enumerate(lins):
+        def p(t):
+            return None if t is None or t.numel() == 0 else t.data_ptr()
+        n_groups = 0 if l.S_group is None else int(l.S_group.shape[0])
+        arr[k] = _lib.EptqLayer(p(l.Q), p(l.g), p(l.h), p(l.O_vals), p(l.O_col), p(l.O_row_ptr), p(l.bias),
+                                p(l.S_group), n_groups, int(l.Q.shape[0]), off)
+        off += l.out_features
+    return arr, off
+
+
+def _parts(mod):
+    return list(mod.parts) if isinstance(mod, EPTQMultiLinear) else [mod]
+
+
+def _cached_array(mod):
+    key = tuple(l.Q.data_ptr() for l in _parts(mod))
+    cached = getattr(mod, "_eptq_array", None)
+    if cached is None or cached[0] != key:
+        cached = (key, *_layer_array(_parts(mod)))
+        mod._eptq_array = cached
+    return cached[1], cached[2]
+
+
+def norm_linear(mod, resid, delta, w, eps, resid_out):
+    """mod(RMSNorm(resid + delta)) with the norm fused into the decode launch;
+    resid + delta is written to resid_out (if given).  Raises EptqError
+    (code EPTQ_EUNSUPPORTED) when the kernel cannot take the shape."""
+    arr, width = _cached_array(mod)
+    B, N = resid.shape
+    y = torch.empty((B, width), dtype=resid.dtype, device=resid.device)
+    rc = _lib.load().eptq_llama_norm_linear(
+        len(arr), arr, _parts(mod)[0]._codebook.data_ptr(), resid.data_ptr(),
+        None if delta is None else delta.data_ptr(), w.data_ptr(), eps,
+        None if resid_out is None else resid_out.data_ptr(), N, B, y.data_ptr(), width, _stream(resid))
+    _lib.check(rc, "eptq_llama_norm_linear")
+    return y
 
 
 class RMSNorm(nn.Module):
@@ -144,6 +187,10 @@ class QuantLlama(nn.Module):
         self.norm = norm
         self.lm_head = lm_head
         self.kc: Optional[list] = None
+        self.split_attention = False
+        # Decode step: the residual add + RMSNorm inside the q|k|v and gate|up
+        # launches (6 launches per layer) or as launches of their own (8).
+        self.fused_ops = True
 
     def alloc_cache(self, batch: int, max_len: int, device):
         cfg = self.cfg
@@ -156,6 +203,13 @@ class QuantLlama(nn.Module):
         f = torch.outer(t, inv)
         emb = torch.cat((f, f), dim=-1)
         self.cos_tab, self.sin_tab = emb.cos().contiguous(), emb.sin().contiguous()
+        # Split-position attention (a workspace of partials and zeroed
+        # counters) only on request: at these context lengths one workgroup
+        # per (head, sequence) measured faster than splitting and combining.
+        self.attn_work = None
+        if self.split_attention:
+            nbytes = _lib.load().eptq_llama_attn_work_bytes(batch, cfg.heads)
+            self.attn_work = torch.zeros(nbytes, dtype=torch.uint8, device=device)
 
     def forward_tokens(self, ids, pos):
         """ids: (B, T) int64, pos: (T,) int64 positions -> logits (B, T, vocab)."""
@@ -171,10 +225,26 @@ class QuantLlama(nn.Module):
         x = self.norm(x)
         return self.lm_head(x)
 
+    def _norm_into(self, mod, x, delta, w):
+        """mod(RMSNorm(x + delta)) and the residual x + delta (a new tensor when
+        fused; x itself, updated in place, on the separate-launch path)."""
+        if self.fused_ops:
+            r = torch.empty_like(x) if delta is not None else None
+            try:
+                return norm_linear(mod, x, delta, w, self.cfg.eps, r), (x if r is None else r)
+            except _lib.EptqError as e:
+                if e.code != _lib.EPTQ_EUNSUPPORTED:
+                    raise
+        return mod(rmsnorm_(x, delta, w, self.cfg.eps)), x
+
     def decode_tokens(self, tok, pos):
         """One token per sequence: tok (B, 1) int64, pos (1,) int64 on the device
-        -> logits (B, vocab).  Fused HIP kernels for everything but the
-        embedding, lm_head and argmax."""
+        -> logits (B, vocab).  HIP kernels for everything but the embedding,
+        lm_head and argmax; with ``fused_ops`` the norms run inside the Linear
+        launches (norm(+residual) -> q|k|v, attention, o, norm(+residual) ->
+        gate|up, silu, down).  (The SiLU gating stays a launch of its own:
+        inside the down launch every workgroup would recompute all of it,
+        which measured slower than the launch it saves.)"""
         cfg = self.cfg
         H, Hk, D = cfg.heads, cfg.kv_heads, cfg.head_dim
         x = self.embed_tokens(tok[:, 0])                    # (B, hidden), the residual stream
@@ -182,16 +252,18 @@ class QuantLlama(nn.Module):
         lib = _lib.load()
         delta = None
         for i, layer in enumerate(self.layers):
-            h = rmsnorm_(x, delta, layer.input_layernorm.weight, cfg.eps)
-            qkv = layer.qkv_proj(h)
+            ln1, ln2 = layer.input_layernorm.weight, layer.post_attention_layernorm.weight
+            qkv, x = self._norm_into(layer.qkv_proj, x, delta, ln1)
             att = torch.empty((B, H * D), dtype=x.dtype, device=x.device)
             rc = lib.eptq_llama_rope_attn(qkv.data_ptr(), pos.data_ptr(), self.cos_tab.data_ptr(),
                                           self.sin_tab.data_ptr(), self.kc[i].data_ptr(), self.vc[i].data_ptr(),
-                                          att.data_ptr(), B, H, Hk, D, self.max_len, _stream(x))
+                                          att.data_ptr(), B, H, Hk, D, self.max_len,
+                                          None if self.attn_work is None else self.attn_work.data_ptr(),
+                                          _stream(x))
             _lib.check(rc, "eptq_llama_rope_attn")
             o = layer.o_proj(att)
-            h = rmsnorm_(x, o, layer.post_attention_layernorm.weight, cfg.eps)
-            delta = layer.down_proj(silu_mul(layer.gate_up_proj(h)))
+            gu, x = self._norm_into(layer.gate_up_proj, x, o, ln2)
+            delta = layer.down_proj(silu_mul(gu))
         h = rmsnorm_(x, delta, self.norm.weight, cfg.eps)
         return self.lm_head(h)
 

@@ -7,10 +7,12 @@
  * embedding, attention over a StaticCache, SiLU gating) driven by
  * bench_decode.py:44-71.  Same conventions as eptq_hip.h: device pointers,
  * fp16 data, asynchronous on `stream`, no allocation; 0 = ok, 1 = invalid
- * argument, 3 = HIP launch error.
+ * argument, 2 = unsupported shape (eptq_llama_norm_linear), 3 = HIP launch error.
  */
 #ifndef EPTQ_LLAMA_H
 #define EPTQ_LLAMA_H
+
+#include "eptq_hip.h"
 
 #ifdef __cplusplus
 extern "C" {
@@ -25,13 +27,35 @@ int eptq_llama_rmsnorm(void* x, const void* delta, const void* w, void* y, int B
  * batch row): rotary on q and k (cos/sin (L, D) fp32 tables), k and v written
  * to the caches (B, Hk, L, D) at pos, out (B, H·D) = softmax(q·Kᵀ/√D)·V over
  * positions 0..pos.  qkv is (B, (H + 2 Hk)·D): [q heads | k heads | v heads].
- * D == 128, H % Hk == 0, L <= 1024. */
+ * D == 128, H % Hk == 0, L <= 1024.
+ * work: NULL (one workgroup per (head, batch row)) or a 16-byte aligned
+ * device buffer of eptq_llama_attn_work_bytes(B, H) bytes, zero-filled
+ * before its first use, with which the positions of each (head, batch row)
+ * are split over several workgroups (softmax partials combined by the last
+ * one).  The kernel leaves the buffer's counters at zero; calls that share a
+ * buffer must not run concurrently. */
 int eptq_llama_rope_attn(const void* qkv, const void* pos, const void* cos_tab, const void* sin_tab,
                          void* k_cache, void* v_cache, void* out, int B, int H, int Hk, int D, int L,
-                         void* stream);
+                         void* work, void* stream);
+
+/* Bytes of the eptq_llama_rope_attn workspace for B batch rows and H heads. */
+long long eptq_llama_attn_work_bytes(int B, int H);
 
 /* out (B, F) = silu(gate) ⊙ up with gate_up (B, 2F) = [gate | up].  F % 8 == 0. */
 int eptq_llama_silu_mul(const void* gate_up, void* out, int B, int F, void* stream);
+
+/* The decoder's RMSNorm fused into the E8-D4 layers that read its output
+ * (q|k|v or gate|up): r = resid + delta (delta may be NULL), the layers'
+ * input is w ⊙ r · rsqrt(mean(r²) + eps) (the same roundings as
+ * eptq_llama_rmsnorm), and r is written to resid_out (may be NULL; must not
+ * overlap resid or delta).  layers, codes (fp16 table), y and ldy as in
+ * eptq_e8d4_forward_multi; resid, delta, resid_out (B, N) fp16; B <= 8.
+ * Error codes and eptq_last_error as in eptq_hip.h: EPTQ_EUNSUPPORTED when
+ * the decode kernel cannot take the shape (then run eptq_llama_rmsnorm and
+ * the Linear apart). */
+int eptq_llama_norm_linear(int n_layers, const eptq_layer* layers, const void* codes,
+                           const void* resid, const void* delta, const void* w, float eps,
+                           void* resid_out, int N, int B, void* y, int ldy, void* stream);
 
 #ifdef __cplusplus
 }

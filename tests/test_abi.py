@@ -18,7 +18,7 @@ HEADER = Path(__file__).resolve().parent.parent / "include" / "eptq_hip.h"
 
 def header_functions(path=HEADER):
     text = re.sub(r"/\*.*?\*/", "", path.read_text(), flags=re.S)
-    return re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(eptq_\w+)\s*\(", text, flags=re.M)
+    return re.findall(r"^\s*(?:const\s+)?(?:long\s+)?\w+\s*\*?\s*(eptq_\w+)\s*\(", text, flags=re.M)
 
 
 @pytest.fixture(scope="module")
@@ -123,9 +123,12 @@ def test_multi_entry_point_validates_every_layer(lib):
 def test_llama_ops_reject_invalid_arguments(lib):
     assert lib.eptq_llama_rmsnorm(None, None, 16, 16, 1, 64, 1e-5, None) == 1
     assert lib.eptq_llama_rmsnorm(16, None, 16, 16, 1, 60, 1e-5, None) == 1
-    assert lib.eptq_llama_rope_attn(16, 16, 16, 16, 16, 16, 16, 1, 4, 3, 128, 64, None) == 1   # H % Hk
-    assert lib.eptq_llama_rope_attn(16, 16, 16, 16, 16, 16, 16, 1, 4, 4, 64, 64, None) == 1    # D != 128
-    assert lib.eptq_llama_rope_attn(16, 16, 16, 16, 16, 16, 16, 1, 4, 4, 128, 2048, None) == 1  # L
+    assert lib.eptq_llama_rope_attn(16, 16, 16, 16, 16, 16, 16, 1, 4, 3, 128, 64, None, None) == 1   # H % Hk
+    assert lib.eptq_llama_rope_attn(16, 16, 16, 16, 16, 16, 16, 1, 4, 4, 64, 64, None, None) == 1    # D != 128
+    assert lib.eptq_llama_rope_attn(16, 16, 16, 16, 16, 16, 16, 1, 4, 4, 128, 2048, None, None) == 1  # L
+    assert lib.eptq_llama_rope_attn(16, 16, 16, 16, 16, 16, 16, 1, 4, 4, 128, 64, 24, None) == 1    # work align
+    assert lib.eptq_llama_attn_work_bytes(1, 32) == 32 * (16 * 130 * 4 + 4)
+    assert lib.eptq_llama_attn_work_bytes(0, 32) == 0
     assert lib.eptq_llama_silu_mul(16, 16, 1, 12, None) == 1
 
 
@@ -154,3 +157,18 @@ def test_chain_entry_points_validate_before_any_device_call(lib):
     assert lib.eptq_e8d4_chain_check(None) == _lib.EPTQ_EINVAL
     assert lib.eptq_e8d4_chain_grid(None) == 0
     lib.eptq_e8d4_chain_destroy(None)
+
+
+def test_fused_llama_linears_validate_arguments(lib):
+    L = _lib.EptqLayer
+    arr = (L * 1)(L(16, 16, 16, None, None, 16, None, None, 0, 4, 0))
+    f = lib.eptq_llama_norm_linear
+    assert f(0, arr, 16, 16, None, 16, 1e-5, None, 64, 1, 16, 32, None) == _lib.EPTQ_EINVAL
+    assert f(1, arr, 16, 16, None, None, 1e-5, None, 64, 1, 16, 32, None) == _lib.EPTQ_EINVAL   # no weight
+    assert "norm weight" in lib.eptq_last_error().decode()
+    assert f(1, arr, 16, 16, None, 16, 1e-5, 16, 64, 1, 16, 32, None) == _lib.EPTQ_EINVAL       # out == resid
+    assert "overlaps" in lib.eptq_last_error().decode()
+    assert f(1, arr, 16, 16, None, 16, 1e-5, None, 64, 9, 16, 32, None) == _lib.EPTQ_EUNSUPPORTED  # B > 8
+    assert f(1, arr, 16, 24, None, 16, 1e-5, None, 64, 1, 16, 32, None) == _lib.EPTQ_EUNSUPPORTED  # misaligned
+    assert f(1, arr, 16, 16, None, 16, 1e-5, None, 64, 0, 16, 32, None) == _lib.EPTQ_OK             # B = 0
+    assert f(1, arr, 16, 16, None, 16, 1e-5, None, 64, 1, 16, 24, None) == _lib.EPTQ_EINVAL         # 8M > ldy

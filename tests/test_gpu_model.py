@@ -130,3 +130,76 @@ def test_multi_linear_matches_separate_layers():
             want = torch.cat([l(x) for l in ls], dim=1).float().cpu().numpy()
             got = multi(x).float().cpu().numpy()
             assert rel_l2(got, want) < 2e-3, (shapes, B)
+
+
+def test_fused_norm_matches_separate_launches():
+    """The decode step with the residual add + RMSNorm inside the q|k|v and
+    gate|up launches against the same step with the norms as launches of
+    their own (the fused entry point must really run: no fallback)."""
+    from eptq_amd.llama import LlamaConfig, build_synthetic
+    import eptq_amd.llama as LL
+    print("synthetic llama: fused norm vs separate launches", flush=True)
+    calls = []
+    real = LL.norm_linear
+    LL.norm_linear = lambda *a, **k: (calls.append(1), real(*a, **k))[1]
+    for kv, B in ((4, 1), (2, 3), (4, 8)):
+        cfg = LlamaConfig(hidden=512, ffn=1024, layers=2, heads=4, kv_heads=kv, vocab=256)
+        model = build_synthetic(cfg, device="cuda", seed=13 + B)
+        model.alloc_cache(B, 64, "cuda")
+        prompt = torch.randint(0, cfg.vocab, (B, 12), device="cuda", generator=torch.Generator("cuda").manual_seed(B))
+        with torch.no_grad():
+            model.forward_tokens(prompt, torch.arange(12, device="cuda"))
+            kc0 = [k.clone() for k in model.kc]
+            vc0 = [v.clone() for v in model.vc]
+            tok = torch.randint(0, cfg.vocab, (B, 1), device="cuda")
+            pos = torch.tensor([12], device="cuda")
+            model.fused_ops = False
+            ref = model.decode_tokens(tok, pos).float()
+            kref = [k[:, :, 12].clone() for k in model.kc]
+            for i in range(cfg.layers):
+                model.kc[i].copy_(kc0[i])
+                model.vc[i].copy_(vc0[i])
+            model.fused_ops = True
+            got = model.decode_tokens(tok, pos).float()
+        assert rel_l2(got.cpu().numpy(), ref.cpu().numpy()) < 2e-3, (kv, B)
+        for i in range(cfg.layers):
+            assert rel_l2(model.kc[i][:, :, 12].float().cpu().numpy(), kref[i].float().cpu().numpy()) < 2e-3
+        assert len(calls) == 2 * cfg.layers, "the fused path ran for every norm"
+        calls.clear()
+    LL.norm_linear = real
+
+
+def test_split_attention_matches_single_workgroup():
+    """Decode attention with positions split over workgroups (partials
+    combined by the last one) against one workgroup per head, at several
+    positions including empty splits, for MHA and GQA."""
+    from eptq_amd.kernels import _lib
+    lib = _lib.load()
+    print("decode attention: split vs single workgroup", flush=True)
+    gen = torch.Generator("cuda").manual_seed(5)
+    D, L = 128, 1024
+    for B, H, Hk in ((1, 32, 32), (2, 8, 2), (3, 4, 4)):
+        kc = (torch.randn((B, Hk, L, D), generator=gen, device="cuda") * 0.5).half()
+        vc = torch.randn((B, Hk, L, D), generator=gen, device="cuda").half()
+        inv = 1.0 / (10000.0 ** (torch.arange(0, D, 2, device="cuda").float() / D))
+        f = torch.outer(torch.arange(L, device="cuda").float(), inv)
+        emb = torch.cat((f, f), dim=-1)
+        cos, sin = emb.cos().contiguous(), emb.sin().contiguous()
+        work = torch.zeros(lib.eptq_llama_attn_work_bytes(B, H), dtype=torch.uint8, device="cuda")
+        s = torch.cuda.current_stream().cuda_stream
+        for p in (0, 5, 17, 300, 1023):
+            qkv = torch.randn((B, (H + 2 * Hk) * D), generator=gen, device="cuda").half()
+            pos = torch.tensor([p], device="cuda")
+            outs, caches = [], []
+            for w in (None, work.data_ptr()):
+                k2, v2 = kc.clone(), vc.clone()
+                out = torch.empty((B, H * D), dtype=torch.float16, device="cuda")
+                rc = lib.eptq_llama_rope_attn(qkv.data_ptr(), pos.data_ptr(), cos.data_ptr(), sin.data_ptr(),
+                                              k2.data_ptr(), v2.data_ptr(), out.data_ptr(), B, H, Hk, D, L, w, s)
+                assert rc == 0
+                outs.append(out.float().cpu().numpy())
+                caches.append((k2, v2))
+            assert rel_l2(outs[1], outs[0]) < 2e-3, (B, H, Hk, p)
+            assert torch.equal(caches[0][0], caches[1][0]) and torch.equal(caches[0][1], caches[1][1])
+        cnt = work[lib.eptq_llama_attn_work_bytes(B, H) - 4 * B * H:].view(torch.int32)
+        assert int(cnt.abs().sum()) == 0, "counters are left at zero"
