@@ -18,12 +18,13 @@
 //    before the MFMAs of step s and its W/X tiles written after them, into
 //    the other half of a double-buffered LDS tile (one barrier per step);
 //    the global loads run kPF steps ahead in a register ring.
-// Critical blocks decode as table row 511 in the main loop.  Their exact
-// contribution is restored in the same pass: the workgroup stages its rows'
-// CSR entries in LDS once (Δ = O·h − fp16(row511·h·S) per output row), 16
-// walker threads list the entries whose column falls in each K-step, and the
-// waves holding those rows add Δ·x from the activation tile already in LDS.
-// The output is g ⊙ acc + bias, written as fp16.
+// Critical blocks are written into the W tile itself: the workgroup stages
+// its rows' CSR entries in LDS once (fp16(O·h) per output row), 16 walker
+// threads list the entries whose column falls in each K-step two steps
+// ahead, and the thread that decodes a marker index writes the entry's
+// values in place of the table row, so the MFMA loop needs no correction.
+// (Entries beyond the LDS cap, only in very dense layers, are added after the
+// loop from global memory.)  The output is g ⊙ acc + bias, written as fp16.
 
 #include "common.h"
 #include "kernels.h"
@@ -47,6 +48,9 @@ typedef f16 h8 __attribute__((ext_vector_type(8)));
 __device__ __forceinline__ uint32_t gperm(uint32_t hi_src, uint32_t lo_src, uint32_t sel) {
   return __builtin_amdgcn_perm(hi_src, lo_src, sel);
 }
+// By value: __builtin_bit_cast applied directly to a vector-element lvalue
+// reads element 0 with this compiler.
+__device__ __forceinline__ uint32_t bits16(f16 v) { return (uint32_t)__builtin_bit_cast(uint16_t, v); }
 __device__ __forceinline__ uint32_t gpk_mul(uint32_t a, uint32_t b) {
   return __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, a) * __builtin_bit_cast(h2, b));
 }
@@ -59,10 +63,9 @@ __global__ __launch_bounds__(kGT, 2) void k_gemm_e8d4(LinearArgs a, int OB) {
   __shared__ __attribute__((aligned(16))) f16 Ws[2][kBM][kLd];
   __shared__ __attribute__((aligned(16))) f16 Xs[2][kBN][kLd];
   __shared__ int ent_col[kEntCap];
-  __shared__ __attribute__((aligned(16))) h8 ent_delta[kEntCap];
-  __shared__ uint16_t lst[2][kBQ][kPerStep];
-  __shared__ int lcnt[2][kBQ];
-  __shared__ unsigned lmask[2];
+  __shared__ __attribute__((aligned(16))) h8 ent_val[kEntCap];
+  __shared__ uint16_t lst[3][kBQ][kPerStep];
+  __shared__ int lcnt[3][kBQ];
   __shared__ int rps[kBQ + 1];
 
   const int tid = threadIdx.x;
@@ -102,26 +105,15 @@ __global__ __launch_bounds__(kGT, 2) void k_gemm_e8d4(LinearArgs a, int OB) {
   for (int e = tid; e < ecount && e < kEntCap; e += kGT) {
     const int gi = e0 + e;
     const int col = a.O_col[gi];
-    int q = 0;
-#pragma unroll
-    for (int r = 1; r < kBQ; ++r) q += (gi >= rps[r]) ? 1 : 0;
     const f16x8 o = *(const f16x8*)(a.O + (size_t)gi * 8);
     const f16 hc = a.h[col];
-    f16 hs = hc;
-    if (HAS_S) {
-      const int g2 = (8 * (m0 + q)) / a.qb;
-      hs = (f16)((float)hc * (float)a.S[(size_t)g2 * N + col]);
-    }
-    h8 d;
+    h8 d;   // the tile's value for the block: O·h (the reference applies no S to O)
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const f16 wm_marker = (f16)((float)t5[k & 3] * (float)hs);   // what the tile holds
-      d[k] = (f16)((float)o[k] * (float)hc - (float)wm_marker);
-    }
+    for (int k = 0; k < 8; ++k) d[k] = (f16)((float)o[k] * (float)hc);
     ent_col[e] = col;
-    ent_delta[e] = d;
+    ent_val[e] = d;
   }
-  __syncthreads();   // staged entries are read by the walkers and the waves
+  __syncthreads();   // staged entries are read by the walkers and the decoders
   // Walker thread q (tid < 16) owns Q-row q's entry cursor.
   int wcur = 0, wend = 0;
   if (tid < kBQ) {
@@ -162,6 +154,20 @@ __global__ __launch_bounds__(kGT, 2) void k_gemm_e8d4(LinearArgs a, int OB) {
     lk[2] = *(const u32x2*)(tabB + a1hi);
     lk[3] = *(const u32x2*)(tabB + a2hi);
   };
+  // Walkers: list the critical blocks of K-step s per Q-row (in list
+  // buffer s % 3, two steps before the decoders read it).
+  auto walk = [&](int s) {
+    if (tid < kBQ) {
+      const int b3 = s % 3;
+      const int kend = (s + 1) * kBK;
+      int nw = 0;
+      while (wcur < wend && wcur < kEntCap && ent_col[wcur] < kend) {
+        lst[b3][tid][nw++] = (uint16_t)wcur;
+        ++wcur;
+      }
+      lcnt[b3][tid] = nw;
+    }
+  };
   auto write_tiles = [&](int slot, int buf, int k0) {
     const u32x2 t1l = lk[0], t2l = lk[1], t1h = lk[2], t2h = lk[3];
     uint32_t pr[8];
@@ -174,23 +180,30 @@ __global__ __launch_bounds__(kGT, 2) void k_gemm_e8d4(LinearArgs a, int OB) {
     pr[6] = gperm(t2h[1], t2l[1], 0x05040100u);
     pr[7] = gperm(t2h[1], t2l[1], 0x07060302u);
 #pragma unroll
-    for (int k = 0; k < 8; ++k) *(uint32_t*)&Ws[buf][8 * dq + k][dc] = gpk_mul(pr[k], hsw[slot]);
+    for (int k = 0; k < 8; ++k) pr[k] = gpk_mul(pr[k], hsw[slot]);
+    // Marker indices (raw 0x7FFF) take their entry's values instead.
+    const uint32_t w = qw[slot];
+    const bool mlo = (w & 0xFFFFu) == 0x7FFFu, mhi = (w >> 16) == 0x7FFFu;
+    if (mlo || mhi) {
+      const int b3 = (k0 / kBK) % 3;
+      const int n = lcnt[b3][dq];
+      for (int e = 0; e < n; ++e) {
+        const int idx = lst[b3][dq][e];
+        const int c = ent_col[idx] - k0 - dc;   // 0: low half, 1: high half
+        if ((c == 0 && mlo) || (c == 1 && mhi)) {
+          const h8 v = ent_val[idx];
+#pragma unroll
+          for (int k = 0; k < 8; ++k) {
+            const uint32_t vb = bits16(v[k]);
+            pr[k] = c == 0 ? (pr[k] & 0xFFFF0000u) | vb : (pr[k] & 0x0000FFFFu) | (vb << 16);
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) *(uint32_t*)&Ws[buf][8 * dq + k][dc] = pr[k];
 #pragma unroll
     for (int i = 0; i < 2; ++i) *(u32x4*)&Xs[buf][xt[i]][xc[i]] = xr[slot][i];
-    // Walkers: list this step's critical blocks per Q-row; bit q of the
-    // step mask says Q-row q has some.
-    int nw = 0;
-    if (tid < kBQ) {
-      while (wcur < wend && wcur < kEntCap && ent_col[wcur] < k0 + kBK) {
-        lst[buf][tid][nw++] = (uint16_t)wcur;
-        ++wcur;
-      }
-      lcnt[buf][tid] = nw;
-    }
-    if (tid < 64) {   // the walkers are lanes 0..15 of wave 0
-      const unsigned long long b = __ballot(nw > 0);
-      if (tid == 0) lmask[buf] = (unsigned)b;
-    }
   };
 
 #pragma unroll
@@ -202,7 +215,10 @@ __global__ __launch_bounds__(kGT, 2) void k_gemm_e8d4(LinearArgs a, int OB) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
-  // prologue: step 0's tiles
+  // prologue: the lists of steps 0 and 1, then step 0's tiles
+  walk(0);
+  if (nsteps > 1) walk(1);
+  __syncthreads();
   lookups(0);
   write_tiles(0, 0, 0);
   load_step(0, kPF);
@@ -235,34 +251,8 @@ __global__ __launch_bounds__(kGT, 2) void k_gemm_e8d4(LinearArgs a, int OB) {
       write_tiles(pn, buf ^ 1, k0 + kBK);
       load_step(pn, s + 1 + kPF);
     }
+    if (s + 2 < nsteps) walk(s + 2);
 
-    // -- critical-block corrections of this step for this wave's 8 Q-rows --
-    // D layout: lane holds rows 4·(lane/16)+v of a 16-row tile, token lane%16.
-    const unsigned rows_here = (lmask[buf] >> (8 * wm)) & 0xFFu;
-    if (rows_here) {
-      for (int qq = 0; qq < 8; ++qq) {
-        if (!((rows_here >> qq) & 1u)) continue;   // uniform
-        const int q = 8 * wm + qq;
-        const int n = lcnt[buf][q];
-        const int ti = qq >> 1;                    // 16-row tile holding rows 8q..8q+7
-        const int lg = lane >> 4;
-        const bool mine = (lg >> 1) == (qq & 1);   // lane groups 2(q%2), 2(q%2)+1
-        for (int e = 0; e < n; ++e) {
-          const int idx = lst[buf][q][e];
-          const int c = ent_col[idx] - k0;
-          const h8 d = ent_delta[idx];
-          if (mine) {
-            const int kb = 4 * (lg & 1);           // first of this lane's 4 rows within 8q..
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-              const float xv = (float)Xs[buf][64 * wn + 16 * j + (lane & 15)][c];
-#pragma unroll
-              for (int v = 0; v < 4; ++v) acc[ti][j][v] += (float)d[kb + v] * xv;
-            }
-          }
-        }
-      }
-    }
     __syncthreads();
   }
   }

@@ -72,4 +72,12 @@ def test_gemm_markers_in_every_step_and_column_edges():
     qd.O = torch.randn((int((Q == 32767).sum()), 8)).half()
     x = make_x(130, 1024, seed=5)
     y, ref = _run(qd, x)
-    assert rel_l2(y, ref) <= TOL
+    e = rel_l2(y, ref)
+    assert e <= TOL
+    # The critical blocks really carry O: against the product that decodes
+    # every marker as the table's reserved row instead, the error is far larger.
+    n = layer_np(qd)
+    tab = table("e8_d4", 1.75)
+    wrong_O = np.tile(np.concatenate([tab[511], tab[511]]), (n["O"].shape[0], 1)).astype(np.float16)
+    wrong = linear_ref(x.float().numpy(), n["Q"], n["g"], n["h"], wrong_O, tab, "e8_d4", n["bias"], n["S_group"])
+    assert rel_l2(y, wrong) > 10 * e
