@@ -37,6 +37,8 @@ constexpr int kGT = 256;            // threads
 constexpr int kBM = 128;            // output features per workgroup (16 Q-rows)
 constexpr int kBQ = kBM / 8;        // Q-rows per workgroup
 constexpr int kBN = 128;            // tokens per workgroup
+constexpr int kTJ = kBN / 32;       // 16-token MFMA tiles per wave (waves split the tokens in two)
+constexpr int kXC = kBN / 64;       // 16-byte activation chunks per thread per K-step
 constexpr int kBK = 32;             // input columns per K-step
 constexpr int kLd = kBK + 8;        // LDS row stride in halves (80 bytes)
 constexpr int kEntCap = 512;        // CSR entries staged in LDS per workgroup
@@ -85,10 +87,10 @@ __global__ __launch_bounds__(kGT, 2) void k_gemm_e8d4(LinearArgs a, int OB) {
   const int qrow = m0 + dq;                      // < M: the launcher requires M % 16 == 0
   const uint32_t* __restrict__ qsrc = (const uint32_t*)(a.Q + (size_t)qrow * N);
   const int grp = HAS_S ? (8 * qrow) / a.qb : 0;
-  // x chunks: two 16-byte pieces, token xt[i], column chunk xc[i]
-  int xt[2], xc[2];
+  // x chunks: kXC 16-byte pieces, token xt[i], column chunk xc[i]
+  int xt[kXC], xc[kXC];
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
+  for (int i = 0; i < kXC; ++i) {
     const int idx = tid + kGT * i;
     xt[i] = idx >> 2;
     xc[i] = (idx & 3) * 8;
@@ -124,7 +126,7 @@ __global__ __launch_bounds__(kGT, 2) void k_gemm_e8d4(LinearArgs a, int OB) {
   // ---- register ring: the global loads of the next kPF steps are in flight ----
   constexpr int kPF = 3;
   uint32_t qw[kPF], hsw[kPF];
-  u32x4 xr[kPF][2];
+  u32x4 xr[kPF][kXC];
   auto load_step = [&](int slot, int s) {
     const int k0 = (s < nsteps ? s : nsteps - 1) * kBK;
     qw[slot] = qsrc[(k0 + dc) >> 1];
@@ -132,7 +134,7 @@ __global__ __launch_bounds__(kGT, 2) void k_gemm_e8d4(LinearArgs a, int OB) {
     if (HAS_S) hw = gpk_mul(hw, *(const uint32_t*)(a.S + (size_t)grp * N + k0 + dc));
     hsw[slot] = hw;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < kXC; ++i) {
       // Tokens past T read a valid row; their output columns are never stored.
       const int tt = t0 + xt[i];
       xr[slot][i] = *(const u32x4*)(a.x + (size_t)(tt < T ? tt : T - 1) * N + k0 + xc[i]);
@@ -203,17 +205,17 @@ __global__ __launch_bounds__(kGT, 2) void k_gemm_e8d4(LinearArgs a, int OB) {
 #pragma unroll
     for (int k = 0; k < 8; ++k) *(uint32_t*)&Ws[buf][8 * dq + k][dc] = pr[k];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) *(u32x4*)&Xs[buf][xt[i]][xc[i]] = xr[slot][i];
+    for (int i = 0; i < kXC; ++i) *(u32x4*)&Xs[buf][xt[i]][xc[i]] = xr[slot][i];
   };
 
 #pragma unroll
   for (int p = 0; p < kPF; ++p) load_step(p, p);
 
-  f32x4 acc[4][4];
+  f32x4 acc[4][kTJ];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < kTJ; ++j) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
   // prologue: the lists of steps 0 and 1, then step 0's tiles
   walk(0);
@@ -234,18 +236,18 @@ __global__ __launch_bounds__(kGT, 2) void k_gemm_e8d4(LinearArgs a, int OB) {
     const int pn = (p + 1) % kPF;              // ring slot holding step s + 1
     const bool more = s + 1 < nsteps;
 
-    h8 af[4], bf[4];
+    h8 af[4], bf[kTJ];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
       af[i] = *(const h8*)&Ws[buf][64 * wm + 16 * i + (lane & 15)][8 * (lane >> 4)];
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      bf[j] = *(const h8*)&Xs[buf][64 * wn + 16 * j + (lane & 15)][8 * (lane >> 4)];
+    for (int j = 0; j < kTJ; ++j)
+      bf[j] = *(const h8*)&Xs[buf][(kBN / 2) * wn + 16 * j + (lane & 15)][8 * (lane >> 4)];
     if (more) lookups(pn);
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+      for (int j = 0; j < kTJ; ++j)
         acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
     if (more) {
       write_tiles(pn, buf ^ 1, k0 + kBK);
@@ -277,8 +279,8 @@ __global__ __launch_bounds__(kGT, 2) void k_gemm_e8d4(LinearArgs a, int OB) {
         if (mine) {
           const int kb = 4 * (lg & 1);
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const int tt = t0 + 64 * wn + 16 * j + (lane & 15);
+          for (int j = 0; j < kTJ; ++j) {
+            const int tt = t0 + (kBN / 2) * wn + 16 * j + (lane & 15);
             const float xv = tt < T ? (float)__builtin_bit_cast(f16, a.x[(size_t)tt * N + col]) : 0.f;
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
@@ -306,8 +308,8 @@ __global__ __launch_bounds__(kGT, 2) void k_gemm_e8d4(LinearArgs a, int OB) {
       bv[v] = a.bias ? (float)a.bias[r0 + v] : 0.0f;
     }
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int tt = t0 + 64 * wn + 16 * j + (lane & 15);
+    for (int j = 0; j < kTJ; ++j) {
+      const int tt = t0 + (kBN / 2) * wn + 16 * j + (lane & 15);
       if (tt >= T) continue;
       f16x4 o;
 #pragma unroll
