@@ -115,16 +115,9 @@ int dispatch(const char* fn, int kind, const eptq::LinearArgs& a, hipStream_t s)
       rc = eptq::launch_matvec<eptq::KIND_E8>(a, s);
     }
   } else if (kind == eptq::KIND_E8D4) {
-    rc = eptq::launch_gemm_e8d4(a, s);
+    rc = eptq::launch_gemm<eptq::KIND_E8D4>(a, s);
   } else {
-    // E8 at large batch: batch tiles through the decode matvec.
-    for (int b0 = 0; b0 < a.B && rc == 0; b0 += eptq::kMatvecMaxBatch) {
-      eptq::LinearArgs t = a;
-      t.B = a.B - b0 < eptq::kMatvecMaxBatch ? a.B - b0 : eptq::kMatvecMaxBatch;
-      t.x = a.x + (size_t)b0 * a.N;
-      t.y = a.y + (size_t)b0 * a.ldy;
-      rc = eptq::launch_matvec<eptq::KIND_E8>(t, s);
-    }
+    rc = eptq::launch_gemm<eptq::KIND_E8>(a, s);
   }
   if (rc) return fail(EPTQ_EUNSUPPORTED, "%s: no kernel for M=%d N=%d B=%d", fn, a.M, a.N, a.B);
   return EPTQ_OK;

@@ -1,9 +1,14 @@
-// Prefill GEMM for E8-D4 layers: y = (decode(Q)·diag(h·S)) · xᵀ ⊙ g + CSR + bias.
+// Prefill GEMM for E8-D4 and E8 layers: y = (decode(Q)·diag(h·S)) · xᵀ ⊙ g + CSR + bias.
 //
 // Counterpart of the reference's large-batch path e8d4_wmma_v2_kernel +
 // at::mul(x, h) (csrc/eptq_kernels.cu:309-461, :520-537), rebuilt for gfx950
 // MFMA.  The contraction is a genuine dense GEMM, so the quantized weight is
 // dequantized tile by tile into LDS and fed to v_mfma_f32_16x16x32_f16.
+//
+// E8 layers (1 MB table, larger than LDS) gather each index's 16-byte table
+// row from global memory (L2-resident after first use) one K-step ahead,
+// through a buffer resource bounded at the table's 65535 rows, so the marker
+// index reads zeros; otherwise the pipeline is the same.
 //
 // Tiling: a workgroup (4 waves) computes 128 output features (16 Q-rows) ×
 // 128 tokens; each wave a 64 × 64 sub-tile as 4 × 4 MFMA tiles of 16 × 16,
@@ -59,9 +64,9 @@ __device__ __forceinline__ uint32_t gpk_mul(uint32_t a, uint32_t b) {
 
 }  // namespace
 
-template <bool HAS_S>
-__global__ __launch_bounds__(kGT, 2) void k_gemm_e8d4(LinearArgs a, int OB) {
-  __shared__ f16x4 tab[512];
+template <int KIND, bool HAS_S>
+__device__ __forceinline__ void gemm_tile(const LinearArgs& a, int OB) {
+  __shared__ f16x4 tab[KIND == KIND_E8D4 ? 512 : 1];
   __shared__ __attribute__((aligned(16))) f16 Ws[2][kBM][kLd];
   __shared__ __attribute__((aligned(16))) f16 Xs[2][kBN][kLd];
   __shared__ int ent_col[kEntCap];
@@ -97,13 +102,18 @@ __global__ __launch_bounds__(kGT, 2) void k_gemm_e8d4(LinearArgs a, int OB) {
   }
 
   // ---- table and CSR staging ----
+  if constexpr (KIND == KIND_E8D4) {
 #pragma unroll
-  for (int p = 0; p < 2; ++p) tab[(tid + kGT * p) ^ 0x100] = ((const f16x4*)a.codes)[tid + kGT * p];
+    for (int p = 0; p < 2; ++p) tab[(tid + kGT * p) ^ 0x100] = ((const f16x4*)a.codes)[tid + kGT * p];
+  }
   if (tid <= kBQ) rps[tid] = a.O_row_ptr[m0 + tid < M ? m0 + tid : M];
   __syncthreads();
   const int e0 = rps[0];
   const int ecount = rps[kBQ] - e0;
-  const f16x4 t5 = tab[511 ^ 0x100];
+  // What a marker index leaves in the tile before its entry replaces it:
+  // E8-D4 table row 511 in both halves, E8 zeros (out of the table's range).
+  f16x4 t5 = {(f16)0.0f, (f16)0.0f, (f16)0.0f, (f16)0.0f};
+  if constexpr (KIND == KIND_E8D4) t5 = tab[511 ^ 0x100];
   for (int e = tid; e < ecount && e < kEntCap; e += kGT) {
     const int gi = e0 + e;
     const int col = a.O_col[gi];
@@ -144,17 +154,28 @@ __global__ __launch_bounds__(kGT, 2) void k_gemm_e8d4(LinearArgs a, int OB) {
   // Step pipeline: the 4 table lookups of the next step are issued before
   // this step's MFMAs and the W/X tiles of the next step are written after
   // them, so LDS latency and dequantization overlap the matrix work.
-  u32x2 lk[4];
+  u32x2 lk[4];    // E8-D4: the four LDS table lookups of the word
+  u32x4 lk8[2];   // E8: the two gathered table rows (low and high index)
+  const __amdgpu_buffer_rsrc_t rtab = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)a.codes, (short)0, KIND == KIND_E8 ? 65535 * 16 : 0, 0x00020000);
   auto lookups = [&](int slot) {
     const uint32_t w = qw[slot];
-    const uint32_t a1lo = (w >> 4) & 0xFF8u;
-    const uint32_t a1hi = (w >> 20) & 0xFF8u;
-    const uint32_t a2lo = bfi(0x3F8u, w << 3, a1lo);
-    const uint32_t a2hi = bfi(0x3F8u, w >> 13, a1hi);
-    lk[0] = *(const u32x2*)(tabB + a1lo);
-    lk[1] = *(const u32x2*)(tabB + a2lo);
-    lk[2] = *(const u32x2*)(tabB + a1hi);
-    lk[3] = *(const u32x2*)(tabB + a2hi);
+    if constexpr (KIND == KIND_E8D4) {
+      const uint32_t a1lo = (w >> 4) & 0xFF8u;
+      const uint32_t a1hi = (w >> 20) & 0xFF8u;
+      const uint32_t a2lo = bfi(0x3F8u, w << 3, a1lo);
+      const uint32_t a2hi = bfi(0x3F8u, w >> 13, a1hi);
+      lk[0] = *(const u32x2*)(tabB + a1lo);
+      lk[1] = *(const u32x2*)(tabB + a2lo);
+      lk[2] = *(const u32x2*)(tabB + a1hi);
+      lk[3] = *(const u32x2*)(tabB + a2hi);
+    } else {
+      // u = Q + 32768 = raw bits ^ 0x8000; the marker (u = 65535) is past
+      // the resource and reads zeros.
+      const uint32_t ulo = (w & 0xFFFFu) ^ 0x8000u, uhi = (w >> 16) ^ 0x8000u;
+      lk8[0] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rtab, ulo * 16, 0, 0));
+      lk8[1] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rtab, uhi * 16, 0, 0));
+    }
   };
   // Walkers: list the critical blocks of K-step s per Q-row (in list
   // buffer s % 3, two steps before the decoders read it).
@@ -171,16 +192,26 @@ __global__ __launch_bounds__(kGT, 2) void k_gemm_e8d4(LinearArgs a, int OB) {
     }
   };
   auto write_tiles = [&](int slot, int buf, int k0) {
-    const u32x2 t1l = lk[0], t2l = lk[1], t1h = lk[2], t2h = lk[3];
+    // pr[k] = (row k at column dc, row k at column dc + 1), fp16 pairs.
     uint32_t pr[8];
-    pr[0] = gperm(t1h[0], t1l[0], 0x05040100u);
-    pr[1] = gperm(t1h[0], t1l[0], 0x07060302u);
-    pr[2] = gperm(t1h[1], t1l[1], 0x05040100u);
-    pr[3] = gperm(t1h[1], t1l[1], 0x07060302u);
-    pr[4] = gperm(t2h[0], t2l[0], 0x05040100u);
-    pr[5] = gperm(t2h[0], t2l[0], 0x07060302u);
-    pr[6] = gperm(t2h[1], t2l[1], 0x05040100u);
-    pr[7] = gperm(t2h[1], t2l[1], 0x07060302u);
+    if constexpr (KIND == KIND_E8D4) {
+      const u32x2 t1l = lk[0], t2l = lk[1], t1h = lk[2], t2h = lk[3];
+      pr[0] = gperm(t1h[0], t1l[0], 0x05040100u);
+      pr[1] = gperm(t1h[0], t1l[0], 0x07060302u);
+      pr[2] = gperm(t1h[1], t1l[1], 0x05040100u);
+      pr[3] = gperm(t1h[1], t1l[1], 0x07060302u);
+      pr[4] = gperm(t2h[0], t2l[0], 0x05040100u);
+      pr[5] = gperm(t2h[0], t2l[0], 0x07060302u);
+      pr[6] = gperm(t2h[1], t2l[1], 0x05040100u);
+      pr[7] = gperm(t2h[1], t2l[1], 0x07060302u);
+    } else {
+      const u32x4 lo = lk8[0], hi = lk8[1];
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        pr[2 * d] = gperm(hi[d], lo[d], 0x05040100u);
+        pr[2 * d + 1] = gperm(hi[d], lo[d], 0x07060302u);
+      }
+    }
 #pragma unroll
     for (int k = 0; k < 8; ++k) pr[k] = gpk_mul(pr[k], hsw[slot]);
     // Marker indices (raw 0x7FFF) take their entry's values instead.
@@ -319,7 +350,18 @@ __global__ __launch_bounds__(kGT, 2) void k_gemm_e8d4(LinearArgs a, int OB) {
   }
 }
 
-int launch_gemm_e8d4(const LinearArgs& a, hipStream_t s) {
+template <bool HAS_S>
+__global__ __launch_bounds__(kGT, 2) void k_gemm_e8d4(LinearArgs a, int OB) {
+  gemm_tile<KIND_E8D4, HAS_S>(a, OB);
+}
+
+template <bool HAS_S>
+__global__ __launch_bounds__(kGT, 2) void k_gemm_e8(LinearArgs a, int OB) {
+  gemm_tile<KIND_E8, HAS_S>(a, OB);
+}
+
+template <int KIND>
+int launch_gemm(const LinearArgs& a, hipStream_t s) {
   // MFMA path: fp16 activations, fp16 table, whole 16-Q-row tiles, K-steps
   // of 32.  Anything else takes batch tiles of the decode matvec.
   const bool mfma_ok = !a.x_bf16 && !a.codes_f32 && (a.N % kBK) == 0 && (a.M % kBQ) == 0 &&
@@ -329,8 +371,13 @@ int launch_gemm_e8d4(const LinearArgs& a, hipStream_t s) {
     const int TB = (a.B + kBN - 1) / kBN;
     const long grid = (long)OB * TB;
     if (grid <= 0x7fffffff) {
-      if (a.S) k_gemm_e8d4<true><<<(unsigned)grid, kGT, 0, s>>>(a, OB);
-      else k_gemm_e8d4<false><<<(unsigned)grid, kGT, 0, s>>>(a, OB);
+      if (KIND == KIND_E8D4) {
+        if (a.S) k_gemm_e8d4<true><<<(unsigned)grid, kGT, 0, s>>>(a, OB);
+        else k_gemm_e8d4<false><<<(unsigned)grid, kGT, 0, s>>>(a, OB);
+      } else {
+        if (a.S) k_gemm_e8<true><<<(unsigned)grid, kGT, 0, s>>>(a, OB);
+        else k_gemm_e8<false><<<(unsigned)grid, kGT, 0, s>>>(a, OB);
+      }
       return 0;
     }
   }
@@ -339,10 +386,13 @@ int launch_gemm_e8d4(const LinearArgs& a, hipStream_t s) {
     t.B = a.B - b0 < kMatvecMaxBatch ? a.B - b0 : kMatvecMaxBatch;
     t.x = a.x + (size_t)b0 * a.N;
     t.y = a.y + (size_t)b0 * a.ldy;
-    const int rc = launch_matvec<KIND_E8D4>(t, s);
+    const int rc = launch_matvec<KIND>(t, s);
     if (rc) return rc;
   }
   return 0;
 }
+
+template int launch_gemm<KIND_E8D4>(const LinearArgs&, hipStream_t);
+template int launch_gemm<KIND_E8>(const LinearArgs&, hipStream_t);
 
 }  // namespace eptq

@@ -67,7 +67,8 @@ struct MultiArgs {
 
 template <int KIND> int launch_dequant(const DequantArgs& a, hipStream_t s);
 template <int KIND> int launch_matvec(const LinearArgs& a, hipStream_t s);
-int launch_gemm_e8d4(const LinearArgs& a, hipStream_t s);
+// MFMA prefill GEMM (B > 16); batch tiles of the matvec where it does not apply.
+template <int KIND> int launch_gemm(const LinearArgs& a, hipStream_t s);
 // Persistent E8-D4 decode (B <= 8); -1 when the layer/batch is outside its range.
 int launch_decode_e8d4(const LinearArgs& a, hipStream_t s);
 // Several layers sharing x (same N, B, table, dtypes) in one launch; -1 when

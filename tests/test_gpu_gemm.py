@@ -48,6 +48,24 @@ def test_gemm_rel_l2(out, inp, T, p, bias, qb):
     assert e <= TOL
 
 
+@pytest.mark.parametrize("out,inp,T,p,bias,qb", [
+    (1024, 1024, 128, 0.002, False, None),
+    (3072, 768, 64, 0.002, True, None),        # OPT-125m fc1 (configuration 0) at 64 tokens
+    (2048, 1024, 300, 0.01, False, 128),       # S_group, partial token tile
+    (256, 4096, 200, 0.05, True, None),        # dense markers: > LDS entry cap per tile
+])
+def test_gemm_e8_rel_l2(out, inp, T, p, bias, qb):
+    """E8-lattice layers at prefill batch sizes take the same MFMA GEMM with
+    table rows gathered from global memory."""
+    print(f"gemm e8 {out}x{inp} T={T} p={p} bias={bias} qb={qb}", flush=True)
+    qd = make_layer(out, inp, seed=out + 3 * T, percmask=p, bias=bias, qb_size=qb)
+    x = make_x(T, inp, seed=T + 1)
+    y, ref = _run(qd, x, kind="e8_lattice", radius=1.6)
+    e = rel_l2(y, ref)
+    print(f"  rel_l2 {e:.2e}")
+    assert e <= TOL
+
+
 def test_gemm_config3_shape():
     """Llama-2-13B q/k/v/o layer, 2048 tokens."""
     print("gemm 5120x5120 T=2048", flush=True)
