@@ -3,6 +3,8 @@
 // index decode) is in decode_layer.h; this file selects the layer of each
 // workgroup and sizes the launch.
 
+#include <stdlib.h>
+
 #include "decode_layer.h"
 
 namespace eptq {
@@ -49,6 +51,16 @@ __global__ __launch_bounds__(kT) void k_decode_e8d4(MultiArgs ma) {
 }
 
 namespace dec {
+
+// Smallest batch that takes the matrix-core decode kernel (EPTQ_MFMA_MIN_BATCH
+// overrides, for tests and tuning).
+int mfma_min_batch_init() {
+  const char* e = getenv("EPTQ_MFMA_MIN_BATCH");
+  if (e && *e) return atoi(e);
+  // Below 5 the vector kernel (one dot product per batch row) is faster on
+  // Llama shapes; from 5 on the MFMA kernel's cost does not grow with B.
+  return 5;
+}
 
 int cu_count() {
   static int n_cu = 0;
@@ -159,6 +171,7 @@ int launch_b(const LinearArgs* l, int n, hipStream_t s) {
 int launch_decode_e8d4_multi(const LinearArgs* l, int n, hipStream_t s) {
   if (n < 1 || n > kMaxLayers) return -1;
   const LinearArgs& a = l[0];
+  if (a.B >= mfma_min_batch() && launch_decode_mfma_multi(l, n, s) == 0) return 0;
   for (int i = 1; i < n; ++i)
     if (l[i].N != a.N || l[i].B != a.B || l[i].x != a.x || l[i].codes != a.codes ||
         l[i].codes_f32 != a.codes_f32 || l[i].x_bf16 != a.x_bf16 || (l[i].S != nullptr) != (a.S != nullptr) ||

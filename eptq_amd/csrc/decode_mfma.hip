@@ -1,0 +1,457 @@
+// E8-D4 decode matvec for batches of 1..16 on the matrix cores.
+//
+// Same result as the reference decode kernels (csrc/eptq_kernels.cu:161-292,
+// kernels/triton_e8d4.py:47-157): y = g ⊙ (decode(Q)·(h ⊙ S ⊙ x)ᵀ + CSR(O)) + bias,
+// here for the batches where the vector kernel (decode_layer.h) would spend
+// one dot-product per batch row and weight: the contraction runs on
+// v_mfma_f32_16x16x32_f16 with the batch as the MFMA's 16 columns.
+//
+// Tiles.  A workgroup owns one tile of 8 block rows (64 output rows) of one
+// layer and all N columns; S "column" waves split the columns in blocks of 64
+// and one more wave stages the tile's critical blocks.  The S partial sums
+// meet in LDS at the end, where the critical-block corrections, g, bias and
+// the activation scale are applied and y is written.
+//
+// MFMA operands.  D(16 x 16) += A(16 x 32)·B(32 x 16) with lane l holding
+// A[l%16][8(l/16) .. +7], B[8(l/16) .. +7][l%16] and D[4(l/16) .. +3][l%16]:
+//   * B = x·h: lane (b = l%16, kg = l/16) holds the activation of batch row b
+//     at the 8 columns of its K group (one 16-byte load per column half of a
+//     block);
+//   * A = weights: lane (i = l%16, kg) decodes the 8 indices of block row
+//     i/2 at those same 8 columns through the LDS table, half i%2 of each
+//     vector (rows 0-3 or 4-7 of the block).  Each table lookup gives 4 rows
+//     of one column; 4 MFMAs per 32 columns take row c (c = 0..3) of the
+//     lane's half, so the operand of MFMA c is a byte-permute of the lookups
+//     and no lane exchanges data with another.
+//   D of MFMA c: lane (b, lg = l/16), element v = output row 16·lg + 4v + c of
+//   the tile for batch row b.
+//
+// Activation scaling is the vector kernel's for B >= 2: h is scaled by a
+// workgroup-uniform power of two 2^-e with max|h|·2^-e <= 1, so the fp16
+// operand |x·h·2^-e| <= |x| cannot overflow; MFMA products of fp16 operands
+// are exact in the fp32 accumulators and 2^e is restored at the output.
+//
+// Critical blocks (v = 32767) decode as table row 511 in both halves; the
+// staging wave loads the tile's CSR entries (column, O, and x·h at that
+// column for each batch row) into LDS while the column waves run, and the
+// output stage adds O·(x h) minus what the marker contributed.
+
+#include "decode_layer.h"
+
+namespace eptq {
+namespace dmf {
+
+using dec::gp;
+using dec::h2;
+using dec::kBufferWord3;
+using dec::kNonTemporal;
+using dec::perm;
+using dec::pk_mul;
+
+constexpr int kTile = 8;        // block rows per tile (64 output rows)
+constexpr int kBlk = 64;        // columns per block: 4 K groups x 16
+constexpr int kDepth = 6;       // blocks of indices and activations in flight per lane
+constexpr int kEarly = 2;       // of which issued before the activation-scale pass
+constexpr int kEntCap = 256;    // critical blocks of a tile prefetched before the column loop
+constexpr int kRedLd = 68;      // floats per batch row of a wave's partial sums
+constexpr int kS = 8;           // column waves per workgroup
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc((void*)p, (short)0, bytes, kBufferWord3);
+}
+template <int AUX = 0>
+__device__ __forceinline__ u32x4 ld16(__amdgpu_buffer_rsrc_t r, int off) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, AUX));
+}
+__device__ __forceinline__ uint16_t ld2(__amdgpu_buffer_rsrc_t r, int off) {
+  return (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+}
+// Bitfield insert with a per-lane mask: (mask & a) | (~mask & b).
+__device__ __forceinline__ uint32_t bfi_v(uint32_t mask, uint32_t a, uint32_t b) {
+  uint32_t r;
+  asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "v"(mask), "v"(a), "v"(b));
+  return r;
+}
+// (t >> 16) & 0xFF8 in one op (SDWA word select of the second operand).
+__device__ __forceinline__ uint32_t hi_addr(uint32_t t) {
+  uint32_t r;
+  asm("v_and_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:WORD_1"
+      : "=v"(r) : "s"(0xFF8u), "v"(t));
+  return r;
+}
+__device__ __forceinline__ f16 as_f16(uint16_t v) { return __builtin_bit_cast(f16, v); }
+__device__ __forceinline__ uint16_t bits(f16 v) { return __builtin_bit_cast(uint16_t, v); }
+
+// Columns rounded up to whole blocks: the activation-scale rows in LDS are
+// zero past N, so the last block's extra columns contribute nothing.
+__host__ __device__ inline int padded_cols(int N) { return (N + kBlk - 1) / kBlk * kBlk; }
+
+// Dynamic LDS: hs[Np] = fp16(h·2^-e) and, with S_group, hss[Np] = fp16(hs·S)
+// during the column loop; the partial sums red[S][16][kRedLd] afterwards.
+__host__ __device__ inline size_t dyn_bytes(int N, bool has_s) {
+  const size_t act = (size_t)padded_cols(N) * 2 * (has_s ? 2 : 1);
+  const size_t red = (size_t)kS * 16 * kRedLd * 4;
+  return act > red ? act : red;
+}
+
+template <int S, bool HAS_S>
+__global__ __launch_bounds__((S + 1) * 64) void k_decode_mfma(MultiArgs ma) {
+  constexpr int NT = (S + 1) * 64;
+  __shared__ f16x4 tab[512];
+  // The tile's critical blocks as the output stage reads them: O, and the
+  // activation operand at the block's column, fp16(x·hs) (xo) and
+  // fp16(x·hsa) (xm: what the main loop multiplied the marker's row by).
+  __shared__ __attribute__((aligned(16))) u32x4 eov[kEntCap];
+  __shared__ __attribute__((aligned(16))) uint16_t exo[kEntCap][16];
+  __shared__ __attribute__((aligned(16))) uint16_t exm[HAS_S ? kEntCap : 1][16];
+  __shared__ int erow[kTile + 1];   // entry index (from the tile's first) where each block row starts
+  __shared__ int ebase;             // the tile's first entry
+  __shared__ float wmax[S + 1];
+  extern __shared__ __attribute__((aligned(16))) char dyn[];
+
+  int li = 0;
+#pragma unroll
+  for (int l = 1; l < kMaxLayers; ++l)
+    if (l < ma.n && (int)blockIdx.x >= ma.start[l]) li = l;
+  const LinearArgs a = li == 0 ? ma.l[0] : li == 1 ? ma.l[1] : li == 2 ? ma.l[2] : ma.l[3];
+  const int tile = (int)blockIdx.x - ma.start[li];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int M = a.M, N = a.N, B = a.B, ldx = a.ldx;
+  const int Np = padded_cols(N), nchp = Np >> 3;
+  const int m0 = tile * kTile;
+  const int grp = HAS_S ? (8 * m0) / a.qb : 0;
+  uint16_t* __restrict__ hs = (uint16_t*)dyn;
+  uint16_t* __restrict__ hss = hs + Np;
+  float (*red)[16][kRedLd] = (float (*)[16][kRedLd])dyn;
+
+  const __amdgpu_buffer_rsrc_t rh = rsrc(a.h, N * 2);
+  const __amdgpu_buffer_rsrc_t rx = rsrc(a.x, ((B - 1) * ldx + N) * 2);
+  const __amdgpu_buffer_rsrc_t rs = rsrc(HAS_S ? a.S + (size_t)grp * N : nullptr, HAS_S ? N * 2 : 0);
+
+  // Table, h and the S row first: their waits then do not include the HBM
+  // index loads (vmcnt counts loads in issue order).
+  f16x4 tload = {};
+  if (tid < 512) tload = ((const f16x4*)a.codes)[tid];
+  u32x4 hw[4], sw[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int c = tid + NT * k;
+    hw[k] = ld16(rh, c * 16);                  // zero past N
+    if (HAS_S) sw[k] = ld16(rs, c * 16);
+  }
+  // g and bias of this thread's two outputs (thread t < 512: rows 2(t%32), +1
+  // of the tile), read long before the output stage needs them.
+  const int orow = 8 * m0 + (tid & 31) * 2;
+  const int oi = orow < 8 * M ? orow : 0;
+  const uint32_t gpair = *gp((const uint32_t*)(a.g + oi));
+  const __amdgpu_buffer_rsrc_t rbias = rsrc(a.bias, a.bias ? 16 * M : 0);
+  const uint32_t bpair = __builtin_amdgcn_raw_buffer_load_b32(rbias, oi * 2, 0, 0);
+
+  // Column waves: blocks [blo, bhi) of the tile's rows, the first kDepth of
+  // them in flight.  Lane (i, kg) reads the 16 indices of block row m0 + i/2
+  // at columns 64·blk + 16·kg .. +15; lane (b, kg) the activations of batch
+  // row b at the same columns (rows past M and batch rows past B read zeros).
+  const int nb = Np / kBlk;
+  const int blo = wave * nb / S, bhi = (wave + 1) * nb / S;
+  const int i = lane & 15, kg = lane >> 4;
+  const int qrow = m0 + (i >> 1);
+  const __amdgpu_buffer_rsrc_t rq = rsrc(a.Q, M * N * 2);
+  int qo = qrow < M ? (qrow * N + blo * kBlk + 16 * kg) * 2 : 0x40000000;
+  int xo = ((lane & 15) * ldx + blo * kBlk + 16 * kg) * 2;
+  u32x4 qv[kDepth][2], xv[kDepth][2];
+  int rpv = 0;
+  if (wave < S) {
+#pragma unroll
+    for (int d = 0; d < kEarly; ++d) {
+      if (blo + d < bhi) {
+        qv[d][0] = ld16<kNonTemporal>(rq, qo + d * kBlk * 2);
+        qv[d][1] = ld16<kNonTemporal>(rq, qo + d * kBlk * 2 + 16);
+        xv[d][0] = ld16(rx, xo + d * kBlk * 2);
+        xv[d][1] = ld16(rx, xo + d * kBlk * 2 + 16);
+      }
+    }
+  } else {
+    // Staging wave: the tile's CSR row pointers.
+    const __amdgpu_buffer_rsrc_t rp = rsrc(a.O_row_ptr, (M + 1) * 4);
+    const int r = m0 + (lane <= kTile ? lane : kTile);
+    rpv = (int)__builtin_amdgcn_raw_buffer_load_b32(rp, (r < M ? r : M) * 4, 0, 0);
+  }
+
+  // h (and the S row) into LDS as loaded; max|h|.
+  float mx = 0.0f;
+  auto put = [&](int c, const u32x4 h, const u32x4 sv) {
+    if (c < nchp) {
+      *(u32x4*)(hs + c * 8) = h;
+      if (HAS_S) *(u32x4*)(hss + c * 8) = sv;
+      const f16x8 hv = __builtin_bit_cast(f16x8, h);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) mx = fmaxf(mx, fabsf((float)hv[e]));
+    }
+  };
+#pragma unroll
+  for (int k = 0; k < 4; ++k) put(tid + NT * k, hw[k], HAS_S ? sw[k] : hw[k]);
+  for (int c = tid + 4 * NT; c < nchp; c += NT) put(c, ld16(rh, c * 16), HAS_S ? ld16(rs, c * 16) : u32x4{});
+  mx = fmaxf(mx, partner<1>(mx));
+  mx = fmaxf(mx, partner<2>(mx));
+  mx = fmaxf(mx, partner<4>(mx));
+  mx = fmaxf(mx, partner<8>(mx));
+  mx = fmaxf(mx, partner<16>(mx));
+  mx = fmaxf(mx, partner<32>(mx));
+  if (lane == 0) wmax[wave] = mx;
+  if (tid < 512) tab[tid ^ 0x100] = tload;
+
+  // Staging wave: the entries' columns and O vectors.
+  const int rsv = __builtin_amdgcn_readlane(rpv, 0);
+  const int nent = __builtin_amdgcn_readlane(rpv, kTile) - rsv;
+  const int nst = nent < kEntCap ? nent : kEntCap;
+  constexpr int kPass = kEntCap / 64;
+  int scol[kPass];
+  u32x4 so[kPass];
+  if (wave == S) {
+    if (lane <= kTile) erow[lane] = rpv - rsv;
+    if (lane == 0) ebase = rsv;
+    const __amdgpu_buffer_rsrc_t rc = rsrc(a.O_col + rsv, nst * 4);
+    const __amdgpu_buffer_rsrc_t ro = rsrc(a.O + (size_t)rsv * 8, nst * 16);
+#pragma unroll
+    for (int p = 0; p < kPass; ++p) {
+      scol[p] = (int)__builtin_amdgcn_raw_buffer_load_b32(rc, (lane + 64 * p) * 4, 0, 0);
+      so[p] = ld16(ro, (lane + 64 * p) * 16);
+    }
+  }
+  __syncthreads();
+  // Workgroup scale 2^-e with max|h|·2^-e <= 1; hs = fp16(h·2^-e), hss = fp16(hs·S).
+  mx = wmax[0];
+#pragma unroll
+  for (int w = 1; w <= S; ++w) mx = fmaxf(mx, wmax[w]);
+  int ex = 0;
+  if (mx > 1.0f) ex = (int)((__builtin_bit_cast(uint32_t, mx) >> 23) & 0xff) - 126;   // 2^ex >= mx
+  const float out_scale = __builtin_ldexpf(1.0f, ex);
+  const f16 down = (f16)__builtin_ldexpf(1.0f, -ex);
+  const uint32_t down2 = __builtin_bit_cast(uint32_t, (h2){down, down});
+  for (int c = tid; c < nchp; c += NT) {
+    u32x4 h = *(const u32x4*)(hs + c * 8);
+#pragma unroll
+    for (int d = 0; d < 4; ++d) h[d] = pk_mul(h[d], down2);
+    *(u32x4*)(hs + c * 8) = h;
+    if (HAS_S) {
+      u32x4 sv = *(const u32x4*)(hss + c * 8);
+#pragma unroll
+      for (int d = 0; d < 4; ++d) sv[d] = pk_mul(h[d], sv[d]);
+      *(u32x4*)(hss + c * 8) = sv;
+    }
+  }
+  __syncthreads();
+  const char* __restrict__ tabB = (const char*)tab;
+  const f16x4 t5 = tab[511 ^ 0x100];
+  const uint16_t* __restrict__ hsa = HAS_S ? hss : hs;   // the scale row of the main loop
+
+  f32x4 acc[4];
+  if (wave < S) {
+    // ---- column wave --------------------------------------------------------
+    // Byte addresses of the two indices of a word w in this lane's half:
+    //   rows 0-3: t = w >> 4;  rows 4-7: t = bfi(0x0C000C00, w >> 4, w << 3)
+    // (bits 10-11 of each half from v >> 4, bits 3-9 = (v & 127) << 3), then
+    // (t & 0xFF8) for the low index and ((t >> 16) & 0xFF8) for the high one.
+    const uint32_t tmask = (i & 1) ? 0x0C000C00u : 0xFFFFFFFFu;
+    const uint32_t tsh = (i & 1) ? 3u : 0u;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) acc[c] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+
+    auto block = [&](const u32x4 (&q)[2], const u32x4 (&x)[2], int blk) {
+#pragma unroll
+      for (int g2 = 0; g2 < 2; ++g2) {
+        const u32x4 sc = *(const u32x4*)(hsa + blk * kBlk + 16 * kg + 8 * g2);
+        u32x4 bx;
+#pragma unroll
+        for (int d = 0; d < 4; ++d) bx[d] = pk_mul(x[g2][d], sc[d]);
+        u32x2 lo[4], hi[4];
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+          const uint32_t w0 = q[g2][d];
+          const uint32_t t = bfi_v(tmask, w0 >> 4, w0 << tsh);
+          lo[d] = *(const u32x2*)(tabB + (t & 0xFF8u));
+          hi[d] = *(const u32x2*)(tabB + hi_addr(t));
+        }
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          u32x4 aw;
+#pragma unroll
+          for (int d = 0; d < 4; ++d) {
+            const uint32_t l = c < 2 ? lo[d][0] : lo[d][1];
+            const uint32_t h = c < 2 ? hi[d][0] : hi[d][1];
+            aw[d] = perm(h, l, (c & 1) ? 0x07060302u : 0x05040100u);
+          }
+          acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, aw),
+                                                          __builtin_bit_cast(f16x8, bx), acc[c], 0, 0, 0);
+        }
+      }
+    };
+
+    for (int k = blo; k < bhi; k += kDepth) {
+#pragma unroll
+      for (int d = 0; d < kDepth; ++d) {
+        const int blk = k + d;
+        if (blk >= bhi) break;                     // uniform
+        // First pass: the ring beyond the kEarly blocks issued up front is
+        // filled one block per step, between the blocks' arithmetic, so the
+        // burst does not hold the wave at its issue.
+        if (d + kEarly < kDepth && k == blo && blk + kEarly < bhi) {
+          const int off = (d + kEarly) * kBlk * 2;
+          qv[d + kEarly < kDepth ? d + kEarly : 0][0] = ld16<kNonTemporal>(rq, qo + off);
+          qv[d + kEarly < kDepth ? d + kEarly : 0][1] = ld16<kNonTemporal>(rq, qo + off + 16);
+          xv[d + kEarly < kDepth ? d + kEarly : 0][0] = ld16(rx, xo + off);
+          xv[d + kEarly < kDepth ? d + kEarly : 0][1] = ld16(rx, xo + off + 16);
+        }
+        block(qv[d], xv[d], blk);
+        if (blk + kDepth < bhi) {
+          const int off = (blk - blo + kDepth) * kBlk * 2;
+          qv[d][0] = ld16<kNonTemporal>(rq, qo + off);
+          qv[d][1] = ld16<kNonTemporal>(rq, qo + off + 16);
+          xv[d][0] = ld16(rx, xo + off);
+          xv[d][1] = ld16(rx, xo + off + 16);
+        }
+      }
+    }
+  } else {
+    // ---- staging wave: the tile's first kEntCap critical blocks into LDS ------
+#pragma unroll
+    for (int p = 0; p < kPass; ++p) {
+      if (64 * p >= nst) break;                    // uniform
+      const int e = lane + 64 * p;
+      const int col = scol[p];
+      const int cc = e < nst && (unsigned)col < (unsigned)N ? col : 0;
+      uint16_t xb[16];
+#pragma unroll
+      for (int bb = 0; bb < 16; ++bb) xb[bb] = ld2(rx, bb < B ? (bb * ldx + cc) * 2 : 0x7ffffff0);
+      const f16 h1 = as_f16(hs[cc]), hm = as_f16(hsa[cc]);
+      if (e < nst) {
+        eov[e] = so[p];
+        u32x4 wo[2], wm[2];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          const f16 x0 = as_f16(xb[2 * q]), x1 = as_f16(xb[2 * q + 1]);
+          wo[q >> 2][q & 3] = (uint32_t)bits(x0 * h1) | ((uint32_t)bits(x1 * h1) << 16);
+          if (HAS_S) wm[q >> 2][q & 3] = (uint32_t)bits(x0 * hm) | ((uint32_t)bits(x1 * hm) << 16);
+        }
+        *(u32x4*)&exo[e][0] = wo[0];
+        *(u32x4*)&exo[e][8] = wo[1];
+        if (HAS_S) {
+          *(u32x4*)&exm[HAS_S ? e : 0][0] = wm[0];
+          *(u32x4*)&exm[HAS_S ? e : 0][8] = wm[1];
+        }
+      }
+    }
+  }
+  // The activation-scale rows are no longer read: the partial sums take
+  // their place.  red[wave][b][16 lg + 4v + c] = acc[c][v].
+  __syncthreads();
+  if (wave < S) {
+    const int b = lane & 15, lg = lane >> 4;
+#pragma unroll
+    for (int v = 0; v < 4; ++v)
+      *(f32x4*)&red[wave][b][16 * lg + 4 * v] = (f32x4){acc[0][v], acc[1][v], acc[2][v], acc[3][v]};
+  }
+  __syncthreads();
+
+  // ---- output: thread t < 512 -> batch row t/32, rows 2(t%32), +1 ----------
+  if (tid < 512) {
+    const int b = tid >> 5, r = (tid & 31) * 2;
+    if (b < B && orow < 8 * M) {
+      float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+      for (int w = 0; w < S; ++w) {
+        const float2 p = *(const float2*)&red[w][b][r];
+        s0 += p.x;
+        s1 += p.y;
+      }
+      // Critical blocks of this block row: rows k, k+1 of each O (one 4-byte
+      // read), two entries per step so the LDS reads of one overlap the other.
+      const int br = r >> 3, k = r & 7;
+      const int e0 = erow[br], e1 = erow[br + 1];
+      const int es = e1 < kEntCap ? e1 : kEntCap;
+      const h2 t5p = {t5[k & 3], t5[(k + 1) & 3]};
+      auto corr1 = [&](int e) {
+        const h2 o = __builtin_bit_cast(h2, *((const uint32_t*)&eov[e] + (k >> 1)));
+        const float xo = (float)as_f16(exo[e][b]);
+        const float xm = HAS_S ? (float)as_f16(exm[HAS_S ? e : 0][b]) : xo;
+        s0 += (float)o[0] * xo - (float)t5p[0] * xm;
+        s1 += (float)o[1] * xo - (float)t5p[1] * xm;
+      };
+      int e = e0;
+      for (; e + 1 < es; e += 2) {
+        corr1(e);
+        corr1(e + 1);
+      }
+      if (e < es) corr1(e);
+      // Beyond the staged entries: straight from memory (the activation
+      // scales are no longer in LDS).
+      for (int e2 = es > e0 ? es : e0; e2 < e1; ++e2) {
+        const int ge = ebase + e2;
+        const int col = gp(a.O_col)[ge];
+        const f16x8 o = *gp((const f16x8*)(a.O + (size_t)ge * 8));
+        const f16 x16 = as_f16(gp(a.x)[(size_t)b * ldx + col]);
+        const f16 h1 = as_f16(gp((const uint16_t*)a.h)[col]) * down;
+        const float xo = (float)(f16)(x16 * h1);
+        const float xm = HAS_S ? (float)(f16)(x16 * (f16)(h1 * as_f16(gp((const uint16_t*)a.S)[(size_t)grp * N + col]))) : xo;
+        s0 += (float)o[k] * xo - (float)t5p[0] * xm;
+        s1 += (float)o[k + 1] * xo - (float)t5p[1] * xm;
+      }
+      const h2 gg = __builtin_bit_cast(h2, gpair), bb = __builtin_bit_cast(h2, bpair);
+      const float y0 = s0 * out_scale * (float)gg[0] + (float)bb[0];
+      const float y1 = s1 * out_scale * (float)gg[1] + (float)bb[1];
+      const uint32_t pk = (uint32_t)bits((f16)y0) | ((uint32_t)bits((f16)y1) << 16);
+      *gp((uint32_t*)(a.y + (size_t)b * a.ldy + orow)) = pk;
+    }
+  }
+}
+
+template <int S, bool HAS_S>
+int launch_t(const LinearArgs* l, int n, hipStream_t s) {
+  MultiArgs ma;
+  ma.n = n;
+  ma.start[0] = 0;
+  for (int k = 0; k < kMaxLayers; ++k) {
+    ma.l[k] = l[k < n ? k : 0];
+    ma.start[k + 1] = ma.start[k] + (k < n ? (l[k].M + kTile - 1) / kTile : 0);
+  }
+  auto kern = k_decode_mfma<S, HAS_S>;
+  const size_t dyn = dyn_bytes(l[0].N, HAS_S);
+  static size_t attr = 0;
+  if (dyn > attr) {
+    if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)dyn) != hipSuccess)
+      return -1;
+    attr = dyn;
+  }
+  kern<<<ma.start[n], (S + 1) * 64, dyn, s>>>(ma);
+  return 0;
+}
+
+}  // namespace dmf
+
+// Returns 0 if launched, -1 if the layers are outside this kernel's range
+// (then the vector decode kernel or the generic matvec takes them).
+int launch_decode_mfma_multi(const LinearArgs* l, int n, hipStream_t s) {
+  if (n < 1 || n > kMaxLayers) return -1;
+  const LinearArgs& a = l[0];
+  if (a.B < 1 || a.B > 16 || a.x_bf16 || a.codes_f32 || a.prep != 0 || (a.N & 7) != 0) return -1;
+  // y is written in pairs of fp16 (4-byte stores).
+  if ((a.ldy & 1) != 0 || ((uintptr_t)a.y & 3) != 0) return -1;
+  for (int i = 0; i < n; ++i) {
+    const LinearArgs& b = l[i];
+    if (b.N != a.N || b.B != a.B || b.x != a.x || b.ldx != a.ldx || b.codes != a.codes ||
+        b.codes_f32 != a.codes_f32 || b.x_bf16 != a.x_bf16 || (b.S != nullptr) != (a.S != nullptr) ||
+        b.prep != 0 || ((uintptr_t)b.y & 3) != 0)
+      return -1;
+    // S_group: one scale row per 64-row tile.
+    if (b.S && (b.qb <= 0 || b.qb % 64 != 0)) return -1;
+    if ((long)b.M * b.N * 2 >= (1L << 30)) return -1;   // 32-bit buffer offsets
+  }
+  if ((long)(a.B - 1) * a.ldx + a.N >= (1L << 30)) return -1;
+  // The activation-scale rows and the staged entries share the 160 KB of LDS.
+  if (dmf::dyn_bytes(a.N, a.S != nullptr) > 120 * 1024) return -1;
+  return a.S ? dmf::launch_t<dmf::kS, true>(l, n, s) : dmf::launch_t<dmf::kS, false>(l, n, s);
+}
+
+}  // namespace eptq

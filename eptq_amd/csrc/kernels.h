@@ -75,6 +75,15 @@ int launch_decode_e8d4(const LinearArgs& a, hipStream_t s);
 // any of them is outside the decode kernel's range.
 int launch_decode_e8d4_multi(const LinearArgs* layers, int n, hipStream_t s);
 
+// Matrix-core E8-D4 decode (B <= 16, fp16 x and table, no fused preparation);
+// -1 when the layers are outside its range.
+int launch_decode_mfma_multi(const LinearArgs* layers, int n, hipStream_t s);
+namespace dec { int mfma_min_batch_init(); }
+inline int mfma_min_batch() {
+  static const int v = dec::mfma_min_batch_init();
+  return v;
+}
+
 // Largest batch served by the decode matvec; larger batches take the GEMM.
 constexpr int kMatvecMaxBatch = 16;
 

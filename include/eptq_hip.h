@@ -83,8 +83,8 @@ typedef struct {
 /*
  * Several E8-D4 layers that read the same activations x (B, N) — e.g. q, k
  * and v, or gate and up — into one output y (B, ldy), in one launch of the
- * decode matvec when it takes them all (up to 4 layers, B <= 8, fp16 table),
- * otherwise one launch per layer.  Each layer keeps its own h, g, CSR, bias
+ * decode matvec when it takes them all (up to 4 layers, B <= 16, fp16 table;
+ * fp16 x for B > 8), otherwise one launch per layer.  Each layer keeps its own h, g, CSR, bias
  * and S_group, so unlike a concatenated weight it needs no shared column
  * scales.  No counterpart in the reference, whose decoder calls one
  * EPTQLinear per projection (kernels/linear.py:154-212); its callers are
