@@ -131,6 +131,10 @@ def make_units(torch, codes, layers, xs, B):
     from eptq_amd.kernels import _lib
     lib = _lib.load()
     units, i = [], 0
+    # Split-K workspace of the matrix-core decode (batches of 5..16); the
+    # launches of a step run one after another on one stream.
+    from eptq_amd.kernels import decode_workspace
+    work = decode_workspace(codes.device)
     while i < len(layers):
         name = layers[i]["name"]
         grp = layers[i:i + 3] if name == "q" else layers[i:i + 2] if name == "gate" else layers[i:i + 1]
@@ -148,7 +152,8 @@ def make_units(torch, codes, layers, xs, B):
 
         def run(stream, arr=arr, n=len(grp), x=x, y=y, off=off, N=grp[0]["inp"]):
             rc = lib.eptq_e8d4_forward_multi(n, arr, codes.data_ptr(), _lib.EPTQ_F16, x.data_ptr(),
-                                             _lib.EPTQ_F16, N, B, y.data_ptr(), off, stream)
+                                             _lib.EPTQ_F16, N, B, y.data_ptr(), off, work.data_ptr(),
+                                             work.numel(), stream)
             if rc:
                 _lib.check(rc, "eptq_e8d4_forward_multi")
         units.append((run, grp, arr, y))

@@ -246,9 +246,11 @@ int eptq_e8_forward(const void* Q, const void* codes, int codes_dtype, const voi
 
 int eptq_e8d4_forward_multi(int n_layers, const eptq_layer* layers, const void* codes,
                             int codes_dtype, const void* x, int x_dtype, int N, int B, void* y,
-                            int ldy, void* stream) {
+                            int ldy, void* work, long long work_bytes, void* stream) {
   const char* fn = "eptq_e8d4_forward_multi";
   if (n_layers <= 0 || !layers) return fail(EPTQ_EINVAL, "%s: n_layers=%d", fn, n_layers);
+  if (work && (!aligned16(work) || work_bytes < 0))
+    return fail(EPTQ_EINVAL, "%s: work must be 16-byte aligned with work_bytes >= 0", fn);
   if (B < 0) return fail(EPTQ_EINVAL, "%s: B=%d", fn, B);
   if (B > 0 && (!x || !y)) return fail(EPTQ_EINVAL, "%s: null x/y", fn);
   eptq::LinearArgs a[eptq::kMaxLayers];
@@ -270,7 +272,7 @@ int eptq_e8d4_forward_multi(int n_layers, const eptq_layer* layers, const void* 
   if (B == 0) return EPTQ_OK;
   hipStream_t s = (hipStream_t)stream;
   // One launch when the decode kernel takes them all, else one per layer.
-  if (n > eptq::kMaxLayers || eptq::launch_decode_e8d4_multi(a, n, s) != 0) {
+  if (n > eptq::kMaxLayers || eptq::launch_decode_e8d4_multi(a, n, s, work, work ? work_bytes : 0) != 0) {
     for (int l = 0; l < n; ++l) {
       eptq::LinearArgs t;
       const eptq_layer& L = layers[l];
@@ -284,6 +286,8 @@ int eptq_e8d4_forward_multi(int n_layers, const eptq_layer* layers, const void* 
   }
   return check_launch(fn);
 }
+
+long long eptq_e8d4_work_bytes(void) { return eptq::decode_mfma_work_bytes(); }
 
 int eptq_e8d4_chain_create(int n_stages, const eptq_stage* stages, const void* codes,
                            int codes_dtype, eptq_chain** chain) {

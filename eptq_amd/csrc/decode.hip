@@ -168,10 +168,10 @@ int launch_b(const LinearArgs* l, int n, hipStream_t s) {
 }  // namespace
 
 // Returns 0 if launched, -1 if the layers/batch are outside the kernel's range.
-int launch_decode_e8d4_multi(const LinearArgs* l, int n, hipStream_t s) {
+int launch_decode_e8d4_multi(const LinearArgs* l, int n, hipStream_t s, void* work, long long work_bytes) {
   if (n < 1 || n > kMaxLayers) return -1;
   const LinearArgs& a = l[0];
-  if (a.B >= mfma_min_batch() && launch_decode_mfma_multi(l, n, s) == 0) return 0;
+  if (a.B >= mfma_min_batch() && launch_decode_mfma_multi(l, n, s, work, work_bytes) == 0) return 0;
   for (int i = 1; i < n; ++i)
     if (l[i].N != a.N || l[i].B != a.B || l[i].x != a.x || l[i].codes != a.codes ||
         l[i].codes_f32 != a.codes_f32 || l[i].x_bf16 != a.x_bf16 || (l[i].S != nullptr) != (a.S != nullptr) ||

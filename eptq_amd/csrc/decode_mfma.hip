@@ -82,6 +82,22 @@ __device__ __forceinline__ uint32_t hi_addr(uint32_t t) {
 __device__ __forceinline__ f16 as_f16(uint16_t v) { return __builtin_bit_cast(f16, v); }
 __device__ __forceinline__ uint16_t bits(f16 v) { return __builtin_bit_cast(uint16_t, v); }
 
+// Split-K workspace: per-tile arrival counters, then the fp32 partial sums
+// [tile][part][16][64] of tiles whose columns are split over P workgroups.
+constexpr int kMaxCounters = 16384;
+constexpr size_t kCntBytes = (size_t)kMaxCounters * 4;
+constexpr size_t kPartBytes = 16 * 64 * 4;
+constexpr int kMaxParts = 4;
+
+__device__ __forceinline__ void st_pair(float* p, float a, float b) {
+  const uint64_t v = (uint64_t)__builtin_bit_cast(uint32_t, a) | ((uint64_t)__builtin_bit_cast(uint32_t, b) << 32);
+  __hip_atomic_store((uint64_t*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float2 ld_pair(const float* p) {
+  const uint64_t v = __hip_atomic_load((const uint64_t*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return make_float2(__builtin_bit_cast(float, (uint32_t)v), __builtin_bit_cast(float, (uint32_t)(v >> 32)));
+}
+
 // Columns rounded up to whole blocks: the activation-scale rows in LDS are
 // zero past N, so the last block's extra columns contribute nothing.
 __host__ __device__ inline int padded_cols(int N) { return (N + kBlk - 1) / kBlk * kBlk; }
@@ -95,7 +111,7 @@ __host__ __device__ inline size_t dyn_bytes(int N, bool has_s) {
 }
 
 template <int S, bool HAS_S>
-__global__ __launch_bounds__((S + 1) * 64) void k_decode_mfma(MultiArgs ma) {
+__global__ __launch_bounds__((S + 1) * 64) void k_decode_mfma(MultiArgs ma, int P, int* wcnt, float* wpart) {
   constexpr int NT = (S + 1) * 64;
   __shared__ f16x4 tab[512];
   // The tile's critical blocks as the output stage reads them: O, and the
@@ -114,7 +130,11 @@ __global__ __launch_bounds__((S + 1) * 64) void k_decode_mfma(MultiArgs ma) {
   for (int l = 1; l < kMaxLayers; ++l)
     if (l < ma.n && (int)blockIdx.x >= ma.start[l]) li = l;
   const LinearArgs a = li == 0 ? ma.l[0] : li == 1 ? ma.l[1] : li == 2 ? ma.l[2] : ma.l[3];
-  const int tile = (int)blockIdx.x - ma.start[li];
+  // Workgroups [start[l], start[l+1]) serve layer l: tile = wgl / P, and
+  // part p of P takes the p-th P-th of the column blocks.
+  const int wgl = (int)blockIdx.x - ma.start[li];
+  const int tile = wgl / P, part = wgl - tile * P;
+  const int tile_g = ma.start[li] / P + tile;     // index among all tiles of the launch
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -154,7 +174,8 @@ __global__ __launch_bounds__((S + 1) * 64) void k_decode_mfma(MultiArgs ma) {
   // at columns 64·blk + 16·kg .. +15; lane (b, kg) the activations of batch
   // row b at the same columns (rows past M and batch rows past B read zeros).
   const int nb = Np / kBlk;
-  const int blo = wave * nb / S, bhi = (wave + 1) * nb / S;
+  const int plo = part * nb / P, pnb = (part + 1) * nb / P - plo;
+  const int blo = plo + wave * pnb / S, bhi = plo + (wave + 1) * pnb / S;
   const int i = lane & 15, kg = lane >> 4;
   const int qrow = m0 + (i >> 1);
   const __amdgpu_buffer_rsrc_t rq = rsrc(a.Q, M * N * 2);
@@ -173,9 +194,10 @@ __global__ __launch_bounds__((S + 1) * 64) void k_decode_mfma(MultiArgs ma) {
       }
     }
   } else {
-    // Staging wave: the tile's CSR row pointers.
+    // Staging wave: the tile's CSR row pointers (part 0 applies the
+    // critical blocks; the other parts see an empty range).
     const __amdgpu_buffer_rsrc_t rp = rsrc(a.O_row_ptr, (M + 1) * 4);
-    const int r = m0 + (lane <= kTile ? lane : kTile);
+    const int r = m0 + (part == 0 && lane <= kTile ? lane : part == 0 ? kTile : 0);
     rpv = (int)__builtin_amdgcn_raw_buffer_load_b32(rp, (r < M ? r : M) * 4, 0, 0);
   }
 
@@ -356,10 +378,11 @@ __global__ __launch_bounds__((S + 1) * 64) void k_decode_mfma(MultiArgs ma) {
   __syncthreads();
 
   // ---- output: thread t < 512 -> batch row t/32, rows 2(t%32), +1 ----------
-  if (tid < 512) {
-    const int b = tid >> 5, r = (tid & 31) * 2;
-    if (b < B && orow < 8 * M) {
-      float s0 = 0.0f, s1 = 0.0f;
+  const int b = (tid >> 5) & 15, r = (tid & 31) * 2;
+  const bool ok = tid < 512 && b < B && orow < 8 * M;
+  float s0 = 0.0f, s1 = 0.0f;
+  {
+    if (ok) {
 #pragma unroll
       for (int w = 0; w < S; ++w) {
         const float2 p = *(const float2*)&red[w][b][r];
@@ -398,23 +421,70 @@ __global__ __launch_bounds__((S + 1) * 64) void k_decode_mfma(MultiArgs ma) {
         s0 += (float)o[k] * xo - (float)t5p[0] * xm;
         s1 += (float)o[k + 1] * xo - (float)t5p[1] * xm;
       }
-      const h2 gg = __builtin_bit_cast(h2, gpair), bb = __builtin_bit_cast(h2, bpair);
-      const float y0 = s0 * out_scale * (float)gg[0] + (float)bb[0];
-      const float y1 = s1 * out_scale * (float)gg[1] + (float)bb[1];
-      const uint32_t pk = (uint32_t)bits((f16)y0) | ((uint32_t)bits((f16)y1) << 16);
-      *gp((uint32_t*)(a.y + (size_t)b * a.ldy + orow)) = pk;
     }
+  }
+  // Split columns: every part leaves its partial sums (device-coherent
+  // stores, complete before the tile's counter is raised); the last part to
+  // arrive adds all P of them in part order, so the result does not depend
+  // on which part came last, writes y and resets the counter.
+  bool fin = true;
+  if (P > 1) {
+    __shared__ int last_part;
+    float* base = wpart + (size_t)tile_g * P * (kPartBytes / 4) + b * 64 + r;
+    if (ok) st_pair(base + part * (kPartBytes / 4), s0, s1);
+    __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
+    __syncthreads();
+    if (tid == 0) {
+      const int old = __hip_atomic_fetch_add(wcnt + tile_g, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      last_part = old == P - 1;
+      if (old == P - 1) __hip_atomic_store(wcnt + tile_g, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    fin = last_part != 0;
+    if (fin && ok) {
+      float t0 = 0.0f, t1 = 0.0f;
+      for (int q = 0; q < P; ++q) {
+        float2 v = make_float2(s0, s1);
+        if (q != part) v = ld_pair(base + q * (kPartBytes / 4));
+        t0 += v.x;
+        t1 += v.y;
+      }
+      s0 = t0;
+      s1 = t1;
+    }
+  }
+  if (fin && ok) {
+    const h2 gg = __builtin_bit_cast(h2, gpair), bb = __builtin_bit_cast(h2, bpair);
+    const float y0 = s0 * out_scale * (float)gg[0] + (float)bb[0];
+    const float y1 = s1 * out_scale * (float)gg[1] + (float)bb[1];
+    const uint32_t pk = (uint32_t)bits((f16)y0) | ((uint32_t)bits((f16)y1) << 16);
+    *gp((uint32_t*)(a.y + (size_t)b * a.ldy + orow)) = pk;
   }
 }
 
+// Parts per tile: as many as keep the grid within one workgroup per CU (one
+// 9-wave workgroup is what a CU holds at this kernel's register count: a
+// second round of workgroups would double the time), within the workspace
+// (none: one part).
+inline int parts_for(int tiles, void* work, long long work_bytes) {
+  if (!work || tiles > kMaxCounters) return 1;
+  int P = dec::cu_count() / tiles;
+  P = P < 1 ? 1 : P > kMaxParts ? kMaxParts : P;
+  while (P > 1 && (long long)(kCntBytes + (size_t)tiles * P * kPartBytes) > work_bytes) --P;
+  return P;
+}
+
 template <int S, bool HAS_S>
-int launch_t(const LinearArgs* l, int n, hipStream_t s) {
+int launch_t(const LinearArgs* l, int n, hipStream_t s, void* work, long long work_bytes) {
+  int tiles = 0;
+  for (int k = 0; k < n; ++k) tiles += (l[k].M + kTile - 1) / kTile;
+  const int P = parts_for(tiles, work, work_bytes);
   MultiArgs ma;
   ma.n = n;
   ma.start[0] = 0;
   for (int k = 0; k < kMaxLayers; ++k) {
     ma.l[k] = l[k < n ? k : 0];
-    ma.start[k + 1] = ma.start[k] + (k < n ? (l[k].M + kTile - 1) / kTile : 0);
+    ma.start[k + 1] = ma.start[k] + (k < n ? (l[k].M + kTile - 1) / kTile * P : 0);
   }
   auto kern = k_decode_mfma<S, HAS_S>;
   const size_t dyn = dyn_bytes(l[0].N, HAS_S);
@@ -424,7 +494,9 @@ int launch_t(const LinearArgs* l, int n, hipStream_t s) {
       return -1;
     attr = dyn;
   }
-  kern<<<ma.start[n], (S + 1) * 64, dyn, s>>>(ma);
+  int* cnt = P > 1 ? (int*)work : nullptr;
+  float* part = P > 1 ? (float*)((char*)work + kCntBytes) : nullptr;
+  kern<<<ma.start[n], (S + 1) * 64, dyn, s>>>(ma, P, cnt, part);
   return 0;
 }
 
@@ -432,7 +504,7 @@ int launch_t(const LinearArgs* l, int n, hipStream_t s) {
 
 // Returns 0 if launched, -1 if the layers are outside this kernel's range
 // (then the vector decode kernel or the generic matvec takes them).
-int launch_decode_mfma_multi(const LinearArgs* l, int n, hipStream_t s) {
+int launch_decode_mfma_multi(const LinearArgs* l, int n, hipStream_t s, void* work, long long work_bytes) {
   if (n < 1 || n > kMaxLayers) return -1;
   const LinearArgs& a = l[0];
   if (a.B < 1 || a.B > 16 || a.x_bf16 || a.codes_f32 || a.prep != 0 || (a.N & 7) != 0) return -1;
@@ -451,7 +523,12 @@ int launch_decode_mfma_multi(const LinearArgs* l, int n, hipStream_t s) {
   if ((long)(a.B - 1) * a.ldx + a.N >= (1L << 30)) return -1;
   // The activation-scale rows and the staged entries share the 160 KB of LDS.
   if (dmf::dyn_bytes(a.N, a.S != nullptr) > 120 * 1024) return -1;
-  return a.S ? dmf::launch_t<dmf::kS, true>(l, n, s) : dmf::launch_t<dmf::kS, false>(l, n, s);
+  return a.S ? dmf::launch_t<dmf::kS, true>(l, n, s, work, work_bytes)
+             : dmf::launch_t<dmf::kS, false>(l, n, s, work, work_bytes);
+}
+
+long long decode_mfma_work_bytes() {
+  return (long long)(dmf::kCntBytes + (size_t)dec::cu_count() * dmf::kPartBytes);
 }
 
 }  // namespace eptq

@@ -73,11 +73,18 @@ template <int KIND> int launch_gemm(const LinearArgs& a, hipStream_t s);
 int launch_decode_e8d4(const LinearArgs& a, hipStream_t s);
 // Several layers sharing x (same N, B, table, dtypes) in one launch; -1 when
 // any of them is outside the decode kernel's range.
-int launch_decode_e8d4_multi(const LinearArgs* layers, int n, hipStream_t s);
+// work (nullable, work_bytes long, zero-filled before its first use): lets the
+// matrix-core kernel split the columns of layers with few row tiles over
+// several workgroups; launches sharing it must not overlap in time.
+int launch_decode_e8d4_multi(const LinearArgs* layers, int n, hipStream_t s, void* work = nullptr,
+                             long long work_bytes = 0);
 
 // Matrix-core E8-D4 decode (B <= 16, fp16 x and table, no fused preparation);
 // -1 when the layers are outside its range.
-int launch_decode_mfma_multi(const LinearArgs* layers, int n, hipStream_t s);
+int launch_decode_mfma_multi(const LinearArgs* layers, int n, hipStream_t s, void* work = nullptr,
+                             long long work_bytes = 0);
+// Workspace bytes that let the matrix-core decode split every launch it takes.
+long long decode_mfma_work_bytes();
 namespace dec { int mfma_min_batch_init(); }
 inline int mfma_min_batch() {
   static const int v = dec::mfma_min_batch_init();

@@ -27,7 +27,7 @@ from ._lib import EPTQ_BF16, EPTQ_F16, EPTQ_F32, EptqError
 
 __all__ = ["e8_forward", "e8d4_forward", "e8_forward_grouped", "e8d4_forward_grouped",
            "e8_dequant", "e8d4_dequant", "EptqError", "linear_forward", "linear_forward_multi",
-           "dequant"]
+           "dequant", "decode_workspace"]
 
 
 def _ptr(t: Optional[torch.Tensor]):
@@ -98,11 +98,22 @@ def linear_forward(kind: str, Q, codes, g, h, x, O_vals, O_col, O_row_ptr, bias=
     return y
 
 
-def linear_forward_multi(layers, codes, x) -> torch.Tensor:
+def decode_workspace(device) -> torch.Tensor:
+    """A zero-filled workspace for ``linear_forward_multi(..., work=)`` on
+    ``device`` (``eptq_e8d4_work_bytes`` bytes)."""
+    with torch.cuda.device(device):
+        n = int(_lib.load().eptq_e8d4_work_bytes())
+    return torch.zeros(n, dtype=torch.uint8, device=device)
+
+
+def linear_forward_multi(layers, codes, x, work: Optional[torch.Tensor] = None) -> torch.Tensor:
     """E8-D4 layers sharing ``x`` (B, N) -> (B, Σ out) with the layers' outputs
     side by side, in one decode launch when the kernel takes them all.
     ``layers``: dicts with Q, g, h, O_vals, O_col, O_row_ptr and optional
-    bias, S_group (the EPTQLinear buffers)."""
+    bias, S_group (the EPTQLinear buffers).  ``work``: optional workspace from
+    ``decode_workspace`` (lets batches of 5..16 split the columns of layers
+    with few row tiles over several workgroups); calls sharing one must not
+    overlap in time."""
     _require(len(layers) > 0, "no layers")
     _require(x.dim() == 2 and x.dtype in (torch.float16, torch.bfloat16) and x.is_contiguous(),
              "x must be a contiguous 2-D fp16/bf16 tensor")
@@ -129,7 +140,8 @@ def linear_forward_multi(layers, codes, x) -> torch.Tensor:
         rc = lib.eptq_e8d4_forward_multi(len(layers), arr, _ptr(codes),
                                          EPTQ_F32 if codes.dtype == torch.float32 else EPTQ_F16, _ptr(x),
                                          EPTQ_BF16 if x.dtype == torch.bfloat16 else EPTQ_F16, N, B,
-                                         _ptr(y), off, stream)
+                                         _ptr(y), off, _ptr(work), 0 if work is None else work.numel(),
+                                         stream)
     _lib.check(rc, "eptq_e8d4_forward_multi")
     return y
 

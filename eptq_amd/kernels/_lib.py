@@ -23,7 +23,8 @@ SIGNATURES = {
     "eptq_last_error": ([], ctypes.c_char_p),
     "eptq_e8d4_forward": ([_P, _P, _I, _P, _P, _P, _I, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _P], _I),
     "eptq_e8_forward": ([_P, _P, _I, _P, _P, _P, _I, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _P], _I),
-    "eptq_e8d4_forward_multi": ([_I, _P, _P, _I, _P, _I, _I, _I, _P, _I, _P], _I),
+    "eptq_e8d4_forward_multi": ([_I, _P, _P, _I, _P, _I, _I, _I, _P, _I, _P, ctypes.c_longlong, _P], _I),
+    "eptq_e8d4_work_bytes": ([], ctypes.c_longlong),
     "eptq_e8d4_chain_create": ([_I, _P, _P, _I, ctypes.POINTER(_P)], _I),
     "eptq_e8d4_chain_run": ([_P, _P], _I),
     "eptq_e8d4_chain_check": ([_P], _I),

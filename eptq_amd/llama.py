@@ -27,7 +27,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from .kernels import _lib
+from .kernels import _lib, decode_workspace
 from .kernels.linear import EPTQLinear, EPTQMultiLinear
 from .quantizers import E8D4Quantizer
 from .synthetic import make_layer
@@ -210,6 +210,9 @@ class QuantLlama(nn.Module):
         if self.split_attention:
             nbytes = _lib.load().eptq_llama_attn_work_bytes(batch, cfg.heads)
             self.attn_work = torch.zeros(nbytes, dtype=torch.uint8, device=device)
+        # Split-K workspace of the decode Linears (batches of 5..16): the
+        # decode step's launches run one after another on one stream.
+        self.lin_work = decode_workspace(device)
 
     def forward_tokens(self, ids, pos):
         """ids: (B, T) int64, pos: (T,) int64 positions -> logits (B, T, vocab)."""
@@ -225,6 +228,20 @@ class QuantLlama(nn.Module):
         x = self.norm(x)
         return self.lm_head(x)
 
+    def _lin(self, mod, x):
+        """mod(x) for a decode step: the E8-D4 parts of ``mod`` in one launch
+        of the multi-layer entry point, with the step's split-K workspace."""
+        arr, width = _cached_array(mod)
+        B, N = x.shape
+        y = torch.empty((B, width), dtype=x.dtype, device=x.device)
+        work = getattr(self, "lin_work", None)
+        rc = _lib.load().eptq_e8d4_forward_multi(
+            len(arr), arr, _parts(mod)[0]._codebook.data_ptr(), _lib.EPTQ_F16, x.data_ptr(), _lib.EPTQ_F16,
+            N, B, y.data_ptr(), width, None if work is None else work.data_ptr(),
+            0 if work is None else work.numel(), _stream(x))
+        _lib.check(rc, "eptq_e8d4_forward_multi")
+        return y
+
     def _norm_into(self, mod, x, delta, w):
         """mod(RMSNorm(x + delta)) and the residual x + delta (a new tensor when
         fused; x itself, updated in place, on the separate-launch path)."""
@@ -235,7 +252,7 @@ class QuantLlama(nn.Module):
             except _lib.EptqError as e:
                 if e.code != _lib.EPTQ_EUNSUPPORTED:
                     raise
-        return mod(rmsnorm_(x, delta, w, self.cfg.eps)), x
+        return self._lin(mod, rmsnorm_(x, delta, w, self.cfg.eps)), x
 
     def decode_tokens(self, tok, pos):
         """One token per sequence: tok (B, 1) int64, pos (1,) int64 on the device
@@ -261,9 +278,9 @@ class QuantLlama(nn.Module):
                                           None if self.attn_work is None else self.attn_work.data_ptr(),
                                           _stream(x))
             _lib.check(rc, "eptq_llama_rope_attn")
-            o = layer.o_proj(att)
+            o = self._lin(layer.o_proj, att)
             gu, x = self._norm_into(layer.gate_up_proj, x, o, ln2)
-            delta = layer.down_proj(silu_mul(gu))
+            delta = self._lin(layer.down_proj, silu_mul(gu))
         h = rmsnorm_(x, delta, self.norm.weight, cfg.eps)
         return self.lm_head(h)
 

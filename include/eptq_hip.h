@@ -89,10 +89,20 @@ typedef struct {
  * scales.  No counterpart in the reference, whose decoder calls one
  * EPTQLinear per projection (kernels/linear.py:154-212); its callers are
  * decode steps that want fewer launches per token.
+ *
+ * work: NULL, or a 16-byte aligned device buffer of work_bytes bytes,
+ * zero-filled before its first use (eptq_e8d4_work_bytes() bytes cover every
+ * launch).  With it, batches of 5..16 on layers with few 64-row tiles have
+ * each tile's columns split over up to 4 workgroups, whose fp32 partial sums
+ * meet in the buffer; the kernel leaves its counters at zero.  Calls that
+ * share a buffer must not run at the same time.
  */
 int eptq_e8d4_forward_multi(int n_layers, const eptq_layer* layers, const void* codes,
                             int codes_dtype, const void* x, int x_dtype, int N, int B, void* y,
-                            int ldy, void* stream);
+                            int ldy, void* work, long long work_bytes, void* stream);
+
+/* Bytes of the eptq_e8d4_forward_multi workspace for the current device. */
+long long eptq_e8d4_work_bytes(void);
 
 /*
  * Decode chain: a sequence of batch-1 E8-D4 stages run by one persistent

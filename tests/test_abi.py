@@ -110,14 +110,16 @@ def test_multi_entry_point_validates_every_layer(lib):
     good = L(16, 16, 16, None, None, 16, None, None, 0, 4, 0)
     arr = (L * 2)(good, L(16, 16, 16, None, None, 16, None, None, 0, 4, 32))
     f = lib.eptq_e8d4_forward_multi
-    assert f(0, arr, 16, 0, 16, 0, 64, 1, 16, 64, None) == _lib.EPTQ_EINVAL
-    assert f(2, arr, 16, 0, 16, 0, 64, 1, 16, 48, None) == _lib.EPTQ_EINVAL   # 2nd layer past ldy
+    assert f(0, arr, 16, 0, 16, 0, 64, 1, 16, 64, None, 0, None) == _lib.EPTQ_EINVAL
+    assert f(2, arr, 16, 0, 16, 0, 64, 1, 16, 48, None, 0, None) == _lib.EPTQ_EINVAL   # 2nd layer past ldy
     assert "outside a y row" in lib.eptq_last_error().decode()
     bad = (L * 2)(good, L(None, 16, 16, None, None, 16, None, None, 0, 4, 32))
-    assert f(2, bad, 16, 0, 16, 0, 64, 1, 16, 64, None) == _lib.EPTQ_EINVAL
+    assert f(2, bad, 16, 0, 16, 0, 64, 1, 16, 64, None, 0, None) == _lib.EPTQ_EINVAL
     odd = (L * 2)(good, L(16, 16, 16, None, None, 16, None, None, 0, 4, 34))
-    assert f(2, odd, 16, 0, 16, 0, 64, 1, 16, 72, None) == _lib.EPTQ_EINVAL
-    assert f(2, arr, 16, 0, None, 0, 64, 0, None, 64, None) == _lib.EPTQ_OK   # B = 0
+    assert f(2, odd, 16, 0, 16, 0, 64, 1, 16, 72, None, 0, None) == _lib.EPTQ_EINVAL
+    assert f(2, arr, 16, 0, None, 0, 64, 0, None, 64, None, 0, None) == _lib.EPTQ_OK   # B = 0
+    assert f(2, arr, 16, 0, 16, 0, 64, 1, 16, 64, 8, 1024, None) == _lib.EPTQ_EINVAL   # work misaligned
+    assert lib.eptq_e8d4_work_bytes() > 0
 
 
 def test_llama_ops_reject_invalid_arguments(lib):

@@ -90,3 +90,50 @@ def test_mfma_decode_batch_rows_independent():
     for b in (0, 7, 15):
         y1 = _run(qd, x[b:b + 1])
         assert rel_l2(y16[b:b + 1], y1) < 2e-3, b
+
+
+@pytest.mark.parametrize("out,inp,B,qb", [
+    (4096, 4096, 8, None),     # 64 tiles: columns split over 4 workgroups
+    (1024, 11008, 16, 128),
+    (520, 776, 6, None),       # 13 column blocks over 4 parts: some waves get none
+])
+def test_mfma_decode_split_columns(out, inp, B, qb):
+    """With a workspace, a layer with few row tiles has each tile's columns
+    split over several workgroups: the result matches the oracle and the
+    unsplit launch (up to fp32 summation order), repeated calls are
+    bit-identical, the counters are back at zero after each call, and graph
+    replays (eager calls in between) reproduce the eager result."""
+    from eptq_amd.kernels import decode_workspace
+    print(f"mfma decode split columns {out}x{inp} B={B} qb={qb}", flush=True)
+    q = E8D4Quantizer(radius=1.75)
+    qd = make_layer(out, inp, seed=out + 3 * inp, percmask=0.002, bias=True, qb_size=qb)
+    lin = EPTQLinear.from_quantized_data(qd, q, "e8_d4").cuda()
+    layers = [dict(Q=lin.Q, g=lin.g, h=lin.h, O_vals=lin.O_vals, O_col=lin.O_col, O_row_ptr=lin.O_row_ptr,
+                   bias=lin.bias, S_group=lin.S_group)]
+    x = make_x(B, inp, seed=9).cuda()
+    work = decode_workspace(x.device)
+    y0 = linear_forward_multi(layers, lin._codebook, x)
+    y1 = linear_forward_multi(layers, lin._codebook, x, work=work)
+    torch.cuda.synchronize()
+    ref = _ref(qd, x.cpu())
+    assert rel_l2(y1.float().cpu().numpy(), ref) <= TOL
+    assert rel_l2(y1.float().cpu().numpy(), y0.float().cpu().numpy()) < 1e-3
+    assert int(work[:65536].view(torch.int32).abs().sum()) == 0
+    y2 = linear_forward_multi(layers, lin._codebook, x, work=work)
+    assert torch.equal(y1, y2)
+    yg = torch.empty_like(y1)
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            yg.copy_(linear_forward_multi(layers, lin._codebook, x, work=work))
+    torch.cuda.current_stream().wait_stream(s)
+    for rep in range(3):
+        yg.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(yg, y1), rep
+        assert torch.equal(linear_forward_multi(layers, lin._codebook, x, work=work), y1), rep
+    assert int(work[:65536].view(torch.int32).abs().sum()) == 0
