@@ -27,6 +27,11 @@ JSON fields beyond the driver contract:
 * ``e2e`` — tokens/s of the synthetic Llama-2-7B (every decoder Linear a
   synthetic E8-D4 layer): 128-token prompt, greedy
   decode, graph-captured step, prefill untimed, batch 1 and 8.
+* ``decode_batches`` — the decode-step Linear units (q|k|v, o, gate|up,
+  down) of Llama-2-7B at batch 1 and 8 and of
+  Llama-3-8B with S_group qb=128 at batch 1, 4 and 16 (configuration 2), one
+  launch each with the decode workspace: microseconds and algorithmic GB/s.
+  Batches of 5..16 run the matrix-core decode kernel.
 * ``prefill`` — the MFMA GEMM on the Llama-2-13B shapes at 2048 tokens
   TFLOP/s and fraction of the 2.5 PFLOP/s fp16
   dense MFMA peak.
@@ -340,6 +345,91 @@ def e2e_decode(torch, dev, batches=(1, 8), new_tokens=256, prompt_len=128):
     return res
 
 
+LLAMA3_8B_QB = 128
+
+
+def decode_batches(torch, dev, stream_bytes=320 << 20):
+    """Decode-step Linear units at the batch sizes of configurations 1 and 2:
+    synthetic Llama-2-7B (B = 1, 8) and Llama-3-8B with S_group qb=128
+    (B = 1, 4, 16).  Each unit is one eptq_e8d4_forward_multi launch with the
+    decode workspace (q|k|v and gate|up as multi-layer launches).  Every unit
+    is built as enough distinct copies (different seeds) to exceed
+    ``stream_bytes`` of indices, more than the 256 MB MALL, and the copies are
+    launched back to back with HIP events around the whole group, as a decode
+    step streams distinct layers.  B = 1..4 run the vector decode kernel,
+    5..16 the matrix-core one."""
+    from eptq_amd.kernels import _lib, decode_workspace
+    from eptq_amd.quantizers import E8D4Quantizer
+    from eptq_amd.synthetic import make_layer, make_x
+
+    codes = E8D4Quantizer(radius=1.75).flat_table().half().to(dev)
+    lib = _lib.load()
+    work = decode_workspace(dev)
+    stream = torch.cuda.current_stream()
+    models = {
+        "llama2_7b": (None, 0.001, (1, 8), [("q|k|v", [(4096, 4096)] * 3), ("o", [(4096, 4096)]),
+                                            ("gate|up", [(11008, 4096)] * 2), ("down", [(4096, 11008)])]),
+        "llama3_8b_qb128": (LLAMA3_8B_QB, 0.002, (1, 4, 16),
+                            [("q|k|v", [(4096, 4096), (1024, 4096), (1024, 4096)]), ("o", [(4096, 4096)]),
+                             ("gate|up", [(14336, 4096)] * 2), ("down", [(4096, 14336)])]),
+    }
+    out = {}
+    for mname, (qb, p, batches, units) in models.items():
+        res = {}
+        for ui, (uname, shapes) in enumerate(units):
+            ubytes = sum(o // 8 * i * 2 for o, i in shapes)
+            copies = []
+            for c in range(-(-stream_bytes // ubytes)):
+                keep = []
+                for k, (o, i) in enumerate(shapes):
+                    qd = make_layer(o, i, seed=5000 + 1000 * c + 37 * ui + k, percmask=p, qb_size=qb, device=dev)
+                    r_, c_ = (qd.Q == 32767).nonzero(as_tuple=True)
+                    rp = torch.cat([torch.zeros(1, dtype=torch.int32, device=dev),
+                                    torch.bincount(r_, minlength=qd.Q.shape[0]).cumsum(0).to(torch.int32)])
+                    keep.append((qd, c_.to(torch.int32), rp))
+                arr = (_lib.EptqLayer * len(keep))()
+                off = 0
+                for k, (qd, oc, rp) in enumerate(keep):
+                    ng = 0 if qd.S_group is None else int(qd.S_group.shape[0])
+                    arr[k] = _lib.EptqLayer(qd.Q.data_ptr(), qd.g.data_ptr(), qd.h.data_ptr(),
+                                            qd.O.data_ptr() if qd.O.numel() else None,
+                                            oc.data_ptr() if oc.numel() else None, rp.data_ptr(), None,
+                                            None if qd.S_group is None else qd.S_group.data_ptr(), ng,
+                                            qd.Q.shape[0], off)
+                    off += 8 * qd.Q.shape[0]
+                copies.append((keep, arr))
+            N = shapes[0][1]
+            width = sum(o for o, _ in shapes)
+            for B in batches:
+                x = make_x(B, N, seed=B, device=dev)
+                y = torch.empty((B, width), dtype=torch.float16, device=dev)
+
+                def f():
+                    for keep, arr in copies:
+                        rc = lib.eptq_e8d4_forward_multi(len(keep), arr, codes.data_ptr(), _lib.EPTQ_F16,
+                                                         x.data_ptr(), _lib.EPTQ_F16, N, B, y.data_ptr(), width,
+                                                         work.data_ptr(), work.numel(), stream.cuda_stream)
+                        if rc:
+                            _lib.check(rc, "eptq_e8d4_forward_multi")
+                f()
+                d, _ = event_timed(torch, [f, f, f], stream)
+                us = statistics.median(d) * 1e3 / len(copies)
+                nbytes = sum(algo_bytes(8 * qd.Q.shape[0], qd.Q.shape[1], B, int(qd.O.shape[0]),
+                                        n_groups=0 if qd.S_group is None else int(qd.S_group.shape[0]))
+                             for qd, _, _ in copies[0][0])
+                res[f"{uname} B={B}"] = {"shape": " + ".join(f"{o}x{i}" for o, i in shapes), "us": round(us, 2),
+                                         "gbs": round(nbytes / (us * 1e-6) / 1e9, 1),
+                                         "kernel": "k_decode_mfma" if B >= 5 else DECODE_KERNEL}
+                del x, y
+            del copies
+            torch.cuda.empty_cache()
+        out[mname] = res
+    out["note"] = ("per launch: HIP events around %d MB+ of distinct copies of the unit launched back to "
+                   "back (median of 3); gbs = algorithmic bytes (indices, S_group, CSR, scales, x, y) / time"
+                   % (stream_bytes >> 20))
+    return out
+
+
 def prefill_gemm(torch, dev, T=2048, reps=10):
     from eptq_amd.kernels import _lib
     from eptq_amd.quantizers import E8D4Quantizer
@@ -382,6 +472,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 --pmc passes")
     ap.add_argument("--no-e2e", action="store_true")
+    ap.add_argument("--no-batches", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--pmc-timeout", type=int, default=240)
     ap.add_argument("--probe-traffic", action="store_true", help=argparse.SUPPRESS)
@@ -516,6 +607,8 @@ def main():
                               "ms_per_step": round(ms_separate, 5),
                               "gbs": round(step_bytes / (ms_separate * 1e-3) / 1e9, 2)},
     }
+    if not args.no_batches:
+        rec["decode_batches"] = decode_batches(torch, dev)
     if not args.no_e2e:
         rec["e2e"] = e2e_decode(torch, dev)
         print(f"# e2e: {rec['e2e']}", file=sys.stderr, flush=True)
