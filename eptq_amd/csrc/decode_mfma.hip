@@ -54,7 +54,7 @@ constexpr int kDepth = 6;       // blocks of indices and activations in flight p
 constexpr int kEarly = 2;       // of which issued before the activation-scale pass
 constexpr int kEntCap = 256;    // critical blocks of a tile prefetched before the column loop
 constexpr int kRedLd = 68;      // floats per batch row of a wave's partial sums
-constexpr int kS = 8;           // column waves per workgroup
+constexpr int kS = 8;           // column waves per workgroup (one workgroup per CU)
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p, int bytes) {
   return __builtin_amdgcn_make_buffer_rsrc((void*)p, (short)0, bytes, kBufferWord3);
@@ -104,14 +104,15 @@ __host__ __device__ inline int padded_cols(int N) { return (N + kBlk - 1) / kBlk
 
 // Dynamic LDS: hs[Np] = fp16(h·2^-e) and, with S_group, hss[Np] = fp16(hs·S)
 // during the column loop; the partial sums red[S][16][kRedLd] afterwards.
-__host__ __device__ inline size_t dyn_bytes(int N, bool has_s) {
+__host__ __device__ inline size_t dyn_bytes(int N, bool has_s, int S) {
   const size_t act = (size_t)padded_cols(N) * 2 * (has_s ? 2 : 1);
-  const size_t red = (size_t)kS * 16 * kRedLd * 4;
+  const size_t red = (size_t)S * 16 * kRedLd * 4;
   return act > red ? act : red;
 }
 
 template <int S, bool HAS_S>
-__global__ __launch_bounds__((S + 1) * 64) void k_decode_mfma(MultiArgs ma, int P, int* wcnt, float* wpart) {
+// At most 168 VGPRs (3 waves per SIMD): one 9-wave workgroup per CU.
+__global__ __launch_bounds__((S + 1) * 64, 3) void k_decode_mfma(MultiArgs ma, int P, int* wcnt, float* wpart) {
   constexpr int NT = (S + 1) * 64;
   __shared__ f16x4 tab[512];
   // The tile's critical blocks as the output stage reads them: O, and the
@@ -377,30 +378,38 @@ __global__ __launch_bounds__((S + 1) * 64) void k_decode_mfma(MultiArgs ma, int 
   }
   __syncthreads();
 
-  // ---- output: thread t < 512 -> batch row t/32, rows 2(t%32), +1 ----------
-  const int b = (tid >> 5) & 15, r = (tid & 31) * 2;
-  const bool ok = tid < 512 && b < B && orow < 8 * M;
-  float s0 = 0.0f, s1 = 0.0f;
-  {
-    if (ok) {
+  // ---- output: item t (< 512) -> batch row t/32, rows 2(t%32), +1; thread
+  // tid takes items tid, tid + NT (NT is a multiple of 32: one row pair).
+  constexpr int kItems = (512 + NT - 1) / NT;
+  const int r = (tid & 31) * 2;
+  const int br = r >> 3, k = r & 7;
+  const h2 t5p = {t5[k & 3], t5[(k + 1) & 3]};
+  float s0[kItems], s1[kItems];
+  bool ok[kItems];
+#pragma unroll
+  for (int it = 0; it < kItems; ++it) {
+    const int oi = tid + NT * it, b = (oi >> 5) & 15;
+    ok[it] = oi < 512 && b < B && orow < 8 * M;
+    s0[it] = 0.0f;
+    s1[it] = 0.0f;
+    if (ok[it]) {
+      float t0 = 0.0f, t1 = 0.0f;
 #pragma unroll
       for (int w = 0; w < S; ++w) {
         const float2 p = *(const float2*)&red[w][b][r];
-        s0 += p.x;
-        s1 += p.y;
+        t0 += p.x;
+        t1 += p.y;
       }
       // Critical blocks of this block row: rows k, k+1 of each O (one 4-byte
       // read), two entries per step so the LDS reads of one overlap the other.
-      const int br = r >> 3, k = r & 7;
       const int e0 = erow[br], e1 = erow[br + 1];
       const int es = e1 < kEntCap ? e1 : kEntCap;
-      const h2 t5p = {t5[k & 3], t5[(k + 1) & 3]};
       auto corr1 = [&](int e) {
         const h2 o = __builtin_bit_cast(h2, *((const uint32_t*)&eov[e] + (k >> 1)));
         const float xo = (float)as_f16(exo[e][b]);
         const float xm = HAS_S ? (float)as_f16(exm[HAS_S ? e : 0][b]) : xo;
-        s0 += (float)o[0] * xo - (float)t5p[0] * xm;
-        s1 += (float)o[1] * xo - (float)t5p[1] * xm;
+        t0 += (float)o[0] * xo - (float)t5p[0] * xm;
+        t1 += (float)o[1] * xo - (float)t5p[1] * xm;
       };
       int e = e0;
       for (; e + 1 < es; e += 2) {
@@ -418,9 +427,11 @@ __global__ __launch_bounds__((S + 1) * 64) void k_decode_mfma(MultiArgs ma, int 
         const f16 h1 = as_f16(gp((const uint16_t*)a.h)[col]) * down;
         const float xo = (float)(f16)(x16 * h1);
         const float xm = HAS_S ? (float)(f16)(x16 * (f16)(h1 * as_f16(gp((const uint16_t*)a.S)[(size_t)grp * N + col]))) : xo;
-        s0 += (float)o[k] * xo - (float)t5p[0] * xm;
-        s1 += (float)o[k + 1] * xo - (float)t5p[1] * xm;
+        t0 += (float)o[k] * xo - (float)t5p[0] * xm;
+        t1 += (float)o[k + 1] * xo - (float)t5p[1] * xm;
       }
+      s0[it] = t0;
+      s1[it] = t1;
     }
   }
   // Split columns: every part leaves its partial sums (device-coherent
@@ -430,8 +441,10 @@ __global__ __launch_bounds__((S + 1) * 64) void k_decode_mfma(MultiArgs ma, int 
   bool fin = true;
   if (P > 1) {
     __shared__ int last_part;
-    float* base = wpart + (size_t)tile_g * P * (kPartBytes / 4) + b * 64 + r;
-    if (ok) st_pair(base + part * (kPartBytes / 4), s0, s1);
+    float* base = wpart + (size_t)tile_g * P * (kPartBytes / 4) + r;
+#pragma unroll
+    for (int it = 0; it < kItems; ++it)
+      if (ok[it]) st_pair(base + part * (kPartBytes / 4) + (((tid + NT * it) >> 5) & 15) * 64, s0[it], s1[it]);
     __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
     __syncthreads();
     if (tid == 0) {
@@ -441,29 +454,38 @@ __global__ __launch_bounds__((S + 1) * 64) void k_decode_mfma(MultiArgs ma, int 
     }
     __syncthreads();
     fin = last_part != 0;
-    if (fin && ok) {
-      float t0 = 0.0f, t1 = 0.0f;
-      for (int q = 0; q < P; ++q) {
-        float2 v = make_float2(s0, s1);
-        if (q != part) v = ld_pair(base + q * (kPartBytes / 4));
-        t0 += v.x;
-        t1 += v.y;
+    if (fin) {
+#pragma unroll
+      for (int it = 0; it < kItems; ++it) {
+        if (!ok[it]) continue;
+        const int b = ((tid + NT * it) >> 5) & 15;
+        float t0 = 0.0f, t1 = 0.0f;
+        for (int q = 0; q < P; ++q) {
+          float2 v = make_float2(s0[it], s1[it]);
+          if (q != part) v = ld_pair(base + q * (kPartBytes / 4) + b * 64);
+          t0 += v.x;
+          t1 += v.y;
+        }
+        s0[it] = t0;
+        s1[it] = t1;
       }
-      s0 = t0;
-      s1 = t1;
     }
   }
-  if (fin && ok) {
+  if (fin) {
     const h2 gg = __builtin_bit_cast(h2, gpair), bb = __builtin_bit_cast(h2, bpair);
-    const float y0 = s0 * out_scale * (float)gg[0] + (float)bb[0];
-    const float y1 = s1 * out_scale * (float)gg[1] + (float)bb[1];
-    const uint32_t pk = (uint32_t)bits((f16)y0) | ((uint32_t)bits((f16)y1) << 16);
-    *gp((uint32_t*)(a.y + (size_t)b * a.ldy + orow)) = pk;
+#pragma unroll
+    for (int it = 0; it < kItems; ++it) {
+      if (!ok[it]) continue;
+      const int b = ((tid + NT * it) >> 5) & 15;
+      const float y0 = s0[it] * out_scale * (float)gg[0] + (float)bb[0];
+      const float y1 = s1[it] * out_scale * (float)gg[1] + (float)bb[1];
+      const uint32_t pk = (uint32_t)bits((f16)y0) | ((uint32_t)bits((f16)y1) << 16);
+      *gp((uint32_t*)(a.y + (size_t)b * a.ldy + orow)) = pk;
+    }
   }
 }
 
-// Parts per tile: as many as keep the grid within one workgroup per CU (one
-// 9-wave workgroup is what a CU holds at this kernel's register count: a
+// Parts per tile: as many as keep the grid within one workgroup per CU (a
 // second round of workgroups would double the time), within the workspace
 // (none: one part).
 inline int parts_for(int tiles, void* work, long long work_bytes) {
@@ -487,7 +509,7 @@ int launch_t(const LinearArgs* l, int n, hipStream_t s, void* work, long long wo
     ma.start[k + 1] = ma.start[k] + (k < n ? (l[k].M + kTile - 1) / kTile * P : 0);
   }
   auto kern = k_decode_mfma<S, HAS_S>;
-  const size_t dyn = dyn_bytes(l[0].N, HAS_S);
+  const size_t dyn = dyn_bytes(l[0].N, HAS_S, S);
   static size_t attr = 0;
   if (dyn > attr) {
     if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)dyn) != hipSuccess)
@@ -522,7 +544,10 @@ int launch_decode_mfma_multi(const LinearArgs* l, int n, hipStream_t s, void* wo
   }
   if ((long)(a.B - 1) * a.ldx + a.N >= (1L << 30)) return -1;
   // The activation-scale rows and the staged entries share the 160 KB of LDS.
-  if (dmf::dyn_bytes(a.N, a.S != nullptr) > 120 * 1024) return -1;
+  if (dmf::dyn_bytes(a.N, a.S != nullptr, dmf::kS) > 120 * 1024) return -1;
+  // (Two 6-wave workgroups per CU for layers with more tiles than CUs, so
+  // that they run in one round, measured slower than two rounds of 9-wave
+  // workgroups: gate|up 11008x4096 at B=8 24.6 us against 22.2 us.)
   return a.S ? dmf::launch_t<dmf::kS, true>(l, n, s, work, work_bytes)
              : dmf::launch_t<dmf::kS, false>(l, n, s, work, work_bytes);
 }
