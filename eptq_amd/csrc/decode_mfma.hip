@@ -36,17 +36,20 @@
 // column for each batch row) into LDS while the column waves run, and the
 // output stage adds O·(x h) minus what the marker contributed.
 
-#include "decode_layer.h"
+#include "mfma_decode.h"
 
 namespace eptq {
 namespace dmf {
 
 using dec::gp;
 using dec::h2;
-using dec::kBufferWord3;
 using dec::kNonTemporal;
-using dec::perm;
 using dec::pk_mul;
+using mdec::as_f16;
+using mdec::bits;
+using mdec::ld16;
+using mdec::ld2;
+using mdec::rsrc;
 
 constexpr int kTile = 8;        // block rows per tile (64 output rows)
 constexpr int kBlk = 64;        // columns per block: 4 K groups x 16
@@ -56,31 +59,6 @@ constexpr int kEntCap = 256;    // critical blocks of a tile prefetched before t
 constexpr int kRedLd = 68;      // floats per batch row of a wave's partial sums
 constexpr int kS = 8;           // column waves per workgroup (one workgroup per CU)
 
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p, int bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc((void*)p, (short)0, bytes, kBufferWord3);
-}
-template <int AUX = 0>
-__device__ __forceinline__ u32x4 ld16(__amdgpu_buffer_rsrc_t r, int off) {
-  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, AUX));
-}
-__device__ __forceinline__ uint16_t ld2(__amdgpu_buffer_rsrc_t r, int off) {
-  return (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
-}
-// Bitfield insert with a per-lane mask: (mask & a) | (~mask & b).
-__device__ __forceinline__ uint32_t bfi_v(uint32_t mask, uint32_t a, uint32_t b) {
-  uint32_t r;
-  asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "v"(mask), "v"(a), "v"(b));
-  return r;
-}
-// (t >> 16) & 0xFF8 in one op (SDWA word select of the second operand).
-__device__ __forceinline__ uint32_t hi_addr(uint32_t t) {
-  uint32_t r;
-  asm("v_and_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:WORD_1"
-      : "=v"(r) : "s"(0xFF8u), "v"(t));
-  return r;
-}
-__device__ __forceinline__ f16 as_f16(uint16_t v) { return __builtin_bit_cast(f16, v); }
-__device__ __forceinline__ uint16_t bits(f16 v) { return __builtin_bit_cast(uint16_t, v); }
 
 // Split-K workspace: per-tile arrival counters, then the fp32 partial sums
 // [tile][part][16][64] of tiles whose columns are split over P workgroups.
@@ -273,12 +251,7 @@ __global__ __launch_bounds__((S + 1) * 64, 3) void k_decode_mfma(MultiArgs ma, i
   f32x4 acc[4];
   if (wave < S) {
     // ---- column wave --------------------------------------------------------
-    // Byte addresses of the two indices of a word w in this lane's half:
-    //   rows 0-3: t = w >> 4;  rows 4-7: t = bfi(0x0C000C00, w >> 4, w << 3)
-    // (bits 10-11 of each half from v >> 4, bits 3-9 = (v & 127) << 3), then
-    // (t & 0xFF8) for the low index and ((t >> 16) & 0xFF8) for the high one.
-    const uint32_t tmask = (i & 1) ? 0x0C000C00u : 0xFFFFFFFFu;
-    const uint32_t tsh = (i & 1) ? 3u : 0u;
+    const mdec::Half half(i);
 #pragma unroll
     for (int c = 0; c < 4; ++c) acc[c] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
 
@@ -290,25 +263,11 @@ __global__ __launch_bounds__((S + 1) * 64, 3) void k_decode_mfma(MultiArgs ma, i
 #pragma unroll
         for (int d = 0; d < 4; ++d) bx[d] = pk_mul(x[g2][d], sc[d]);
         u32x2 lo[4], hi[4];
+        half.lookup(q[g2], tabB, lo, hi);
 #pragma unroll
-        for (int d = 0; d < 4; ++d) {
-          const uint32_t w0 = q[g2][d];
-          const uint32_t t = bfi_v(tmask, w0 >> 4, w0 << tsh);
-          lo[d] = *(const u32x2*)(tabB + (t & 0xFF8u));
-          hi[d] = *(const u32x2*)(tabB + hi_addr(t));
-        }
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          u32x4 aw;
-#pragma unroll
-          for (int d = 0; d < 4; ++d) {
-            const uint32_t l = c < 2 ? lo[d][0] : lo[d][1];
-            const uint32_t h = c < 2 ? hi[d][0] : hi[d][1];
-            aw[d] = perm(h, l, (c & 1) ? 0x07060302u : 0x05040100u);
-          }
-          acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, aw),
+        for (int c = 0; c < 4; ++c)
+          acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, mdec::Half::operand(lo, hi, c)),
                                                           __builtin_bit_cast(f16x8, bx), acc[c], 0, 0, 0);
-        }
       }
     };
 

@@ -37,6 +37,7 @@ def _run(qd, x, kind="e8_d4", radius=1.75):
     (2048, 1024, 64, 0.01, False, 128),        # S_group, more critical blocks
     (512, 512, 17, 0.002, False, None),        # just above the matvec range
     (256, 4096, 1000, 0.05, True, 64),         # dense markers: > LDS entry cap per tile
+    (1152, 1024, 200, 0.002, True, 128),       # 144 Q-rows: 9 row tiles, S_group and bias
 ])
 def test_gemm_rel_l2(out, inp, T, p, bias, qb):
     print(f"gemm {out}x{inp} T={T} p={p} bias={bias} qb={qb}", flush=True)
