@@ -90,16 +90,29 @@ __global__ __launch_bounds__(kT) void k_rmsnorm(f16* __restrict__ x, const f16* 
 }
 
 // Decode attention for head h of batch row b, head_dim D = 128, positions
-// 0..pos split over ns workgroups (blockIdx.z): each computes the softmax
-// partial of its positions (local max m, sum l of exp(s - m), o = Σ exp(s - m)
-// V), and the last of the ns to finish (an atomic count per (b, h)) rescales
-// and sums them:  out = Σ_s o_s e^(m_s - M) / Σ_s l_s e^(m_s - M), M = max m_s.
-// Partials move through device-coherent (sc1) stores and loads, and each
-// split waits for its stores (vmcnt) before it counts itself, so no cache
+// 0..pos split over ns workgroups (blockIdx.z).
+//
+// Layout: thread (pg = t / 16, dc = t % 16) holds dims 8dc..8dc+7 of the
+// cache rows p ≡ pg (mod 16) of a 256-row chunk, so one wave load covers four
+// whole 256-byte rows (K as well as V: no lane strides across rows).  A
+// row's score is the sum of its 16 lanes' partial dot products; the 16 rows of
+// a lane group are reduced together by a transposed butterfly (15 DPP adds),
+// after which lane dc holds the score of row pg + 16 dc.  Each lane group keeps
+// its own online softmax (running max m, rescaled sum l and o = Σ e^(s-m) V),
+// so no workgroup-wide barrier separates the chunks; the 16 groups are
+// combined once at the end:  out = Σ_g o_g e^(m_g - M) / Σ_g l_g e^(m_g - M).
+//
+// Unsplit (ns = 1) the first 256 rows are requested at entry, before pos has
+// arrived: rows at or past pos are loaded but not used.  Split, the workgroup
+// computes the same partial (M, l, o) over its positions [p0, p1), and the
+// last of the ns to finish (an atomic count per (b, h)) rescales and sums
+// them.  Partials move through device-coherent (sc1) stores and loads, and
+// each split waits for its stores (vmcnt) before it counts itself, so no cache
 // writeback or invalidate is needed across XCDs; the last split resets the
-// count to zero for the next call.  ns = 1 (no workspace) writes directly.
+// count to zero for the next call.
 // qkv: (B, (H + 2 Hk) D) = [q heads | k heads | v heads]; caches (B, Hk, L, D);
 // cos/sin: (L, D) fp32 (HF rotary layout: frequencies repeated over both halves).
+// pos outside [0, L): zero output, no cache access.
 constexpr int kPart = 2 + 128;   // floats per partial: m, l, o[128]
 
 __device__ __forceinline__ void st_coh(float* p, float v) {
@@ -109,136 +122,213 @@ __device__ __forceinline__ float ld_coh(const float* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Lane moves within each row of 16 lanes (gfx9 dpp_ctrl): lane i reads lane
+// i ^ 15 (row_mirror), i ^ 7 (row_half_mirror), i ^ 3 (quad_perm 3,2,1,0) or
+// i ^ 1 (quad_perm 1,0,3,2).  The four masks span all 16 lanes.
+constexpr int kX15 = 0x140, kX7 = 0x141, kX3 = 0x1B, kX1 = 0xB1;
+template <int CTRL>
+__device__ __forceinline__ float dpp16(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float max16(float v) {
+  v = fmaxf(v, dpp16<kX15>(v));
+  v = fmaxf(v, dpp16<kX7>(v));
+  v = fmaxf(v, dpp16<kX3>(v));
+  return fmaxf(v, dpp16<kX1>(v));
+}
+__device__ __forceinline__ float sum16(float v) {
+  v += dpp16<kX15>(v);
+  v += dpp16<kX7>(v);
+  v += dpp16<kX3>(v);
+  return v + dpp16<kX1>(v);
+}
+// One halving step of the transposed sum: lanes whose bit B (of lane & 15)
+// is clear keep values [0, n), the others [n, 2n), each adding its partner's
+// (lane ^ mask, which differs in bit B and agrees in the higher bits).
+template <int N, int CTRL>
+__device__ __forceinline__ void halve(float (&v)[16], bool hi) {
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    const float keep = hi ? v[i + N] : v[i], send = hi ? v[i] : v[i + N];
+    v[i] = keep + dpp16<CTRL>(send);
+  }
+}
+// v[u] = this lane's part of row u (u < 16) -> sum over the 16 lanes of row
+// (lane & 15).
+__device__ __forceinline__ float transpose_sum16(float (&v)[16], int l16) {
+  halve<8, kX15>(v, l16 & 8);
+  halve<4, kX7>(v, l16 & 4);
+  halve<2, kX3>(v, l16 & 2);
+  halve<1, kX1>(v, l16 & 1);
+  return v[0];
+}
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t cache_rsrc(const f16* p, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc((void*)p, (short)0, bytes, 0x00020000);
+}
+// Rows c + pg + 16u (u < 16), dims 8dc..: keys first (the scores need them
+// first), then values.  Offsets past the resource's size read as zero.
+__device__ __forceinline__ void load_rows(__amdgpu_buffer_rsrc_t rk, __amdgpu_buffer_rsrc_t rv, int c, int pg,
+                                          int dc, f16x8 (&kk)[16], f16x8 (&vv)[16]) {
+#pragma unroll
+  for (int u = 0; u < 16; ++u)
+    kk[u] = __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(rk, ((c + pg + 16 * u) * 128 + dc * 8) * 2, 0, 0));
+#pragma unroll
+  for (int u = 0; u < 16; ++u)
+    vv[u] = __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(rv, ((c + pg + 16 * u) * 128 + dc * 8) * 2, 0, 0));
+}
+
 __global__ __launch_bounds__(kT) void k_rope_attn(const f16* __restrict__ qkv, const int64_t* __restrict__ posp,
                                                  const float* __restrict__ cosv, const float* __restrict__ sinv,
                                                  f16* __restrict__ kc, f16* __restrict__ vc, f16* __restrict__ out,
                                                  int H, int Hk, int L, float scale, float* __restrict__ part,
                                                  int* __restrict__ cnt) {
   constexpr int D = 128;
-  __shared__ float qs[D], ks[D], vs[D];
-  __shared__ float prob[1024];
-  __shared__ float sh[kT / 64];
+  __shared__ float probl[16][16];
   __shared__ float opart[16][D];
+  __shared__ float gmax[16], gsum[16];
   __shared__ int s_last;
   const int h = blockIdx.x, b = blockIdx.y, t = threadIdx.x;
   const int sp = blockIdx.z, ns = gridDim.z;
-  const int hk = h / (H / Hk);
-  const int64_t pos64 = *posp;
-  if (pos64 < 0 || pos64 >= L) {   // outside the cache: no cache access, zero output
-    if (sp == 0 && t < D) out[(size_t)b * H * D + (size_t)h * D + t] = (f16)0.0f;
-    return;
+  const int grp = H / Hk, hk = h / grp;
+  const int dc = t & 15, pg = t >> 4, d0 = dc * 8;
+  const size_t kvbase = ((size_t)b * Hk + hk) * L * D;
+  f16x8 ka[16], va[16];
+  {  // unsplit: rows 0..255 now (an empty resource when split)
+    const int bytes = ns == 1 ? L * D * 2 : 0;
+    load_rows(cache_rsrc(kc + kvbase, bytes), cache_rsrc(vc + kvbase, bytes), 0, pg, dc, ka, va);
   }
-  const int pos = (int)pos64;
-  // This split's positions [p0, p1) of 0..pos.
-  const int per = (pos + 1 + ns - 1) / ns;
-  const int p0 = sp * per;
-  const int p1 = p0 + per < pos + 1 ? p0 + per : pos + 1;
+  // This lane's 8 dims of q, k, v and the rotary partners (dims d ± 64).
   const size_t row = (size_t)b * (H + 2 * Hk) * D;
   const f16* q = qkv + row + (size_t)h * D;
   const f16* k = qkv + row + (size_t)(H + hk) * D;
   const f16* v = qkv + row + (size_t)(H + Hk + hk) * D;
-  if (t < D) {
-    qs[t] = (float)q[t];
-    ks[t] = (float)k[t];
-    vs[t] = (float)v[t];
-  }
-  __syncthreads();
-  float qr = 0.0f, kr = 0.0f;
-  if (t < D) {
-    const float c = cosv[(size_t)pos * D + t], s = sinv[(size_t)pos * D + t];
-    const float qrot = t < D / 2 ? -qs[t + D / 2] : qs[t - D / 2];
-    const float krot = t < D / 2 ? -ks[t + D / 2] : ks[t - D / 2];
-    // fp16 rounding of the rotated q and k, as a fp16 model holds them
-    qr = (float)(f16)(qs[t] * c + qrot * s);
-    kr = (float)(f16)(ks[t] * c + krot * s);
-  }
-  __syncthreads();
-  if (t < D) {
-    qs[t] = qr;
-    ks[t] = kr;
-  }
-  const size_t kvbase = ((size_t)b * Hk + hk) * L * D;
-  if (sp == 0 && h % (H / Hk) == 0 && t < D) {   // one writer per kv head
-    kc[kvbase + (size_t)pos * D + t] = (f16)kr;
-    vc[kvbase + (size_t)pos * D + t] = (f16)vs[t];
-  }
-  __syncthreads();
-
-  // Scores for positions p = p0 + t, + kT, ... < p1 (the current one from
-  // LDS): each thread reads its key rows with 16-byte loads, issued together.
-  float mx = -INFINITY;
-  for (int p = p0 + t; p < p1; p += kT) {
-    float s = 0.0f;
-    if (p == pos) {
-      for (int d = 0; d < D; ++d) s += qs[d] * ks[d];
-    } else {
-      const f16x8* kp = (const f16x8*)(kc + kvbase + (size_t)p * D);
-      f16x8 kv8[D / 8];
-#pragma unroll
-      for (int c = 0; c < D / 8; ++c) kv8[c] = kp[c];
-#pragma unroll
-      for (int c = 0; c < D / 8; ++c)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) s += qs[c * 8 + e] * (float)kv8[c][e];
-    }
-    s *= scale;
-    prob[p - p0] = s;
-    mx = fmaxf(mx, s);
-  }
-  mx = block_max(mx, sh);
-  float sum = 0.0f;
-  for (int p = p0 + t; p < p1; p += kT) {
-    const float e = __expf(prob[p - p0] - mx);
-    prob[p - p0] = e;
-    sum += e;
-  }
-  sum = block_sum(sum, sh);   // block_sum synchronizes: prob[] complete
-  // o = Σ_p prob[p] V[p]: thread (pg, dc) takes 8 dims dc·8.. of the
-  // positions p ≡ p0 + pg (mod 16), four rows in flight, then the 16 position
-  // groups are summed through LDS.
-  const int dc = t & 15, pg = t >> 4;
-  float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-  const f16* vb = vc + kvbase + dc * 8;
-  int p = p0 + pg;
-  for (; p + 48 < p1 && p + 48 < pos; p += 64) {
-    f16x8 v4[4];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) v4[u] = *(const f16x8*)(vb + (size_t)(p + 16 * u) * D);
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const float pr = prob[p + 16 * u - p0];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) acc[e] += pr * (float)v4[u][e];
-    }
-  }
-  for (; p < p1; p += 16) {
-    const float pr = prob[p - p0];
+  const f16x8 q8 = *(const f16x8*)(q + d0), qp8 = *(const f16x8*)(q + (d0 ^ 64));
+  const f16x8 k8 = *(const f16x8*)(k + d0), kp8 = *(const f16x8*)(k + (d0 ^ 64));
+  const f16x8 v8 = *(const f16x8*)(v + d0);
+  const int64_t pos64 = *posp;
+  const bool ok = pos64 >= 0 && pos64 < L;
+  const int pos = ok ? (int)pos64 : 0;
+  // This split's positions [p0, p1) of 0..pos.
+  const int per = (pos + 1 + ns - 1) / ns;
+  const int p0 = sp * per;
+  const int p1 = p0 + per < pos + 1 ? p0 + per : pos + 1;
+  const __amdgpu_buffer_rsrc_t rk = cache_rsrc(kc + kvbase, p1 * D * 2);
+  const __amdgpu_buffer_rsrc_t rv = cache_rsrc(vc + kvbase, p1 * D * 2);
+  if (ns > 1) load_rows(rk, rv, p0, pg, dc, ka, va);
+  // Rotary (q·cos + rotate_half(q)·sin), rounded to fp16 as a fp16 model
+  // holds the rotated q and k.
+  float qv[8], kv[8];
+  {
+    const float4* cr = (const float4*)(cosv + (size_t)pos * D + d0);
+    const float4* sr = (const float4*)(sinv + (size_t)pos * D + d0);
+    const float4 c0 = cr[0], c1 = cr[1], s0 = sr[0], s1 = sr[1];
+    const float cs[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+    const float sn[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+    const float sg = dc < 8 ? -1.0f : 1.0f;   // rotate_half: (-x2, x1)
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const float vv = p == pos ? vs[dc * 8 + e] : (float)vb[(size_t)p * D + e];
-      acc[e] += pr * vv;
+      qv[e] = (float)(f16)((float)q8[e] * cs[e] + sg * (float)qp8[e] * sn[e]);
+      kv[e] = (float)(f16)((float)k8[e] * cs[e] + sg * (float)kp8[e] * sn[e]);
     }
   }
+  if (ok && sp == 0 && h % grp == 0 && pg == 0) {   // one writer per kv head
+    f16x8 ko;
 #pragma unroll
-  for (int e = 0; e < 8; ++e) opart[pg][dc * 8 + e] = acc[e];
+    for (int e = 0; e < 8; ++e) ko[e] = (f16)kv[e];
+    *(f16x8*)(kc + kvbase + (size_t)pos * D + d0) = ko;
+    *(f16x8*)(vc + kvbase + (size_t)pos * D + d0) = v8;
+  }
+  // q as fp16 pairs (exact: it is fp16-rounded) for the dot2 products; the
+  // current row's k and v come from registers, not the cache.
+  f16x2 qh[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) qh[i] = f16x2{(f16)qv[2 * i], (f16)qv[2 * i + 1]};
+  float dself = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) dself += qv[e] * kv[e];
+  float m = -INFINITY, lsum = 0.0f;
+  float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  auto chunk = [&](int c, const f16x8(&kk)[16], const f16x8(&vv)[16]) {
+    float pt[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      float s = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) s = __builtin_amdgcn_fdot2(qh[i], f16x2{kk[u][2 * i], kk[u][2 * i + 1]}, s, false);
+      pt[u] = c + pg + 16 * u == pos ? dself : s;
+    }
+    float s = transpose_sum16(pt, dc) * scale;   // row c + pg + 16 dc
+    if (c + pg + 16 * dc >= p1) s = -INFINITY;
+    const float mn = fmaxf(m, max16(s));
+    const float alpha = mn == -INFINITY ? 1.0f : __expf(m - mn);
+    const float e = s == -INFINITY ? 0.0f : __expf(s - mn);
+    m = mn;
+    lsum = lsum * alpha + e;
+    // The group's 16 weights to every lane of the group (one wave: LDS
+    // operations of a wave complete in order).
+    probl[pg][dc] = e;
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    const float4* pr4 = (const float4*)probl[pg];
+    const float4 w0 = pr4[0], w1 = pr4[1], w2 = pr4[2], w3 = pr4[3];
+    const float w[16] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w,
+                         w2.x, w2.y, w2.z, w2.w, w3.x, w3.y, w3.z, w3.w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] *= alpha;
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      const int r = c + pg + 16 * u;
+      f16x8 x = r == pos ? v8 : vv[u];
+      if (r >= p1) x = f16x8{};   // rows past the range: weight 0, contents unknown
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[i] += w[u] * (float)x[i];
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+  };
+  if (p0 + 256 < p1) {   // a second chunk: requested before the first is used
+    f16x8 kb[16], vb[16];
+    load_rows(rk, rv, p0 + 256, pg, dc, kb, vb);
+    chunk(p0, ka, va);
+    for (int c = p0 + 256; c < p1; c += 256) {
+      chunk(c, kb, vb);
+      if (c + 256 < p1) load_rows(rk, rv, c + 256, pg, dc, kb, vb);
+    }
+  } else {
+    chunk(p0, ka, va);
+  }
+  // Combine the 16 lane groups.
+  const float lg = sum16(lsum);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) opart[pg][d0 + i] = acc[i];
+  if (dc == 0) {
+    gmax[pg] = m;
+    gsum[pg] = lg;
+  }
   __syncthreads();
-  float o = 0.0f;
+  float M = -INFINITY, o = 0.0f, l = 0.0f;
   if (t < D) {
 #pragma unroll
-    for (int g2 = 0; g2 < 16; ++g2) o += opart[g2][t];
+    for (int g = 0; g < 16; ++g) M = fmaxf(M, gmax[g]);
+#pragma unroll
+    for (int g = 0; g < 16; ++g) {
+      const float wg = gmax[g] == -INFINITY ? 0.0f : __expf(gmax[g] - M);
+      o += wg * opart[g][t];
+      l += wg * gsum[g];
+    }
   }
   f16* orow = out + (size_t)b * H * D + (size_t)h * D;
   if (ns == 1) {
-    if (t < D) orow[t] = (f16)(o / sum);
+    if (t < D) orow[t] = ok ? (f16)(o / l) : (f16)0.0f;
     return;
   }
-  // Publish this split's partial, then count it.
+  // Publish this split's partial (an empty split: M = -inf, l = o = 0), then
+  // count it.
   const int bh = b * H + h;
   float* mine = part + ((size_t)bh * ns + sp) * kPart;
   if (t < D) st_coh(mine + 2 + t, o);
   if (t == 0) {
-    st_coh(mine, mx);
-    st_coh(mine + 1, sum);
+    st_coh(mine, M);
+    st_coh(mine + 1, l);
   }
   __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): the stores are complete
   __syncthreads();
@@ -250,16 +340,17 @@ __global__ __launch_bounds__(kT) void k_rope_attn(const f16* __restrict__ qkv, c
   __syncthreads();
   if (!s_last) return;
   const float* all = part + (size_t)bh * ns * kPart;
-  float M = -INFINITY;
-  for (int s2 = 0; s2 < ns; ++s2) M = fmaxf(M, ld_coh(all + s2 * kPart));
-  float lsum = 0.0f, osum = 0.0f;
+  float Ms = -INFINITY;
+  for (int s2 = 0; s2 < ns; ++s2) Ms = fmaxf(Ms, ld_coh(all + s2 * kPart));
+  float lsum2 = 0.0f, osum = 0.0f;
   for (int s2 = 0; s2 < ns; ++s2) {
     const float* ps = all + s2 * kPart;
-    const float w = __expf(ld_coh(ps) - M);   // empty splits: m = -inf, weight 0
-    lsum += ld_coh(ps + 1) * w;
+    const float ms = ld_coh(ps);
+    const float w = ms == -INFINITY ? 0.0f : __expf(ms - Ms);   // empty splits weigh 0
+    lsum2 += ld_coh(ps + 1) * w;
     if (t < D) osum += ld_coh(ps + 2 + t) * w;
   }
-  if (t < D) orow[t] = (f16)(osum / lsum);
+  if (t < D) orow[t] = ok ? (f16)(osum / lsum2) : (f16)0.0f;
 }
 
 __global__ __launch_bounds__(kT) void k_silu_mul(const f16* __restrict__ gu, f16* __restrict__ a, int F) {
