@@ -182,11 +182,16 @@ bool overlaps(const void* a, const void* b, size_t bytes) {
 
 // Layers reading an activation that the decode kernel forms itself (prep 1:
 // residual add + RMSNorm); see LinearArgs.
+// pair: layers[0] = gate, layers[1] = up of equal M; y (B, 8M) = silu(gate) ⊙ up
+// (ldy = 8M, the layers' y offsets unused).
 int fused_linear(const char* fn, int n, const eptq_layer* layers, const void* codes, const void* x,
                  int ldx, int prep, const void* x2, const void* nw, float eps, void* xsum, int N, int B,
-                 void* y, int ldy, void* stream) {
+                 void* y, int ldy, void* stream, bool pair = false) {
   if (n < 1 || n > eptq::kMaxLayers || !layers) return fail(EPTQ_EINVAL, "%s: n_layers=%d (1..%d)", fn, n, eptq::kMaxLayers);
-  if (B < 0 || B > 8) return fail(B < 0 ? EPTQ_EINVAL : EPTQ_EUNSUPPORTED, "%s: B=%d (0..8)", fn, B);
+  if (pair && layers[0].M != layers[1].M)
+    return fail(EPTQ_EINVAL, "%s: gate M=%d and up M=%d differ", fn, layers[0].M, layers[1].M);
+  const int bmax = pair ? 2 : 8;
+  if (B < 0 || B > bmax) return fail(B < 0 ? EPTQ_EINVAL : EPTQ_EUNSUPPORTED, "%s: B=%d (0..%d)", fn, B, bmax);
   if (B > 0 && (!x || !y)) return fail(EPTQ_EINVAL, "%s: null input/y", fn);
   if (prep == 1 && !nw) return fail(EPTQ_EINVAL, "%s: null norm weight", fn);
   if ((x && !aligned16(x)) || (x2 && !aligned16(x2)) || (nw && !aligned16(nw)) || (xsum && !aligned16(xsum)))
@@ -200,10 +205,10 @@ int fused_linear(const char* fn, int n, const eptq_layer* layers, const void* co
     int rc = layer_args(fn, eptq::KIND_E8D4, L.Q, codes, EPTQ_F16, L.g, L.h, x, EPTQ_F16, L.O_vals, L.O_col,
                         L.O_row_ptr, L.bias, L.S_group, L.n_groups, L.M, N, B, &a[l]);
     if (rc) return rc;
-    if (L.y_offset < 0 || L.y_offset + 8LL * L.M > (long long)ldy || (L.y_offset & 3))
+    if (!pair && (L.y_offset < 0 || L.y_offset + 8LL * L.M > (long long)ldy || (L.y_offset & 3)))
       return fail(EPTQ_EINVAL, "%s: layer %d columns [%lld, %lld) outside a y row of %d (offset %% 4 == 0)",
                   fn, l, L.y_offset, L.y_offset + 8LL * L.M, ldy);
-    a[l].y = (uint16_t*)y + L.y_offset;
+    a[l].y = (uint16_t*)y + (pair ? 0 : L.y_offset);
     a[l].ldy = ldy;
     a[l].prep = prep;
     a[l].ldx = ldx;
@@ -213,8 +218,9 @@ int fused_linear(const char* fn, int n, const eptq_layer* layers, const void* co
     a[l].xsum = (uint16_t*)xsum;
   }
   if (B == 0) return EPTQ_OK;
-  if (eptq::launch_decode_e8d4_multi(a, n, (hipStream_t)stream) != 0)
-    return fail(EPTQ_EUNSUPPORTED, "%s: the decode kernel does not take N=%d B=%d here", fn, N, B);
+  const int lrc = pair ? eptq::launch_decode_e8d4_pair(a, (hipStream_t)stream)
+                       : eptq::launch_decode_e8d4_multi(a, n, (hipStream_t)stream);
+  if (lrc != 0) return fail(EPTQ_EUNSUPPORTED, "%s: the decode kernel does not take N=%d B=%d here", fn, N, B);
   return check_launch(fn);
 }
 
@@ -370,6 +376,13 @@ int eptq_llama_norm_linear(int n_layers, const eptq_layer* layers, const void* c
                            void* resid_out, int N, int B, void* y, int ldy, void* stream) {
   return fused_linear("eptq_llama_norm_linear", n_layers, layers, codes, resid, N, 1, delta, w, eps, resid_out,
                       N, B, y, ldy, stream);
+}
+
+int eptq_llama_norm_swiglu(const eptq_layer* gate_up, const void* codes, const void* resid, const void* delta,
+                           const void* w, float eps, void* resid_out, int N, int B, void* out, void* stream) {
+  if (!gate_up) return fail(EPTQ_EINVAL, "eptq_llama_norm_swiglu: null layers");
+  return fused_linear("eptq_llama_norm_swiglu", 2, gate_up, codes, resid, N, 1, delta, w, eps, resid_out, N, B, out,
+                      8 * gate_up[0].M, stream, true);
 }
 
 int eptq_e8d4_dequant(const void* Q, const void* codes_f32, const void* g, const void* h,

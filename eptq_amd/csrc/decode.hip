@@ -50,6 +50,46 @@ __global__ __launch_bounds__(kT) void k_decode_e8d4(MultiArgs ma) {
   layer.rows(st, sm, out_scale);
 }
 
+// One activation table of a pair, rounded up to 16 bytes (the tables are
+// read with 16-byte LDS loads).
+__host__ __device__ inline size_t pair_table_bytes(int N, int BT) { return (act_lds_bytes(N, BT) + 15) & ~(size_t)15; }
+
+// SwiGLU pair: layers ma.l[0] (gate) and ma.l[1] (up) of equal shape, every
+// workgroup serving the same rows of both (wave w: layer w % 2, row slot
+// w / 2); y = silu(gate) ⊙ up at ma.l[0].y.  Both activation tables are
+// built from one read of x (and one RMSNorm, prep 1).
+template <int BT, int J, int P, bool HAS_S>
+__global__ __launch_bounds__(kT) void k_decode_e8d4_pair(MultiArgs ma) {
+  __shared__ f16x4 tab[512];
+  __shared__ float red[2][kW][BT * 8];
+  __shared__ float wmax[2][kW];
+  __shared__ uint16_t pairx[2][2][64];
+  extern __shared__ __align__(16) char dyn[];
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const bool up = wave & 1;
+  const LinearArgs a = up ? ma.l[1] : ma.l[0];
+  using L = Layer<BT, J, P, 1, HAS_S, f16, false, true>;
+  const L layer(a, (int)blockIdx.x, (int)gridDim.x);
+  const size_t act = pair_table_bytes(a.N, BT);   // the second table 16-byte aligned
+  const Smem<BT> sm0{tab, red, wmax[0], (uint16_t*)dyn, (float*)(dyn + BT * (a.N + 8) * 2)};
+  const Smem<BT> sm1{tab, red, wmax[1], (uint16_t*)(dyn + act), (float*)(dyn + act + BT * (a.N + 8) * 2)};
+  typename L::State st;
+  layer.rows_first(st);
+  const int tid = threadIdx.x;
+  f16x4 tload[2];
+#pragma unroll
+  for (int p = 0; p < 2; ++p) tload[p] = ((const f16x4*)a.codes)[tid + kT * p];   // fp16 table
+  float scale1;
+  const float scale0 =
+      L(ma.l[0], (int)blockIdx.x, (int)gridDim.x).template build_act<true>(sm0, ma.l[1].h, &sm1, &scale1);
+  layer.issue_ring(st);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int p = 0; p < 2; ++p) tab[(tid + kT * p) ^ 0x100] = tload[p];
+  __syncthreads();
+  layer.rows(st, up ? sm1 : sm0, up ? scale1 : scale0, pairx);
+}
+
 namespace dec {
 
 // Smallest batch that takes the matrix-core decode kernel (EPTQ_MFMA_MIN_BATCH
@@ -124,6 +164,51 @@ int launch_k(const LinearArgs* layers, int n, hipStream_t s) {
   return 0;
 }
 
+template <int BT, int J, bool HAS_S>
+int launch_pair_k(const LinearArgs* l, hipStream_t s) {
+  constexpr int P = 8 / (J > 4 ? 4 : J);
+  using L = Layer<BT, J, P, 1, HAS_S, f16, false, true>;
+  // The fused RMSNorm keeps a whole row in the first CAP chunks per thread.
+  if (l[0].prep == 1 && L::CAP * kT * 8 < l[0].N) return -1;
+  auto kern = k_decode_e8d4_pair<BT, J, P, HAS_S>;
+  static int reg_cu = 0;
+  static size_t static_lds = 0;
+  if (reg_cu == 0) {
+    hipFuncAttributes fa;
+    int v = 128;
+    if (hipFuncGetAttributes(&fa, (const void*)kern) == hipSuccess) {
+      if (fa.numRegs > 0) v = fa.numRegs;
+      static_lds = fa.sharedSizeBytes;
+    }
+    const int waves = 512 / ((v + 7) / 8 * 8);
+    reg_cu = waves < 1 ? 1 : (waves > 8 ? 8 : waves);
+  }
+  const size_t dyn = 2 * pair_table_bytes(l[0].N, BT);
+  int per_cu = (int)(kLdsPerCu / (static_lds + dyn + 256));
+  if (per_cu > reg_cu) per_cu = reg_cu;
+  if (per_cu < 1) per_cu = 1;
+  const int RG = (l[0].M + L::R - 1) / L::R;
+  const int G = cu_count() * per_cu < RG ? cu_count() * per_cu : RG;
+  MultiArgs ma;
+  ma.n = 2;
+  ma.l[0] = l[0];
+  ma.l[1] = l[1];
+  ma.l[2] = ma.l[3] = l[0];
+  ma.start[0] = 0;
+  ma.start[1] = ma.start[2] = ma.start[3] = ma.start[4] = G;
+  kern<<<G, kT, dyn, s>>>(ma);
+  return 0;
+}
+
+template <int BT, bool HAS_S>
+int launch_pair_bt(const LinearArgs* l, hipStream_t s) {
+  const int J = chunks_for(l[0].N >> 3, 1);
+  if (J == 0 || 2 * pair_table_bytes(l[0].N, BT) > kActLdsMax) return -1;
+  if (J == 2) return launch_pair_k<BT, 2, HAS_S>(l, s);
+  if (J == 4) return launch_pair_k<BT, 4, HAS_S>(l, s);
+  return launch_pair_k<BT, 8, HAS_S>(l, s);
+}
+
 template <int BT, int S, bool HAS_S, typename XT>
 int launch_s(const LinearArgs* l, int n, hipStream_t s) {
   const int J = chunks_for(l[0].N >> 3, S);
@@ -189,5 +274,19 @@ int launch_decode_e8d4_multi(const LinearArgs* l, int n, hipStream_t s, void* wo
 }
 
 int launch_decode_e8d4(const LinearArgs& a, hipStream_t s) { return launch_decode_e8d4_multi(&a, 1, s); }
+
+// Returns 0 if launched, -1 if the pair is outside the kernel's range.
+int launch_decode_e8d4_pair(const LinearArgs* l, hipStream_t s) {
+  const LinearArgs& a = l[0];
+  const LinearArgs& b = l[1];
+  if (b.M != a.M || b.N != a.N || b.B != a.B || b.x != a.x || b.codes != a.codes || b.codes_f32 || a.codes_f32 ||
+      a.x_bf16 || b.x_bf16 || (b.S != nullptr) != (a.S != nullptr) || b.prep != a.prep || b.ldx != a.ldx ||
+      b.x2 != a.x2 || b.nw != a.nw || b.xsum != a.xsum || b.eps != a.eps)
+    return -1;
+  const int B = a.B;
+  if (B == 1) return a.S ? launch_pair_bt<1, true>(l, s) : launch_pair_bt<1, false>(l, s);
+  if (B == 2) return a.S ? launch_pair_bt<2, true>(l, s) : launch_pair_bt<2, false>(l, s);
+  return -1;   // B >= 3: two activation tables exceed the workgroup's activation LDS at N = 4096
+}
 
 }  // namespace eptq

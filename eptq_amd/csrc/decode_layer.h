@@ -153,9 +153,12 @@ struct Walk {
   const LinearArgs& a;
   int wg, G, S, J, K, R, slot, seg, lane, tid, V;
 
-  __device__ __forceinline__ Walk(const LinearArgs& a_, int wg_, int G_, int S_, int J_, int V_)
-      : a(a_), wg(wg_), G(G_), S(S_), J(J_), K(J_ > 4 ? 4 : J_), R(kW / S_),
-        slot(__builtin_amdgcn_readfirstlane(threadIdx.x >> 6) / S_),
+  // pair: the workgroup serves two layers of equal shape (SwiGLU gate and
+  // up), wave w layer w % 2 at row slot w / 2 (S = 1): R = 2 rows per layer.
+  __device__ __forceinline__ Walk(const LinearArgs& a_, int wg_, int G_, int S_, int J_, int V_, bool pair = false)
+      : a(a_), wg(wg_), G(G_), S(S_), J(J_), K(J_ > 4 ? 4 : J_), R(pair ? kW / S_ / 2 : kW / S_),
+        slot(pair ? (__builtin_amdgcn_readfirstlane(threadIdx.x >> 6) / S_) >> 1
+                  : __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) / S_),
         seg(__builtin_amdgcn_readfirstlane(threadIdx.x >> 6) % S_), lane(threadIdx.x & 63),
         tid(threadIdx.x), V(V_) {}
 
@@ -247,10 +250,15 @@ struct Walk {
   }
 };
 
-template <int BT, int J, int P, int S, bool HAS_S, typename XT, bool COH>
+// PAIR (S = 1): two layers of equal shape in one workgroup, wave w computing
+// layer w % 2 (gate, up) at row slot w / 2; the output is the SwiGLU product
+// silu(gate) ⊙ up, each factor rounded to the activation type first, as the
+// unfused Linear outputs are.
+template <int BT, int J, int P, int S, bool HAS_S, typename XT, bool COH, bool PAIR = false>
 struct Layer {
   static constexpr int V = BT * 8;
-  static constexpr int R = kW / S;                        // rows per row group
+  static constexpr int R = PAIR ? kW / S / 2 : kW / S;   // rows per row group (per layer)
+  static_assert(!PAIR || (S == 1 && !COH), "pairs: whole-row waves, one launch per layer pair");
   static constexpr int K = J > 4 ? 4 : J;                 // chunks of a row in flight
   static_assert(P * K == kRing, "the ring holds kRing chunks");
   static_assert(J % K == 0, "chunks per row must be a multiple of the chunks in flight");
@@ -269,9 +277,9 @@ struct Layer {
 
   __device__ __forceinline__ Layer(const LinearArgs& a_, int wg_, int G_)
       : a(a_), wg(wg_), G(G_), tid(threadIdx.x), lane(threadIdx.x & 63),
-        wave(__builtin_amdgcn_readfirstlane(threadIdx.x >> 6)), slot(wave / S), seg(wave % S),
-        N(a_.N), M(a_.M), B(a_.B), nch(a_.N >> 3), NP(a_.N + 8), RG((a_.M + R - 1) / R),
-        w(a_, wg_, G_, S, J, V) {}
+        wave(__builtin_amdgcn_readfirstlane(threadIdx.x >> 6)), slot(PAIR ? (wave / S) >> 1 : wave / S),
+        seg(wave % S), N(a_.N), M(a_.M), B(a_.B), nch(a_.N >> 3), NP(a_.N + 8), RG((a_.M + R - 1) / R),
+        w(a_, wg_, G_, S, J, V, PAIR) {}
 
   __device__ __forceinline__ int chunk(int j) const { return w.chunk(j); }
   __device__ __forceinline__ void rows_first(State& st) const { w.rows_first(st); }
@@ -282,12 +290,17 @@ struct Layer {
   // offsets past the end read zero), then the LDS table is written.  Needs a
   // barrier before the row loop reads it.  With a.prep == 1 the Linear's
   // input is formed here first: the RMSNorm of a residual sum (see
-  // LinearArgs).
-  __device__ __forceinline__ float build_act(const Smem<BT>& sm) const {
+  // LinearArgs).  TWO: a second table from the same x and a second h (hup)
+  // into sm2, its output scale into *out_scale2 (the layer pair's up side).
+  template <bool TWO = false>
+  __device__ __forceinline__ float build_act(const Smem<BT>& sm, const f16* hup = nullptr,
+                                             const Smem<BT>* sm2 = nullptr, float* out_scale2 = nullptr) const {
     uint16_t* __restrict__ xs = sm.xs;
     float* __restrict__ csc = sm.csc;
     const int prep = a.prep, ldx = a.ldx;
     const __amdgpu_buffer_rsrc_t rh = __builtin_amdgcn_make_buffer_rsrc((void*)a.h, (short)0, N * 2, kBufferWord3);
+    const __amdgpu_buffer_rsrc_t rh2 =
+        __builtin_amdgcn_make_buffer_rsrc((void*)hup, (short)0, TWO ? N * 2 : 0, kBufferWord3);
     const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void*)a.x, (short)0, B * ldx * 2, kBufferWord3);
     // The residual delta (prep 1; an empty resource when absent).
     const __amdgpu_buffer_rsrc_t r2 = __builtin_amdgcn_make_buffer_rsrc(
@@ -309,6 +322,14 @@ struct Layer {
     u32x4 hpre[CAP], xpre[CAP][BT], dpre[CAP][BT];
 #pragma unroll
     for (int k = 0; k < CAP; ++k) load_hx(tid + kT * k, hpre[k], xpre[k], dpre[k]);
+    u32x4 h2pre[TWO ? CAP : 1];
+    auto load_h2 = [&](int c) {
+      return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rh2, c < nch ? c * 16 : N * 2, 0, 0));
+    };
+    if constexpr (TWO) {
+#pragma unroll
+      for (int k = 0; k < CAP; ++k) h2pre[k] = load_h2(tid + kT * k);
+    }
     if (prep == 1) {
       // r = fp16(x + x2) (every chunk is among the first CAP: the launch
       // checks N <= CAP·kT·8), sum of squares per batch row, then
@@ -382,16 +403,22 @@ struct Layer {
     };
 
     float out_scale = 1.0f;
+    if constexpr (TWO) *out_scale2 = 1.0f;
     if (tid == 0) {   // the zero chunk past the end of every row
 #pragma unroll
       for (int b = 0; b < BT; ++b) *(u32x4*)(xs + b * NP + nch * 8) = (u32x4){0u, 0u, 0u, 0u};
       if (BT == 1) csc[nch] = 1.0f;
+      if constexpr (TWO) {
+#pragma unroll
+        for (int b = 0; b < BT; ++b) *(u32x4*)(sm2->xs + b * NP + nch * 8) = (u32x4){0u, 0u, 0u, 0u};
+        if (BT == 1) sm2->csc[nch] = 1.0f;
+      }
     }
     if constexpr (BT == 1) {
       // Per chunk of 8 columns: xs = fp16(x·h·2^-e), csc = 2^e with
       // max|x·h|·2^-e in [0.5, 1), so the fp16 accumulation of a chunk (|c| < 2,
       // 8 columns) cannot overflow; the main loop applies 2^e in fp32.
-      auto prep = [&](int c, const u32x4 hw, const u32x4 xw) {
+      auto prep = [&](uint16_t* __restrict__ xsd, float* __restrict__ cscd, int c, const u32x4 hw, const u32x4 xw) {
         const f16x8 hv = __builtin_bit_cast(f16x8, hw);
         const u16x8 xv = __builtin_bit_cast(u16x8, xw);
         float xf[8], mx = 0.0f;
@@ -407,61 +434,89 @@ struct Layer {
         for (int d = 0; d < 4; ++d)
           w[d] = __builtin_bit_cast(uint32_t, (h2){(f16)(xf[2 * d] * down), (f16)(xf[2 * d + 1] * down)});
         if (c < nch) {
-          *(u32x4*)(xs + c * 8) = w;
-          csc[c] = __builtin_ldexpf(1.0f, ex);
+          *(u32x4*)(xsd + c * 8) = w;
+          cscd[c] = __builtin_ldexpf(1.0f, ex);
         }
       };
 #pragma unroll
-      for (int k = 0; k < CAP; ++k) prep(tid + kT * k, hpre[k], xpre[k][0]);
+      for (int k = 0; k < CAP; ++k) {
+        prep(xs, csc, tid + kT * k, hpre[k], xpre[k][0]);
+        if constexpr (TWO) prep(sm2->xs, sm2->csc, tid + kT * k, h2pre[k], xpre[k][0]);
+      }
       for (int c = tid + kT * CAP; c < nch; c += kT) {
         u32x4 hw, xw[BT];
         load_more(c, hw, xw);
-        prep(c, hw, xw[0]);
+        u32x4 hw2 = hw;
+        if constexpr (TWO) hw2 = load_h2(c);
+        prep(xs, csc, c, hw, xw[0]);
+        if constexpr (TWO) prep(sm2->xs, sm2->csc, c, hw2, xw[0]);
       }
     } else {
       // Workgroup-uniform power-of-two scale with max|h|·2^-e <= 1, so the fp16
       // pairs |x·h·2^-e| <= |x| cannot overflow (dot2 accumulates in fp32).
-      float mx = 0.0f;
-      auto hmax = [&](const u32x4 hw) {
+      float mx = 0.0f, mx2 = 0.0f;
+      auto hmax = [&](float& m, const u32x4 hw) {
         const f16x8 hv = __builtin_bit_cast(f16x8, hw);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) mx = fmaxf(mx, fabsf((float)hv[e]));
+        for (int e = 0; e < 8; ++e) m = fmaxf(m, fabsf((float)hv[e]));
       };
 #pragma unroll
-      for (int k = 0; k < CAP; ++k) hmax(hpre[k]);
-      for (int c = tid + kT * CAP; c < nch; c += kT)
-        hmax(__builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rh, c * 16, 0, 0)));
-      mx = fmaxf(mx, partner<1>(mx));
-      mx = fmaxf(mx, partner<2>(mx));
-      mx = fmaxf(mx, partner<4>(mx));
-      mx = fmaxf(mx, partner<8>(mx));
-      mx = fmaxf(mx, partner<16>(mx));
-      mx = fmaxf(mx, partner<32>(mx));
+      for (int k = 0; k < CAP; ++k) {
+        hmax(mx, hpre[k]);
+        if constexpr (TWO) hmax(mx2, h2pre[k]);
+      }
+      for (int c = tid + kT * CAP; c < nch; c += kT) {
+        hmax(mx, __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rh, c * 16, 0, 0)));
+        if constexpr (TWO) hmax(mx2, load_h2(c));
+      }
+      auto wave_max = [&](float m) {
+        m = fmaxf(m, partner<1>(m));
+        m = fmaxf(m, partner<2>(m));
+        m = fmaxf(m, partner<4>(m));
+        m = fmaxf(m, partner<8>(m));
+        m = fmaxf(m, partner<16>(m));
+        return fmaxf(m, partner<32>(m));
+      };
+      mx = wave_max(mx);
       if (lane == 0) sm.wmax[wave] = mx;
+      if constexpr (TWO) {
+        mx2 = wave_max(mx2);
+        if (lane == 0) sm2->wmax[wave] = mx2;
+      }
       __syncthreads();
-      mx = fmaxf(fmaxf(sm.wmax[0], sm.wmax[1]), fmaxf(sm.wmax[2], sm.wmax[3]));
-      int ex = 0;
-      if (mx > 1.0f) ex = (int)((__builtin_bit_cast(uint32_t, mx) >> 23) & 0xff) - 126;  // 2^ex >= mx
-      out_scale = __builtin_ldexpf(1.0f, ex);
-      const f16 down = (f16)__builtin_ldexpf(1.0f, -ex);
-      const uint32_t down2 = __builtin_bit_cast(uint32_t, (h2){down, down});
-      auto prep = [&](int c, const u32x4 hw, const u32x4 (&xw)[BT]) {
+      // Workgroup-uniform scale 2^ex >= max|h| (ex = 0 when max|h| <= 1).
+      auto scale_of = [&](const float* wm, float& osc) {
+        const float m = fmaxf(fmaxf(wm[0], wm[1]), fmaxf(wm[2], wm[3]));
+        int ex = 0;
+        if (m > 1.0f) ex = (int)((__builtin_bit_cast(uint32_t, m) >> 23) & 0xff) - 126;
+        osc = __builtin_ldexpf(1.0f, ex);
+        const f16 down = (f16)__builtin_ldexpf(1.0f, -ex);
+        return __builtin_bit_cast(uint32_t, (h2){down, down});
+      };
+      const uint32_t down2 = scale_of(sm.wmax, out_scale);
+      uint32_t down2b = down2;
+      if constexpr (TWO) down2b = scale_of(sm2->wmax, *out_scale2);
+      auto prep = [&](uint16_t* __restrict__ xsd, uint32_t dn, int c, const u32x4 hw, const u32x4 (&xw)[BT]) {
         if (c < nch) {
 #pragma unroll
           for (int b = 0; b < BT; ++b) {
             u32x4 w;
 #pragma unroll
-            for (int d = 0; d < 4; ++d) w[d] = pk_mul(xw[b][d], pk_mul(hw[d], down2));
-            *(u32x4*)(xs + b * NP + c * 8) = w;
+            for (int d = 0; d < 4; ++d) w[d] = pk_mul(xw[b][d], pk_mul(hw[d], dn));
+            *(u32x4*)(xsd + b * NP + c * 8) = w;
           }
         }
       };
 #pragma unroll
-      for (int k = 0; k < CAP; ++k) prep(tid + kT * k, hpre[k], xpre[k]);
+      for (int k = 0; k < CAP; ++k) {
+        prep(xs, down2, tid + kT * k, hpre[k], xpre[k]);
+        if constexpr (TWO) prep(sm2->xs, down2b, tid + kT * k, h2pre[k], xpre[k]);
+      }
       for (int c = tid + kT * CAP; c < nch; c += kT) {
         u32x4 hw, xw[BT];
         load_more(c, hw, xw);
-        prep(c, hw, xw);
+        prep(xs, down2, c, hw, xw);
+        if constexpr (TWO) prep(sm2->xs, down2b, c, load_h2(c), xw);
       }
     }
     return out_scale;
@@ -469,7 +524,9 @@ struct Layer {
 
   // The row groups of this workgroup, starting from the state the ring and
   // entry prefetch left.  The LDS table and activation table must be ready.
-  __device__ __forceinline__ void rows(State& st, const Smem<BT>& sm, float out_scale) const {
+  // PAIR: pairx is LDS for the up side's outputs, [2][2][64].
+  __device__ __forceinline__ void rows(State& st, const Smem<BT>& sm, float out_scale,
+                                       uint16_t (*pairx)[2][64] = nullptr) const {
     const char* __restrict__ tabB = (const char*)sm.tab;
     const uint16_t* __restrict__ xs = sm.xs;
     const float* __restrict__ csc = sm.csc;
@@ -627,7 +684,27 @@ struct Layer {
       st.nrb = frb; st.nre = fre;
 
       const int base = wave_reduce_halving<V>(acc);
-      if constexpr (S == 1) {
+      if constexpr (PAIR) {
+        // The up wave hands its rounded outputs to the gate wave of the same
+        // row slot through LDS (same reducing lanes), which writes
+        // silu(gate) * up with the roundings of the separate SwiGLU kernel.
+        (void)base;
+        const bool writer = WaveReduceOut<V>::writer(lane);
+        const uint16_t v16 = Act<XT>::from_f32(acc[0] * out_scale * (float)og + (float)ob);
+        if ((wave & 1) && writer) pairx[par][slot][lane] = v16;
+        // One barrier per row group; pairx alternates like red[] below.
+        __syncthreads();
+        if (!(wave & 1) && row_ok && writer && wb < B) {
+          const float gf = Act<XT>::to_f32(v16), uf = Act<XT>::to_f32(pairx[par][slot][lane]);
+          float o = gf / (1.0f + __expf(-gf)) * uf;
+          // The fp32 rounding of the product before the fp16 one, as the
+          // separate kernel computes it (without this the compiler fuses the
+          // multiply and the conversion into one mixed-precision FMA).
+          asm volatile("" : "+v"(o));
+          store_y<COH>(a.y + (size_t)wb * a.ldy + 8 * m + wk, Act<XT>::from_f32(o));
+        }
+        par ^= 1;
+      } else if constexpr (S == 1) {
         // The wave owns the row: write straight from the reducing lanes.
         (void)base;
         if (row_ok && WaveReduceOut<V>::writer(lane) && wb < B) {

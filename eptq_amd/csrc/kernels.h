@@ -79,6 +79,11 @@ int launch_decode_e8d4(const LinearArgs& a, hipStream_t s);
 int launch_decode_e8d4_multi(const LinearArgs* layers, int n, hipStream_t s, void* work = nullptr,
                              long long work_bytes = 0);
 
+// SwiGLU pair (B <= 2, fp16): layers[0] = gate and layers[1] = up of equal
+// shape in one launch, y = silu(gate) ⊙ up written at layers[0].y with
+// layers[0].ldy; -1 when the pair is outside the kernel's range.
+int launch_decode_e8d4_pair(const LinearArgs* layers, hipStream_t s);
+
 // Matrix-core E8-D4 decode (B <= 16, fp16 x and table, no fused preparation);
 // -1 when the layers are outside its range.
 int launch_decode_mfma_multi(const LinearArgs* layers, int n, hipStream_t s, void* work = nullptr,

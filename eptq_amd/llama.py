@@ -116,6 +116,21 @@ def norm_linear(mod, resid, delta, w, eps, resid_out):
     return y
 
 
+def norm_swiglu(mod, resid, delta, w, eps, resid_out):
+    """silu(gate(t)) * up(t) for t = RMSNorm(resid + delta), ``mod`` the fused
+    gate|up module, in one decode launch; resid + delta is written to
+    resid_out (if given).  Raises EptqError (code EPTQ_EUNSUPPORTED) when the
+    kernel cannot take the shape or batch."""
+    arr, width = _cached_array(mod)
+    B, N = resid.shape
+    out = torch.empty((B, width // 2), dtype=resid.dtype, device=resid.device)
+    rc = _lib.load().eptq_llama_norm_swiglu(
+        arr, _parts(mod)[0]._codebook.data_ptr(), resid.data_ptr(), None if delta is None else delta.data_ptr(),
+        w.data_ptr(), eps, None if resid_out is None else resid_out.data_ptr(), N, B, out.data_ptr(), _stream(resid))
+    _lib.check(rc, "eptq_llama_norm_swiglu")
+    return out
+
+
 class RMSNorm(nn.Module):
     def __init__(self, dim: int, eps: float):
         super().__init__()
@@ -254,14 +269,28 @@ class QuantLlama(nn.Module):
                     raise
         return self._lin(mod, rmsnorm_(x, delta, w, self.cfg.eps)), x
 
+    def _norm_swiglu(self, mod, x, delta, w):
+        """silu(gate) * up of RMSNorm(x + delta) and the residual, in one launch
+        where the kernel takes it (fused ops, B <= 2), else as the fused-norm
+        gate|up launch followed by the SiLU kernel."""
+        if self.fused_ops and x.shape[0] <= 2:
+            r = torch.empty_like(x) if delta is not None else None
+            try:
+                return norm_swiglu(mod, x, delta, w, self.cfg.eps, r), (x if r is None else r)
+            except _lib.EptqError as e:
+                if e.code != _lib.EPTQ_EUNSUPPORTED:
+                    raise
+        gu, x = self._norm_into(mod, x, delta, w)
+        return silu_mul(gu), x
+
     def decode_tokens(self, tok, pos):
         """One token per sequence: tok (B, 1) int64, pos (1,) int64 on the device
         -> logits (B, vocab).  HIP kernels for everything but the embedding,
         lm_head and argmax; with ``fused_ops`` the norms run inside the Linear
         launches (norm(+residual) -> q|k|v, attention, o, norm(+residual) ->
-        gate|up, silu, down).  (The SiLU gating stays a launch of its own:
-        inside the down launch every workgroup would recompute all of it,
-        which measured slower than the launch it saves.)"""
+        gate|up -> silu·up, down; for B <= 2 the SwiGLU product is formed in
+        the gate|up launch itself, whose workgroups compute the same rows of
+        both layers, otherwise it is a launch of its own)."""
         cfg = self.cfg
         H, Hk, D = cfg.heads, cfg.kv_heads, cfg.head_dim
         x = self.embed_tokens(tok[:, 0])                    # (B, hidden), the residual stream
@@ -279,8 +308,8 @@ class QuantLlama(nn.Module):
                                           _stream(x))
             _lib.check(rc, "eptq_llama_rope_attn")
             o = self._lin(layer.o_proj, att)
-            gu, x = self._norm_into(layer.gate_up_proj, x, o, ln2)
-            delta = self._lin(layer.down_proj, silu_mul(gu))
+            act, x = self._norm_swiglu(layer.gate_up_proj, x, o, ln2)
+            delta = self._lin(layer.down_proj, act)
         h = rmsnorm_(x, delta, self.norm.weight, cfg.eps)
         return self.lm_head(h)
 

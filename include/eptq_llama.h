@@ -57,6 +57,20 @@ int eptq_llama_norm_linear(int n_layers, const eptq_layer* layers, const void* c
                            const void* resid, const void* delta, const void* w, float eps,
                            void* resid_out, int N, int B, void* y, int ldy, void* stream);
 
+/* The feed-forward input of a decoder layer in one launch (SwiGLU): the
+ * RMSNorm of eptq_llama_norm_linear (r = resid + delta written to resid_out,
+ * t = w ⊙ r · rsqrt(mean(r²) + eps)), then out (B, F) = silu(gate(t)) ⊙ up(t)
+ * with gate_up[0] = gate, gate_up[1] = up of equal M and F = 8·M; each factor
+ * is rounded to fp16 before the product, so out is bit-identical to
+ * eptq_llama_norm_linear followed by eptq_llama_silu_mul when both layers
+ * run whole-row waves there.  The layers' y_offset fields are not used.
+ * B <= 2; EPTQ_EUNSUPPORTED for larger batches or shapes the kernel does not
+ * take (then run eptq_llama_norm_linear and eptq_llama_silu_mul).  No
+ * counterpart in the reference, whose decode step runs the gate and up
+ * Linears and the SiLU product as separate operators (bench_decode.py). */
+int eptq_llama_norm_swiglu(const eptq_layer* gate_up, const void* codes, const void* resid, const void* delta,
+                           const void* w, float eps, void* resid_out, int N, int B, void* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -174,3 +174,12 @@ def test_fused_llama_linears_validate_arguments(lib):
     assert f(1, arr, 16, 24, None, 16, 1e-5, None, 64, 1, 16, 32, None) == _lib.EPTQ_EUNSUPPORTED  # misaligned
     assert f(1, arr, 16, 16, None, 16, 1e-5, None, 64, 0, 16, 32, None) == _lib.EPTQ_OK             # B = 0
     assert f(1, arr, 16, 16, None, 16, 1e-5, None, 64, 1, 16, 24, None) == _lib.EPTQ_EINVAL         # 8M > ldy
+    pair = (L * 2)(L(16, 16, 16, None, None, 16, None, None, 0, 4, 0), L(16, 16, 16, None, None, 16, None, None, 0, 4, 0))
+    g = lib.eptq_llama_norm_swiglu
+    assert g(None, 16, 16, None, 16, 1e-5, None, 64, 1, 16, None) == _lib.EPTQ_EINVAL             # no layers
+    assert g(pair, 16, 16, None, None, 1e-5, None, 64, 1, 16, None) == _lib.EPTQ_EINVAL           # no weight
+    assert g(pair, 16, 16, None, 16, 1e-5, None, 64, 3, 16, None) == _lib.EPTQ_EUNSUPPORTED       # B > 2
+    assert g(pair, 16, 16, None, 16, 1e-5, None, 64, 0, 16, None) == _lib.EPTQ_OK                 # B = 0
+    pair[1].M = 8
+    assert g(pair, 16, 16, None, 16, 1e-5, None, 64, 1, 16, None) == _lib.EPTQ_EINVAL             # M differ
+    assert "differ" in lib.eptq_last_error().decode()

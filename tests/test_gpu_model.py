@@ -135,13 +135,15 @@ def test_multi_linear_matches_separate_layers():
 def test_fused_norm_matches_separate_launches():
     """The decode step with the residual add + RMSNorm inside the q|k|v and
     gate|up launches against the same step with the norms as launches of
-    their own (the fused entry point must really run: no fallback)."""
+    their own (the fused entry points must really run: no fallback; gate|up
+    takes the SwiGLU launch for B <= 2)."""
     from eptq_amd.llama import LlamaConfig, build_synthetic
     import eptq_amd.llama as LL
     print("synthetic llama: fused norm vs separate launches", flush=True)
-    calls = []
-    real = LL.norm_linear
+    calls, swiglu = [], []
+    real, real_sw = LL.norm_linear, LL.norm_swiglu
     LL.norm_linear = lambda *a, **k: (calls.append(1), real(*a, **k))[1]
+    LL.norm_swiglu = lambda *a, **k: (swiglu.append(1), real_sw(*a, **k))[1]
     for kv, B in ((4, 1), (2, 3), (4, 8)):
         cfg = LlamaConfig(hidden=512, ffn=1024, layers=2, heads=4, kv_heads=kv, vocab=256)
         model = build_synthetic(cfg, device="cuda", seed=13 + B)
@@ -164,9 +166,11 @@ def test_fused_norm_matches_separate_launches():
         assert rel_l2(got.cpu().numpy(), ref.cpu().numpy()) < 2e-3, (kv, B)
         for i in range(cfg.layers):
             assert rel_l2(model.kc[i][:, :, 12].float().cpu().numpy(), kref[i].float().cpu().numpy()) < 2e-3
-        assert len(calls) == 2 * cfg.layers, "the fused path ran for every norm"
+        n_sw = cfg.layers if B <= 2 else 0
+        assert len(swiglu) == n_sw and len(calls) == 2 * cfg.layers - n_sw, "the fused path ran for every norm"
         calls.clear()
-    LL.norm_linear = real
+        swiglu.clear()
+    LL.norm_linear, LL.norm_swiglu = real, real_sw
 
 
 def test_split_attention_matches_single_workgroup():
