@@ -92,13 +92,16 @@ __device__ __forceinline__ void gemm_tile(const LinearArgs& a, int OB) {
   const int qrow = m0 + dq;                      // < M: the launcher requires M % 16 == 0
   const uint32_t* __restrict__ qsrc = (const uint32_t*)(a.Q + (size_t)qrow * N);
   const int grp = HAS_S ? (8 * qrow) / a.qb : 0;
-  // x chunks: kXC 16-byte pieces, token xt[i], column chunk xc[i]
+  // x chunks: kXC 16-byte pieces, token xt[i], column chunk xc[i].  Sixteen
+  // consecutive lanes take 16 tokens at one chunk, so each 16-lane pass of
+  // the 16-byte LDS writes hits 64 distinct banks (80-byte rows); a wave
+  // still reads whole 64-byte pieces of 16 token rows from global memory.
   int xt[kXC], xc[kXC];
 #pragma unroll
   for (int i = 0; i < kXC; ++i) {
     const int idx = tid + kGT * i;
-    xt[i] = idx >> 2;
-    xc[i] = (idx & 3) * 8;
+    xt[i] = (idx & 15) | ((idx >> 6) << 4);
+    xc[i] = ((idx >> 4) & 3) * 8;
   }
 
   // ---- table and CSR staging ----
