@@ -44,6 +44,15 @@ template <> struct Act<bf16> {
 };
 
 // Bitfield insert: (mask & a) | (~mask & b) in one VALU op.
+// (t >> 16) & 0xFF8 in one op (SDWA word select of the second operand): the
+// table byte address of the upper index of a 32-bit word t = w >> 4.
+__device__ __forceinline__ uint32_t hi_addr(uint32_t t) {
+  uint32_t r;
+  asm("v_and_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:WORD_1"
+      : "=v"(r) : "s"(0xFF8u), "v"(t));
+  return r;
+}
+
 __device__ __forceinline__ uint32_t bfi(uint32_t mask, uint32_t a, uint32_t b) {
   uint32_t r;
   asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "s"(mask), "v"(a), "v"(b));

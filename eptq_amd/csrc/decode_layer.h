@@ -586,8 +586,9 @@ struct Layer {
 #pragma unroll
           for (int d = 0; d < 4; ++d) {
             const uint32_t q = st.ring[p * K + j % K][d];
-            const uint32_t a1lo = (q >> 4) & 0xFF8u;
-            const uint32_t a1hi = (q >> 20) & 0xFF8u;
+            const uint32_t q4 = q >> 4;
+            const uint32_t a1lo = q4 & 0xFF8u;
+            const uint32_t a1hi = hi_addr(q4);   // (q >> 20) & 0xFF8
             const uint32_t a2lo = bfi(0x3F8u, q << 3, a1lo);
             const uint32_t a2hi = bfi(0x3F8u, q >> 13, a1hi);
             t1l[d] = *(const u32x2*)(tabB + a1lo);

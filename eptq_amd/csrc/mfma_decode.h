@@ -41,13 +41,6 @@ __device__ __forceinline__ uint32_t bfi_v(uint32_t mask, uint32_t a, uint32_t b)
   asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "v"(mask), "v"(a), "v"(b));
   return r;
 }
-// (t >> 16) & 0xFF8 in one op (SDWA word select of the second operand).
-__device__ __forceinline__ uint32_t hi_addr(uint32_t t) {
-  uint32_t r;
-  asm("v_and_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:WORD_1"
-      : "=v"(r) : "s"(0xFF8u), "v"(t));
-  return r;
-}
 __device__ __forceinline__ f16 as_f16(uint16_t v) { return __builtin_bit_cast(f16, v); }
 __device__ __forceinline__ uint16_t bits(f16 v) { return __builtin_bit_cast(uint16_t, v); }
 
