@@ -61,7 +61,8 @@ constexpr int kS = 8;           // column waves per workgroup (one workgroup per
 
 
 // Split-K workspace: per-tile arrival counters, then the fp32 partial sums
-// [tile][part][16][64] of tiles whose columns are split over P workgroups.
+// [split tile][part][16][64] of the tiles whose columns are split over P
+// workgroups.
 constexpr int kMaxCounters = 16384;
 constexpr size_t kCntBytes = (size_t)kMaxCounters * 4;
 constexpr size_t kPartBytes = 16 * 64 * 4;
@@ -90,7 +91,11 @@ __host__ __device__ inline size_t dyn_bytes(int N, bool has_s, int S) {
 
 template <int S, bool HAS_S>
 // At most 168 VGPRs (3 waves per SIMD): one 9-wave workgroup per CU.
-__global__ __launch_bounds__((S + 1) * 64, 3) void k_decode_mfma(MultiArgs ma, int P, int* wcnt, float* wpart) {
+// Work split: tiles [0, T1) take one workgroup each; the tiles from T1 on
+// have their columns split over P workgroups (T1 = 0: every tile).  ma.start
+// counts tiles.
+__global__ __launch_bounds__((S + 1) * 64, 3) void k_decode_mfma(MultiArgs ma, int P, int T1, int* wcnt,
+                                                                 float* wpart) {
   constexpr int NT = (S + 1) * 64;
   __shared__ f16x4 tab[512];
   // The tile's critical blocks as the output stage reads them: O, and the
@@ -104,16 +109,18 @@ __global__ __launch_bounds__((S + 1) * 64, 3) void k_decode_mfma(MultiArgs ma, i
   __shared__ float wmax[S + 1];
   extern __shared__ __attribute__((aligned(16))) char dyn[];
 
+  // This workgroup's tile (index among all tiles of the launch) and part:
+  // part p of Pt takes the p-th Pt-th of the tile's column blocks.
+  const int g = (int)blockIdx.x;
+  const int Pt = g < T1 ? 1 : P;
+  const int tile_g = g < T1 ? g : T1 + (g - T1) / P;
+  const int part = g < T1 ? 0 : (g - T1) - (tile_g - T1) * P;
   int li = 0;
 #pragma unroll
   for (int l = 1; l < kMaxLayers; ++l)
-    if (l < ma.n && (int)blockIdx.x >= ma.start[l]) li = l;
+    if (l < ma.n && tile_g >= ma.start[l]) li = l;
   const LinearArgs a = li == 0 ? ma.l[0] : li == 1 ? ma.l[1] : li == 2 ? ma.l[2] : ma.l[3];
-  // Workgroups [start[l], start[l+1]) serve layer l: tile = wgl / P, and
-  // part p of P takes the p-th P-th of the column blocks.
-  const int wgl = (int)blockIdx.x - ma.start[li];
-  const int tile = wgl / P, part = wgl - tile * P;
-  const int tile_g = ma.start[li] / P + tile;     // index among all tiles of the launch
+  const int tile = tile_g - ma.start[li];         // within layer li
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -153,7 +160,7 @@ __global__ __launch_bounds__((S + 1) * 64, 3) void k_decode_mfma(MultiArgs ma, i
   // at columns 64·blk + 16·kg .. +15; lane (b, kg) the activations of batch
   // row b at the same columns (rows past M and batch rows past B read zeros).
   const int nb = Np / kBlk;
-  const int plo = part * nb / P, pnb = (part + 1) * nb / P - plo;
+  const int plo = part * nb / Pt, pnb = (part + 1) * nb / Pt - plo;
   const int blo = plo + wave * pnb / S, bhi = plo + (wave + 1) * pnb / S;
   const int i = lane & 15, kg = lane >> 4;
   const int qrow = m0 + (i >> 1);
@@ -395,12 +402,12 @@ __global__ __launch_bounds__((S + 1) * 64, 3) void k_decode_mfma(MultiArgs ma, i
   }
   // Split columns: every part leaves its partial sums (device-coherent
   // stores, complete before the tile's counter is raised); the last part to
-  // arrive adds all P of them in part order, so the result does not depend
+  // arrive adds all Pt of them in part order, so the result does not depend
   // on which part came last, writes y and resets the counter.
   bool fin = true;
-  if (P > 1) {
+  if (Pt > 1) {
     __shared__ int last_part;
-    float* base = wpart + (size_t)tile_g * P * (kPartBytes / 4) + r;
+    float* base = wpart + (size_t)(tile_g - T1) * Pt * (kPartBytes / 4) + r;
 #pragma unroll
     for (int it = 0; it < kItems; ++it)
       if (ok[it]) st_pair(base + part * (kPartBytes / 4) + (((tid + NT * it) >> 5) & 15) * 64, s0[it], s1[it]);
@@ -408,8 +415,8 @@ __global__ __launch_bounds__((S + 1) * 64, 3) void k_decode_mfma(MultiArgs ma, i
     __syncthreads();
     if (tid == 0) {
       const int old = __hip_atomic_fetch_add(wcnt + tile_g, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      last_part = old == P - 1;
-      if (old == P - 1) __hip_atomic_store(wcnt + tile_g, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      last_part = old == Pt - 1;
+      if (old == Pt - 1) __hip_atomic_store(wcnt + tile_g, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
     fin = last_part != 0;
@@ -419,7 +426,7 @@ __global__ __launch_bounds__((S + 1) * 64, 3) void k_decode_mfma(MultiArgs ma, i
         if (!ok[it]) continue;
         const int b = ((tid + NT * it) >> 5) & 15;
         float t0 = 0.0f, t1 = 0.0f;
-        for (int q = 0; q < P; ++q) {
+        for (int q = 0; q < Pt; ++q) {
           float2 v = make_float2(s0[it], s1[it]);
           if (q != part) v = ld_pair(base + q * (kPartBytes / 4) + b * 64);
           t0 += v.x;
@@ -444,14 +451,14 @@ __global__ __launch_bounds__((S + 1) * 64, 3) void k_decode_mfma(MultiArgs ma, i
   }
 }
 
-// Parts per tile: as many as keep the grid within one workgroup per CU (a
-// second round of workgroups would double the time), within the workspace
-// (none: one part).
-inline int parts_for(int tiles, void* work, long long work_bytes) {
-  if (!work || tiles > kMaxCounters) return 1;
-  int P = dec::cu_count() / tiles;
+// Parts for `split` tiles: as many as keep them within one workgroup per CU
+// (a further round of workgroups would add a whole tile's time), within the
+// workspace (none: one part).
+inline int parts_for(int split, int tiles, void* work, long long work_bytes) {
+  if (!work || tiles > kMaxCounters || split <= 0) return 1;
+  int P = dec::cu_count() / split;
   P = P < 1 ? 1 : P > kMaxParts ? kMaxParts : P;
-  while (P > 1 && (long long)(kCntBytes + (size_t)tiles * P * kPartBytes) > work_bytes) --P;
+  while (P > 1 && (long long)(kCntBytes + (size_t)split * P * kPartBytes) > work_bytes) --P;
   return P;
 }
 
@@ -459,14 +466,21 @@ template <int S, bool HAS_S>
 int launch_t(const LinearArgs* l, int n, hipStream_t s, void* work, long long work_bytes) {
   int tiles = 0;
   for (int k = 0; k < n; ++k) tiles += (l[k].M + kTile - 1) / kTile;
-  const int P = parts_for(tiles, work, work_bytes);
+  // One workgroup per CU.  Up to one round of tiles: each tile's columns
+  // split P ways.  More tiles than CUs: the first round takes whole tiles,
+  // and the tiles left for the second round are split so that it is shorter.
+  const int cu = dec::cu_count();
+  int T1 = tiles > cu ? cu : 0;
+  int P = parts_for(tiles - T1, tiles, work, work_bytes);
+  if (P == 1) T1 = 0;
   MultiArgs ma;
   ma.n = n;
   ma.start[0] = 0;
   for (int k = 0; k < kMaxLayers; ++k) {
     ma.l[k] = l[k < n ? k : 0];
-    ma.start[k + 1] = ma.start[k] + (k < n ? (l[k].M + kTile - 1) / kTile * P : 0);
+    ma.start[k + 1] = ma.start[k] + (k < n ? (l[k].M + kTile - 1) / kTile : 0);   // tiles
   }
+  const int grid = T1 + (tiles - T1) * P;
   auto kern = k_decode_mfma<S, HAS_S>;
   const size_t dyn = dyn_bytes(l[0].N, HAS_S, S);
   static size_t attr = 0;
@@ -477,7 +491,7 @@ int launch_t(const LinearArgs* l, int n, hipStream_t s, void* work, long long wo
   }
   int* cnt = P > 1 ? (int*)work : nullptr;
   float* part = P > 1 ? (float*)((char*)work + kCntBytes) : nullptr;
-  kern<<<ma.start[n], (S + 1) * 64, dyn, s>>>(ma, P, cnt, part);
+  kern<<<grid, (S + 1) * 64, dyn, s>>>(ma, P, T1, cnt, part);
   return 0;
 }
 

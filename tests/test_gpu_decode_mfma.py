@@ -137,3 +137,50 @@ def test_mfma_decode_split_columns(out, inp, B, qb):
         assert torch.equal(yg, y1), rep
         assert torch.equal(linear_forward_multi(layers, lin._codebook, x, work=work), y1), rep
     assert int(work[:65536].view(torch.int32).abs().sum()) == 0
+
+
+@pytest.mark.parametrize("shapes,B,qb", [
+    ([(11008, 4096)] * 2, 8, None),    # gate|up: 344 tiles, more than one workgroup per CU
+    ([(20480, 1024)], 16, 128),        # 320 tiles of one layer, S_group
+])
+def test_mfma_decode_tail_tiles_split(shapes, B, qb):
+    """More tiles than CUs: the first round takes whole tiles and the tiles
+    left for the second have their columns split.  Every layer matches the
+    oracle and the launch without a workspace (up to fp32 summation order),
+    repeated calls and graph replays are bit-identical, and the counters are
+    back at zero."""
+    from eptq_amd.kernels import decode_workspace
+    print(f"mfma decode tail split {shapes} B={B} qb={qb}", flush=True)
+    q = E8D4Quantizer(radius=1.75)
+    qds = [make_layer(o, i, seed=500 + k, percmask=0.002, bias=True, qb_size=qb) for k, (o, i) in enumerate(shapes)]
+    lins = [EPTQLinear.from_quantized_data(qd, q, "e8_d4").cuda() for qd in qds]
+    layers = [dict(Q=l.Q, g=l.g, h=l.h, O_vals=l.O_vals, O_col=l.O_col, O_row_ptr=l.O_row_ptr,
+                   bias=l.bias, S_group=l.S_group) for l in lins]
+    x = make_x(B, shapes[0][1], seed=11).cuda()
+    work = decode_workspace(x.device)
+    y0 = linear_forward_multi(layers, lins[0]._codebook, x)
+    y1 = linear_forward_multi(layers, lins[0]._codebook, x, work=work)
+    torch.cuda.synchronize()
+    off = 0
+    for qd, (o, _) in zip(qds, shapes):
+        want = _ref(qd, x.cpu())
+        assert rel_l2(y1[:, off:off + o].float().cpu().numpy(), want) <= TOL
+        off += o
+    assert rel_l2(y1.float().cpu().numpy(), y0.float().cpu().numpy()) < 1e-3
+    assert int(work[:65536].view(torch.int32).abs().sum()) == 0
+    assert torch.equal(linear_forward_multi(layers, lins[0]._codebook, x, work=work), y1)
+    yg = torch.empty_like(y1)
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            yg.copy_(linear_forward_multi(layers, lins[0]._codebook, x, work=work))
+    torch.cuda.current_stream().wait_stream(s)
+    for rep in range(3):
+        yg.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(yg, y1), rep
+    assert int(work[:65536].view(torch.int32).abs().sum()) == 0
