@@ -11,6 +11,9 @@
 //                   pos: rotary on q and the head's k, k/v written to the cache
 //                   at pos, softmax(q·Kᵀ/√D)·V over positions 0..pos.
 //  * k_silu_mul:    a = silu(gate) ⊙ up from the fused gate|up projection.
+//  * k_lm_head_argmax: the step's tail — final RMSNorm, the fp16 lm_head
+//                   matvec, the logits, the greedy next token and the position
+//                   advance — in one launch (B <= 2).
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -368,6 +371,174 @@ __global__ __launch_bounds__(kT) void k_silu_mul(const f16* __restrict__ gu, f16
   *(f16x8*)(a + (size_t)b * F + c * 8) = o;
 }
 
+// ---- the decode step's tail: final RMSNorm + lm_head + greedy argmax -------
+//
+// Every workgroup forms t = RMSNorm(x + delta) for the B rows in LDS with the
+// chunk order and roundings of k_rmsnorm (so t is bit-identical to it), then
+// each wave streams vocab rows v = wave id + k · waves: lane l holds columns
+// 8(64c + l) .. +7 (c < CH) of t in registers and of W row v (a wave load
+// covers 1 KB of the row), fp32 dot2 sums, a wave reduction, and lane 0
+// writes fp16 logits[b][v].  The greedy choice is the largest fp16 logit,
+// the smallest index among equal ones (as torch.argmax): an order-preserving
+// 64-bit key per (b, v), reduced per workgroup and combined with one
+// device-scope atomic max per batch row; the last workgroup to finish (an
+// atomic count) writes tok[b], adds 1 to *pos (if given) and clears the keys
+// and the count for the next call.  The next row is requested before the
+// current one is summed (two rows in flight per wave).
+constexpr int kHeadPerCu = 2;   // workgroups per CU
+
+__device__ __forceinline__ unsigned long long head_key(f16 v, int idx) {
+  const uint32_t b = __builtin_bit_cast(uint16_t, v);
+  const uint32_t o = (b & 0x8000u) ? (~b & 0xFFFFu) : (b | 0x8000u);   // fp16 order as unsigned
+  return ((unsigned long long)o << 32) | (0xFFFFFFFFu - (uint32_t)idx);
+}
+
+// By value: __builtin_bit_cast applied directly to a vector element (a[d])
+// reads element 0 with this compiler.
+__device__ __forceinline__ float dot2w(uint32_t a, uint32_t b, float acc) {
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, a), __builtin_bit_cast(f16x2, b), acc, false);
+}
+__device__ __forceinline__ float dot8(const u32x4 a, const u32x4 b, float acc) {
+#pragma unroll
+  for (int d = 0; d < 4; ++d) acc = dot2w(a[d], b[d], acc);
+  return acc;
+}
+
+template <int B, int CH>
+__global__ __launch_bounds__(kT) void k_lm_head_argmax(const f16* __restrict__ x, const f16* __restrict__ delta,
+                                                       const f16* __restrict__ nw, float eps,
+                                                       const f16* __restrict__ W, int V, f16* __restrict__ logits,
+                                                       int64_t* __restrict__ tok, int64_t* __restrict__ pos,
+                                                       unsigned long long* __restrict__ keys, int* __restrict__ cnt) {
+  constexpr int H = CH * 512;
+  constexpr int MAXV = H / 8 / kT;   // 16-byte chunks per thread in the norm (H/8 chunks over kT threads)
+  static_assert(MAXV * kT * 8 == H, "H is a multiple of 2048");
+  __shared__ __attribute__((aligned(16))) f16 ts[B][H];
+  __shared__ float sh[kT / 64];
+  __shared__ unsigned long long wbest[B][kT / 64];
+  __shared__ int s_last;
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  // t = fp16(w ⊙ r · rsqrt(mean(r²) + eps)), r = fp16(x + delta): k_rmsnorm's steps.
+#pragma unroll
+  for (int b = 0; b < B; ++b) {
+    f16x8 v[MAXV];
+    float ss = 0.0f;
+#pragma unroll
+    for (int k = 0; k < MAXV; ++k) {
+      const int c = t + kT * k;
+      f16x8 a = *(const f16x8*)(x + (size_t)b * H + c * 8);
+      if (delta) {
+        const f16x8 d = *(const f16x8*)(delta + (size_t)b * H + c * 8);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) a[e] = (f16)((float)a[e] + (float)d[e]);
+      }
+      v[k] = a;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss += (float)a[e] * (float)a[e];
+    }
+    const float inv = rsqrtf(block_sum(ss, sh) / (float)H + eps);
+#pragma unroll
+    for (int k = 0; k < MAXV; ++k) {
+      const int c = t + kT * k;
+      const f16x8 wv = *(const f16x8*)(nw + c * 8);
+      f16x8 o;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = (f16)((float)v[k][e] * inv * (float)wv[e]);
+      *(f16x8*)&ts[b][c * 8] = o;
+    }
+  }
+  __syncthreads();
+  u32x4 tr[B][CH];
+#pragma unroll
+  for (int b = 0; b < B; ++b)
+#pragma unroll
+    for (int c = 0; c < CH; ++c) tr[b][c] = *(const u32x4*)&ts[b][(c * 64 + lane) * 8];
+
+  const int waves = (int)gridDim.x * (kT / 64);
+  unsigned long long best[B];
+#pragma unroll
+  for (int b = 0; b < B; ++b) best[b] = 0ull;
+  auto load_row = [&](int v, u32x4 (&w)[CH]) {
+    const u32x4* p = (const u32x4*)(W + (size_t)v * H);
+#pragma unroll
+    for (int c = 0; c < CH; ++c) w[c] = __builtin_nontemporal_load(p + c * 64 + lane);
+  };
+  auto row = [&](int v, const u32x4 (&w)[CH]) {
+#pragma unroll
+    for (int b = 0; b < B; ++b) {
+      float s = 0.0f;
+#pragma unroll
+      for (int c = 0; c < CH; ++c) s = dot8(w[c], tr[b][c], s);
+      s += partner<1>(s);
+      s += partner<2>(s);
+      s += partner<4>(s);
+      s += partner<8>(s);
+      s += partner<16>(s);
+      s += partner<32>(s);
+      if (lane == 0) {
+        const f16 l16 = (f16)s;
+        logits[(size_t)b * V + v] = l16;
+        const unsigned long long k = head_key(l16, v);
+        best[b] = k > best[b] ? k : best[b];
+      }
+    }
+  };
+  u32x4 wa[CH], wb[CH];
+  int v = (int)blockIdx.x * (kT / 64) + wave;
+  if (v < V) load_row(v, wa);
+  while (v < V) {
+    const int v1 = v + waves;
+    if (v1 < V) load_row(v1, wb);
+    row(v, wa);
+    if (v1 >= V) break;
+    const int v2 = v1 + waves;
+    if (v2 < V) load_row(v2, wa);
+    row(v1, wb);
+    v = v2;
+  }
+  // Workgroup maximum per batch row, one device-scope atomic each; the last
+  // workgroup to arrive finishes the step.
+  if (lane == 0) {
+#pragma unroll
+    for (int b = 0; b < B; ++b) wbest[b][wave] = best[b];
+  }
+  __syncthreads();
+  if (t < B) {
+    unsigned long long m = wbest[t][0];
+#pragma unroll
+    for (int w2 = 1; w2 < kT / 64; ++w2) m = wbest[t][w2] > m ? wbest[t][w2] : m;
+    __hip_atomic_fetch_max(keys + t, m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): the atomics are complete
+  __syncthreads();
+  if (t == 0) {
+    const int prev = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = prev == (int)gridDim.x - 1;
+    if (s_last) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  if (!s_last) return;
+  if (t < B) {
+    const unsigned long long k = __hip_atomic_load(keys + t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    tok[t] = (int64_t)(0xFFFFFFFFu - (uint32_t)(k & 0xFFFFFFFFull));
+    __hip_atomic_store(keys + t, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  if (t == 0 && pos) pos[0] = pos[0] + 1;
+}
+
+template <int B, int CH>
+int launch_head(const f16* x, const f16* delta, const f16* w, float eps, const f16* W, int V, f16* logits,
+                int64_t* tok, int64_t* pos, unsigned long long* keys, int* cnt, hipStream_t s) {
+  int dev = 0, cus = 256;
+  if (hipGetDevice(&dev) == hipSuccess) (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  int G = cus * kHeadPerCu;
+  const int rows_per_wg = kT / 64;
+  if (G * rows_per_wg > V) G = (V + rows_per_wg - 1) / rows_per_wg;
+  hipLaunchKernelGGL((k_lm_head_argmax<B, CH>), dim3(G), dim3(kT), 0, s, x, delta, w, eps, W, V, logits, tok, pos,
+                     keys, cnt);
+  return 0;
+}
+
 }  // namespace
 }  // namespace eptq
 
@@ -410,6 +581,37 @@ int eptq_llama_rope_attn(const void* qkv, const void* pos, const void* cos_tab, 
                      (const eptq::f16*)qkv, (const int64_t*)pos, (const float*)cos_tab,
                      (const float*)sin_tab, (eptq::f16*)k_cache, (eptq::f16*)v_cache, (eptq::f16*)out,
                      H, Hk, L, 1.0f / sqrtf((float)D), part, cnt);
+  return hipGetLastError() == hipSuccess ? 0 : 3;
+}
+
+long long eptq_llama_lm_head_work_bytes(int B) {
+  if (B <= 0) return 0;
+  return (long long)B * 8 + 8;   // one 64-bit key per batch row, then the count
+}
+
+int eptq_llama_lm_head_argmax(const void* x, const void* delta, const void* w, float eps, const void* W, int V,
+                              int H, int B, void* logits, void* tok, void* pos, void* work, void* stream) {
+  if (!x || !w || !W || !logits || !tok || !work || V <= 0 || B <= 0) return 1;
+  if (((uintptr_t)x | (uintptr_t)w | (uintptr_t)W | (uintptr_t)(delta ? delta : x)) & 15) return 1;
+  if (((uintptr_t)work & 7) || ((uintptr_t)logits & 1) || ((uintptr_t)tok & 7) || ((uintptr_t)pos & 7)) return 1;
+  if (B > 2 || (H != 4096 && H != 6144 && H != 8192)) return 2;
+  using eptq::f16;
+  auto* keys = (unsigned long long*)work;
+  int* cnt = (int*)(keys + B);
+  const hipStream_t s = (hipStream_t)stream;
+  const f16 *px = (const f16*)x, *pd = (const f16*)delta, *pw = (const f16*)w, *pW = (const f16*)W;
+  f16* pl = (f16*)logits;
+  int64_t *pt = (int64_t*)tok, *pp = (int64_t*)pos;
+  const int CH = H / 512;
+  if (B == 1) {
+    if (CH == 8) eptq::launch_head<1, 8>(px, pd, pw, eps, pW, V, pl, pt, pp, keys, cnt, s);
+    else if (CH == 12) eptq::launch_head<1, 12>(px, pd, pw, eps, pW, V, pl, pt, pp, keys, cnt, s);
+    else eptq::launch_head<1, 16>(px, pd, pw, eps, pW, V, pl, pt, pp, keys, cnt, s);
+  } else {
+    if (CH == 8) eptq::launch_head<2, 8>(px, pd, pw, eps, pW, V, pl, pt, pp, keys, cnt, s);
+    else if (CH == 12) eptq::launch_head<2, 12>(px, pd, pw, eps, pW, V, pl, pt, pp, keys, cnt, s);
+    else eptq::launch_head<2, 16>(px, pd, pw, eps, pW, V, pl, pt, pp, keys, cnt, s);
+  }
   return hipGetLastError() == hipSuccess ? 0 : 3;
 }
 

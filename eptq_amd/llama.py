@@ -131,6 +131,20 @@ def norm_swiglu(mod, resid, delta, w, eps, resid_out):
     return out
 
 
+def lm_head_argmax(x, delta, w, eps, W, tok, pos, work):
+    """logits (B, V) = RMSNorm(x + delta) · Wᵀ, tok[:, 0] <- argmax, pos += 1,
+    in one launch.  Raises EptqError (code EPTQ_EUNSUPPORTED) for B > 2 or an
+    unsupported hidden size."""
+    B, H = x.shape
+    V = W.shape[0]
+    logits = torch.empty((B, V), dtype=x.dtype, device=x.device)
+    rc = _lib.load().eptq_llama_lm_head_argmax(
+        x.data_ptr(), None if delta is None else delta.data_ptr(), w.data_ptr(), eps, W.data_ptr(), V, H, B,
+        logits.data_ptr(), tok.data_ptr(), None if pos is None else pos.data_ptr(), work.data_ptr(), _stream(x))
+    _lib.check(rc, "eptq_llama_lm_head_argmax")
+    return logits
+
+
 class RMSNorm(nn.Module):
     def __init__(self, dim: int, eps: float):
         super().__init__()
@@ -228,6 +242,11 @@ class QuantLlama(nn.Module):
         # Split-K workspace of the decode Linears (batches of 5..16): the
         # decode step's launches run one after another on one stream.
         self.lin_work = decode_workspace(device)
+        # Workspace of the fused final norm + lm_head + argmax (B <= 2).
+        self.head_work = None
+        if batch <= 2:
+            nbytes = _lib.load().eptq_llama_lm_head_work_bytes(batch)
+            self.head_work = torch.zeros(nbytes, dtype=torch.uint8, device=device)
 
     def forward_tokens(self, ids, pos):
         """ids: (B, T) int64, pos: (T,) int64 positions -> logits (B, T, vocab)."""
@@ -291,6 +310,13 @@ class QuantLlama(nn.Module):
         gate|up -> silu·up, down; for B <= 2 the SwiGLU product is formed in
         the gate|up launch itself, whose workgroups compute the same rows of
         both layers, otherwise it is a launch of its own)."""
+        x, delta = self._decode_layers(tok, pos)
+        h = rmsnorm_(x, delta, self.norm.weight, self.cfg.eps)
+        return self.lm_head(h)
+
+    def _decode_layers(self, tok, pos):
+        """The decoder layers of one decode step: the residual stream x and the
+        last layer's output delta (their sum is the final norm's input)."""
         cfg = self.cfg
         H, Hk, D = cfg.heads, cfg.kv_heads, cfg.head_dim
         x = self.embed_tokens(tok[:, 0])                    # (B, hidden), the residual stream
@@ -310,8 +336,26 @@ class QuantLlama(nn.Module):
             o = self._lin(layer.o_proj, att)
             act, x = self._norm_swiglu(layer.gate_up_proj, x, o, ln2)
             delta = self._lin(layer.down_proj, act)
-        h = rmsnorm_(x, delta, self.norm.weight, cfg.eps)
-        return self.lm_head(h)
+        return x, delta
+
+    def decode_next(self, tok, pos):
+        """One greedy step in place: logits (B, vocab) for tok at pos, then
+        tok <- argmax(logits) and pos += 1.  With ``fused_ops`` and B <= 2
+        the final norm, lm_head, argmax and position advance are one launch
+        (``eptq_llama_lm_head_argmax``); otherwise PyTorch's lm_head and
+        argmax follow the decode step."""
+        x, delta = self._decode_layers(tok, pos)
+        W = self.lm_head.weight
+        if self.fused_ops and self.head_work is not None and W.dtype == torch.float16 and W.is_contiguous():
+            try:
+                return lm_head_argmax(x, delta, self.norm.weight, self.cfg.eps, W, tok, pos, self.head_work)
+            except _lib.EptqError as e:
+                if e.code != _lib.EPTQ_EUNSUPPORTED:
+                    raise
+        logits = self.lm_head(rmsnorm_(x, delta, self.norm.weight, self.cfg.eps))
+        tok.copy_(logits.argmax(-1, keepdim=True))
+        pos.add_(1)
+        return logits
 
 
 def build_synthetic(cfg: LlamaConfig = LLAMA2_7B, device="cuda", seed: int = 4000,
@@ -378,11 +422,11 @@ class GraphDecoder:
     @torch.no_grad()
     def _step(self):
         if self.fused:
-            logits = self.model.decode_tokens(self.tok, self.pos)
+            self.model.decode_next(self.tok, self.pos)
         else:
             logits = self.model.forward_tokens(self.tok, self.pos)[:, -1]
-        self.tok.copy_(logits.argmax(-1, keepdim=True))
-        self.pos.add_(1)
+            self.tok.copy_(logits.argmax(-1, keepdim=True))
+            self.pos.add_(1)
 
     @torch.no_grad()
     def capture(self):

@@ -7,7 +7,7 @@
  * embedding, attention over a StaticCache, SiLU gating) driven by
  * bench_decode.py:44-71.  Same conventions as eptq_hip.h: device pointers,
  * fp16 data, asynchronous on `stream`, no allocation; 0 = ok, 1 = invalid
- * argument, 2 = unsupported shape (eptq_llama_norm_linear), 3 = HIP launch error.
+ * argument, 2 = unsupported shape, 3 = HIP launch error.
  */
 #ifndef EPTQ_LLAMA_H
 #define EPTQ_LLAMA_H
@@ -70,6 +70,22 @@ int eptq_llama_norm_linear(int n_layers, const eptq_layer* layers, const void* c
  * Linears and the SiLU product as separate operators (bench_decode.py). */
 int eptq_llama_norm_swiglu(const eptq_layer* gate_up, const void* codes, const void* resid, const void* delta,
                            const void* w, float eps, void* resid_out, int N, int B, void* out, void* stream);
+
+/* Bytes of the eptq_llama_lm_head_argmax workspace for B batch rows
+ * (zero-filled before its first use; every call leaves it zeroed). */
+long long eptq_llama_lm_head_work_bytes(int B);
+
+/* The decode step's tail in one launch: t = w ⊙ r · rsqrt(mean(r²) + eps) for
+ * r = x + delta (delta may be NULL; the roundings of eptq_llama_rmsnorm),
+ * logits (B, V) fp16 = t · Wᵀ for the fp16 lm_head weight W (V, H) row-major,
+ * tok[b] (int64) = the index of the largest fp16 logit of row b (the smallest
+ * index among equal ones), and *pos += 1 (int64) when pos is not NULL.
+ * work: eptq_llama_lm_head_work_bytes(B) bytes, 8-byte aligned; calls sharing
+ * it must not overlap in time.  B <= 2 and H in {4096, 6144, 8192}, 2
+ * (unsupported) otherwise.  No counterpart in the reference, which runs the
+ * final norm, lm_head and argmax as separate ops (bench_decode.py:44-71). */
+int eptq_llama_lm_head_argmax(const void* x, const void* delta, const void* w, float eps, const void* W, int V,
+                              int H, int B, void* logits, void* tok, void* pos, void* work, void* stream);
 
 #ifdef __cplusplus
 }

@@ -183,3 +183,9 @@ def test_fused_llama_linears_validate_arguments(lib):
     pair[1].M = 8
     assert g(pair, 16, 16, None, 16, 1e-5, None, 64, 1, 16, None) == _lib.EPTQ_EINVAL             # M differ
     assert "differ" in lib.eptq_last_error().decode()
+    h = lib.eptq_llama_lm_head_argmax
+    assert lib.eptq_llama_lm_head_work_bytes(2) >= 24
+    assert h(None, None, 16, 1e-5, 16, 100, 4096, 1, 16, 16, None, 16, None) == 1          # null x
+    assert h(16, None, 16, 1e-5, 16, 100, 4096, 1, 16, 16, None, 20, None) == 1            # work misaligned
+    assert h(16, None, 16, 1e-5, 16, 100, 4096, 3, 16, 16, None, 16, None) == 2            # B > 2
+    assert h(16, None, 16, 1e-5, 16, 100, 1000, 1, 16, 16, None, 16, None) == 2            # hidden size
