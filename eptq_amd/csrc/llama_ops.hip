@@ -373,12 +373,13 @@ __global__ __launch_bounds__(kT) void k_silu_mul(const f16* __restrict__ gu, f16
 
 // ---- the decode step's tail: final RMSNorm + lm_head + greedy argmax -------
 //
-// Every workgroup forms t = RMSNorm(x + delta) for the B rows in LDS with the
-// chunk order and roundings of k_rmsnorm (so t is bit-identical to it), then
-// each wave streams vocab rows v = wave id + k · waves: lane l holds columns
-// 8(64c + l) .. +7 (c < CH) of t in registers and of W row v (a wave load
-// covers 1 KB of the row), fp32 dot2 sums, a wave reduction, and lane 0
-// writes fp16 logits[b][v].  The greedy choice is the largest fp16 logit,
+// Every workgroup forms t = RMSNorm(x + delta) for the nb <= B rows in LDS
+// with the chunk order and roundings of k_rmsnorm (so t is bit-identical to
+// it), then each wave streams vocab rows v = wave id + k · waves: lane l
+// holds columns 8(64c + l) .. +7 (c < CH) of W row v (a wave load covers 1 KB
+// of the row) and of t — in registers for B <= 2, read from LDS per row
+// otherwise (1 KB contiguous per wave load, no bank conflicts) — fp32 dot2
+// sums, a wave reduction, and lane 0 writes fp16 logits[b][v].  The greedy choice is the largest fp16 logit,
 // the smallest index among equal ones (as torch.argmax): an order-preserving
 // 64-bit key per (b, v), reduced per workgroup and combined with one
 // device-scope atomic max per batch row; the last workgroup to finish (an
@@ -407,13 +408,16 @@ __device__ __forceinline__ float dot8(const u32x4 a, const u32x4 b, float acc) {
 template <int B, int CH>
 __global__ __launch_bounds__(kT) void k_lm_head_argmax(const f16* __restrict__ x, const f16* __restrict__ delta,
                                                        const f16* __restrict__ nw, float eps,
-                                                       const f16* __restrict__ W, int V, f16* __restrict__ logits,
-                                                       int64_t* __restrict__ tok, int64_t* __restrict__ pos,
+                                                       const f16* __restrict__ W, int V, int nb,
+                                                       f16* __restrict__ logits, int64_t* __restrict__ tok,
+                                                       int64_t* __restrict__ pos,
                                                        unsigned long long* __restrict__ keys, int* __restrict__ cnt) {
   constexpr int H = CH * 512;
   constexpr int MAXV = H / 8 / kT;   // 16-byte chunks per thread in the norm (H/8 chunks over kT threads)
   static_assert(MAXV * kT * 8 == H, "H is a multiple of 2048");
-  __shared__ __attribute__((aligned(16))) f16 ts[B][H];
+  constexpr bool TREG = B <= 2;      // t in registers (else read from LDS per row)
+  extern __shared__ __attribute__((aligned(16))) char head_dyn[];
+  f16 (*ts)[H] = (f16 (*)[H])head_dyn;   // [B][H]
   __shared__ float sh[kT / 64];
   __shared__ unsigned long long wbest[B][kT / 64];
   __shared__ int s_last;
@@ -421,6 +425,7 @@ __global__ __launch_bounds__(kT) void k_lm_head_argmax(const f16* __restrict__ x
   // t = fp16(w ⊙ r · rsqrt(mean(r²) + eps)), r = fp16(x + delta): k_rmsnorm's steps.
 #pragma unroll
   for (int b = 0; b < B; ++b) {
+    if (b >= nb) break;   // uniform
     f16x8 v[MAXV];
     float ss = 0.0f;
 #pragma unroll
@@ -448,11 +453,13 @@ __global__ __launch_bounds__(kT) void k_lm_head_argmax(const f16* __restrict__ x
     }
   }
   __syncthreads();
-  u32x4 tr[B][CH];
+  u32x4 tr[TREG ? B : 1][CH];
+  if constexpr (TREG) {
 #pragma unroll
-  for (int b = 0; b < B; ++b)
+    for (int b = 0; b < B; ++b)
 #pragma unroll
-    for (int c = 0; c < CH; ++c) tr[b][c] = *(const u32x4*)&ts[b][(c * 64 + lane) * 8];
+      for (int c = 0; c < CH; ++c) tr[b][c] = *(const u32x4*)&ts[b][(c * 64 + lane) * 8];
+  }
 
   const int waves = (int)gridDim.x * (kT / 64);
   unsigned long long best[B];
@@ -466,9 +473,11 @@ __global__ __launch_bounds__(kT) void k_lm_head_argmax(const f16* __restrict__ x
   auto row = [&](int v, const u32x4 (&w)[CH]) {
 #pragma unroll
     for (int b = 0; b < B; ++b) {
+      if (b >= nb) break;   // uniform
       float s = 0.0f;
 #pragma unroll
-      for (int c = 0; c < CH; ++c) s = dot8(w[c], tr[b][c], s);
+      for (int c = 0; c < CH; ++c)
+        s = dot8(w[c], TREG ? tr[TREG ? b : 0][c] : *(const u32x4*)&ts[b][(c * 64 + lane) * 8], s);
       s += partner<1>(s);
       s += partner<2>(s);
       s += partner<4>(s);
@@ -503,7 +512,7 @@ __global__ __launch_bounds__(kT) void k_lm_head_argmax(const f16* __restrict__ x
     for (int b = 0; b < B; ++b) wbest[b][wave] = best[b];
   }
   __syncthreads();
-  if (t < B) {
+  if (t < nb) {
     unsigned long long m = wbest[t][0];
 #pragma unroll
     for (int w2 = 1; w2 < kT / 64; ++w2) m = wbest[t][w2] > m ? wbest[t][w2] : m;
@@ -518,7 +527,7 @@ __global__ __launch_bounds__(kT) void k_lm_head_argmax(const f16* __restrict__ x
   }
   __syncthreads();
   if (!s_last) return;
-  if (t < B) {
+  if (t < nb) {
     const unsigned long long k = __hip_atomic_load(keys + t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     tok[t] = (int64_t)(0xFFFFFFFFu - (uint32_t)(k & 0xFFFFFFFFull));
     __hip_atomic_store(keys + t, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -527,15 +536,22 @@ __global__ __launch_bounds__(kT) void k_lm_head_argmax(const f16* __restrict__ x
 }
 
 template <int B, int CH>
-int launch_head(const f16* x, const f16* delta, const f16* w, float eps, const f16* W, int V, f16* logits,
+int launch_head(const f16* x, const f16* delta, const f16* w, float eps, const f16* W, int V, int nb, f16* logits,
                 int64_t* tok, int64_t* pos, unsigned long long* keys, int* cnt, hipStream_t s) {
   int dev = 0, cus = 256;
   if (hipGetDevice(&dev) == hipSuccess) (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
   int G = cus * kHeadPerCu;
   const int rows_per_wg = kT / 64;
   if (G * rows_per_wg > V) G = (V + rows_per_wg - 1) / rows_per_wg;
-  hipLaunchKernelGGL((k_lm_head_argmax<B, CH>), dim3(G), dim3(kT), 0, s, x, delta, w, eps, W, V, logits, tok, pos,
-                     keys, cnt);
+  auto kern = k_lm_head_argmax<B, CH>;
+  const size_t dyn = (size_t)B * CH * 512 * 2;
+  static size_t attr = 0;
+  if (dyn > 64 * 1024 && dyn > attr) {
+    if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)dyn) != hipSuccess)
+      return 3;
+    attr = dyn;
+  }
+  hipLaunchKernelGGL(kern, dim3(G), dim3(kT), dyn, s, x, delta, w, eps, W, V, nb, logits, tok, pos, keys, cnt);
   return 0;
 }
 
@@ -594,7 +610,7 @@ int eptq_llama_lm_head_argmax(const void* x, const void* delta, const void* w, f
   if (!x || !w || !W || !logits || !tok || !work || V <= 0 || B <= 0) return 1;
   if (((uintptr_t)x | (uintptr_t)w | (uintptr_t)W | (uintptr_t)(delta ? delta : x)) & 15) return 1;
   if (((uintptr_t)work & 7) || ((uintptr_t)logits & 1) || ((uintptr_t)tok & 7) || ((uintptr_t)pos & 7)) return 1;
-  if (B > 2 || (H != 4096 && H != 6144 && H != 8192)) return 2;
+  if (B > 8 || (H != 4096 && H != 6144 && H != 8192) || (size_t)B * H * 2 > 128 * 1024) return 2;
   using eptq::f16;
   auto* keys = (unsigned long long*)work;
   int* cnt = (int*)(keys + B);
@@ -603,15 +619,17 @@ int eptq_llama_lm_head_argmax(const void* x, const void* delta, const void* w, f
   f16* pl = (f16*)logits;
   int64_t *pt = (int64_t*)tok, *pp = (int64_t*)pos;
   const int CH = H / 512;
-  if (B == 1) {
-    if (CH == 8) eptq::launch_head<1, 8>(px, pd, pw, eps, pW, V, pl, pt, pp, keys, cnt, s);
-    else if (CH == 12) eptq::launch_head<1, 12>(px, pd, pw, eps, pW, V, pl, pt, pp, keys, cnt, s);
-    else eptq::launch_head<1, 16>(px, pd, pw, eps, pW, V, pl, pt, pp, keys, cnt, s);
-  } else {
-    if (CH == 8) eptq::launch_head<2, 8>(px, pd, pw, eps, pW, V, pl, pt, pp, keys, cnt, s);
-    else if (CH == 12) eptq::launch_head<2, 12>(px, pd, pw, eps, pW, V, pl, pt, pp, keys, cnt, s);
-    else eptq::launch_head<2, 16>(px, pd, pw, eps, pW, V, pl, pt, pp, keys, cnt, s);
-  }
+  int rc = 0;
+#define EPTQ_HEAD(BT)                                                                                   \
+  rc = CH == 8    ? eptq::launch_head<BT, 8>(px, pd, pw, eps, pW, V, B, pl, pt, pp, keys, cnt, s)      \
+       : CH == 12 ? eptq::launch_head<BT, 12>(px, pd, pw, eps, pW, V, B, pl, pt, pp, keys, cnt, s)     \
+                  : eptq::launch_head<BT, 16>(px, pd, pw, eps, pW, V, B, pl, pt, pp, keys, cnt, s)
+  if (B == 1) { EPTQ_HEAD(1); }
+  else if (B == 2) { EPTQ_HEAD(2); }
+  else if (B <= 4) { EPTQ_HEAD(4); }
+  else { EPTQ_HEAD(8); }
+#undef EPTQ_HEAD
+  if (rc) return rc;
   return hipGetLastError() == hipSuccess ? 0 : 3;
 }
 

@@ -133,7 +133,7 @@ def norm_swiglu(mod, resid, delta, w, eps, resid_out):
 
 def lm_head_argmax(x, delta, w, eps, W, tok, pos, work):
     """logits (B, V) = RMSNorm(x + delta) · Wᵀ, tok[:, 0] <- argmax, pos += 1,
-    in one launch.  Raises EptqError (code EPTQ_EUNSUPPORTED) for B > 2 or an
+    in one launch.  Raises EptqError (code EPTQ_EUNSUPPORTED) for B > 8 or an
     unsupported hidden size."""
     B, H = x.shape
     V = W.shape[0]
@@ -242,9 +242,9 @@ class QuantLlama(nn.Module):
         # Split-K workspace of the decode Linears (batches of 5..16): the
         # decode step's launches run one after another on one stream.
         self.lin_work = decode_workspace(device)
-        # Workspace of the fused final norm + lm_head + argmax (B <= 2).
+        # Workspace of the fused final norm + lm_head + argmax (B <= 8).
         self.head_work = None
-        if batch <= 2:
+        if batch <= 8:
             nbytes = _lib.load().eptq_llama_lm_head_work_bytes(batch)
             self.head_work = torch.zeros(nbytes, dtype=torch.uint8, device=device)
 
@@ -340,7 +340,7 @@ class QuantLlama(nn.Module):
 
     def decode_next(self, tok, pos):
         """One greedy step in place: logits (B, vocab) for tok at pos, then
-        tok <- argmax(logits) and pos += 1.  With ``fused_ops`` and B <= 2
+        tok <- argmax(logits) and pos += 1.  With ``fused_ops`` and B <= 8
         the final norm, lm_head, argmax and position advance are one launch
         (``eptq_llama_lm_head_argmax``); otherwise PyTorch's lm_head and
         argmax follow the decode step."""

@@ -81,8 +81,8 @@ long long eptq_llama_lm_head_work_bytes(int B);
  * tok[b] (int64) = the index of the largest fp16 logit of row b (the smallest
  * index among equal ones), and *pos += 1 (int64) when pos is not NULL.
  * work: eptq_llama_lm_head_work_bytes(B) bytes, 8-byte aligned; calls sharing
- * it must not overlap in time.  B <= 2 and H in {4096, 6144, 8192}, 2
- * (unsupported) otherwise.  No counterpart in the reference, which runs the
+ * it must not overlap in time.  B <= 8, H in {4096, 6144, 8192} and B·H·2 <=
+ * 128 KB; 2 (unsupported) otherwise.  No counterpart in the reference, which runs the
  * final norm, lm_head and argmax as separate ops (bench_decode.py:44-71). */
 int eptq_llama_lm_head_argmax(const void* x, const void* delta, const void* w, float eps, const void* W, int V,
                               int H, int B, void* logits, void* tok, void* pos, void* work, void* stream);

@@ -187,5 +187,5 @@ def test_fused_llama_linears_validate_arguments(lib):
     assert lib.eptq_llama_lm_head_work_bytes(2) >= 24
     assert h(None, None, 16, 1e-5, 16, 100, 4096, 1, 16, 16, None, 16, None) == 1          # null x
     assert h(16, None, 16, 1e-5, 16, 100, 4096, 1, 16, 16, None, 20, None) == 1            # work misaligned
-    assert h(16, None, 16, 1e-5, 16, 100, 4096, 3, 16, 16, None, 16, None) == 2            # B > 2
+    assert h(16, None, 16, 1e-5, 16, 100, 4096, 9, 16, 16, None, 16, None) == 2            # B > 8
     assert h(16, None, 16, 1e-5, 16, 100, 1000, 1, 16, 16, None, 16, None) == 2            # hidden size

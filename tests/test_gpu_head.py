@@ -41,7 +41,8 @@ def _work(B):
 
 
 @pytest.mark.parametrize("B,H,V,delta", [(1, 4096, 32000, True), (2, 4096, 1000, True), (1, 8192, 777, False),
-                                         (2, 6144, 64, True)])
+                                         (2, 6144, 64, True), (3, 4096, 2000, True), (8, 4096, 32000, True),
+                                         (5, 8192, 513, False), (8, 6144, 100, True)])
 def test_head_matches_fp32_reference(B, H, V, delta):
     print(f"lm_head+argmax B={B} H={H} V={V} delta={delta}", flush=True)
     x, d, w, W = _setup(B, H, V, seed=B + H + V, delta=delta)
@@ -116,7 +117,7 @@ def test_decode_next_matches_decode_tokens_and_argmax():
     print("synthetic llama: decode_next vs decode_tokens + argmax", flush=True)
     cfg = LlamaConfig(hidden=4096, ffn=1024, layers=1, heads=32, kv_heads=32, vocab=2048)
     model = build_synthetic(cfg, device="cuda", seed=21)
-    for B in (1, 2):
+    for B in (1, 2, 8):
         model.alloc_cache(B, 16, "cuda")
         tok = torch.randint(0, cfg.vocab, (B, 1), device="cuda", generator=torch.Generator("cuda").manual_seed(B))
         pos = torch.tensor([3], device="cuda")
