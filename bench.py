@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark: E8-D4 fused decode matvec on synthetic Llama-2-7B layers, one MI355X.
 
-Workload (``config.workload`` = llama2_7b_decoder_linears_decode; BASELINE
+Workload (``config.workload`` = llama2_7b_decoder_linears_decode; benchmark
 configuration 1 at batch 1): the seven quantized Linears of each of
 Llama-2-7B's 32 decoder layers — q/k/v/o 4096x4096, gate/up 11008x4096, down
 4096x11008 — E8-D4 codebook at radius 1.75, 0.1% critical blocks, seeded
@@ -25,15 +25,15 @@ JSON fields beyond the driver contract:
   one step, each scaled by the same counter's reading for a 512 MiB device
   copy; the passes run as child processes before this process touches the GPU.
 * ``e2e`` — tokens/s of the synthetic Llama-2-7B (every decoder Linear a
-  synthetic E8-D4 layer): 128-token prompt, greedy
+  synthetic E8-D4 layer, benchmark configuration 4): 128-token prompt, greedy
   decode, graph-captured step, prefill untimed, batch 1 and 8.
 * ``decode_batches`` — the decode-step Linear units (q|k|v, o, gate|up,
-  down) of Llama-2-7B at batch 1 and 8 and of
+  down) of Llama-2-7B at batch 1 and 8 (benchmark configuration 1) and of
   Llama-3-8B with S_group qb=128 at batch 1, 4 and 16 (configuration 2), one
   launch each with the decode workspace: microseconds and algorithmic GB/s.
   Batches of 5..16 run the matrix-core decode kernel.
 * ``prefill`` — the MFMA GEMM on the Llama-2-13B shapes at 2048 tokens
-  TFLOP/s and fraction of the 2.5 PFLOP/s fp16
+  (benchmark configuration 3): TFLOP/s and fraction of the 2.5 PFLOP/s fp16
   dense MFMA peak.
 * ``cpu_baseline`` — the reference CPU path (per-column ``dequantize_layer``
   restatement + fp32 ``torch.matmul``) on one decoder layer's seven Linears at

@@ -12,7 +12,7 @@ baseline), the reference algorithms the HIP path must reproduce:
   bit-exact definition of the fp16 weight, plus the CSR build of
   ``kernels/linear.py:122-139``.
 * ``matvec``     — the fused decode math of ``test_e8_cuda.py:23-53`` /
-  ``csrc/eptq_kernels.cu:161-292`` in float64, and the BASELINE CPU path
+  ``csrc/eptq_kernels.cu:161-292`` in float64, and the reference's CPU path
   (dequantize + fp32 matmul).
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s

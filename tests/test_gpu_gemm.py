@@ -68,7 +68,7 @@ def test_gemm_e8_rel_l2(out, inp, T, p, bias, qb):
 
 
 def test_gemm_config3_shape():
-    """Llama-2-13B q/k/v/o layer, 2048 tokens."""
+    """Llama-2-13B q/k/v/o layer, 2048 tokens (the prefill benchmark shape)."""
     print("gemm 5120x5120 T=2048", flush=True)
     qd = make_layer(5120, 5120, seed=3000, percmask=0.002)
     x = make_x(2048, 5120, seed=3001)

@@ -1,6 +1,6 @@
 """GPU parity: the fused HIP quantized Linear (decode matvec B<=16, GEMM above)
 is within 1e-2 relative L2 of the fp32 reconstruct+matmul reference
-(oracle.matvec.linear_ref), on the BASELINE layer distributions."""
+(oracle.matvec.linear_ref), on the benchmark configurations' layer distributions (g, h, x, O)."""
 
 import numpy as np
 import pytest
