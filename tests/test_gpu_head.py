@@ -134,3 +134,38 @@ def test_decode_next_matches_decode_tokens_and_argmax():
         assert rel_l2(got.float().cpu().numpy(), ref.float().cpu().numpy()) < 2e-3, B
         assert torch.equal(t2[:, 0].cpu(), got.cpu().argmax(-1)), B
         assert int(p2.item()) == 4
+
+
+@pytest.mark.parametrize("B", [1, 8])
+def test_graph_decode_with_fused_tail_crosses_the_chunk_boundary(B):
+    """Greedy decode from a 250-token prompt for 12 steps (positions 250..261,
+    across the attention kernel's 256-row chunk), replayed from one HIP graph
+    with the fused tail, against the same steps run eagerly: same tokens at
+    every step, and the fused tail (not the PyTorch fallback) ran."""
+    import eptq_amd.llama as LL
+    from eptq_amd.llama import GraphDecoder, LlamaConfig, build_synthetic
+    print(f"synthetic llama: graph decode with fused tail, B={B}", flush=True)
+    cfg = LlamaConfig(hidden=4096, ffn=1024, layers=1, heads=32, kv_heads=32, vocab=4096)
+    model = build_synthetic(cfg, device="cuda", seed=31)
+    dec = GraphDecoder(model, B, 272, device="cuda")
+    prompt = torch.randint(0, cfg.vocab, (B, 250), device="cuda", generator=torch.Generator("cuda").manual_seed(B))
+    calls = []
+    real = LL.lm_head_argmax
+    LL.lm_head_argmax = lambda *a, **k: (calls.append(1), real(*a, **k))[1]
+    try:
+        dec.prefill(prompt)
+        eager = []
+        for _ in range(12):
+            dec.step()
+            eager.append(dec.tok.clone())
+        assert len(calls) == 12, "the fused tail ran at every eager step"
+        assert int(dec.pos.item()) == 262
+    finally:
+        LL.lm_head_argmax = real
+    dec.prefill(prompt)
+    dec.capture()
+    for i in range(12):
+        dec.step()
+        torch.cuda.synchronize()
+        assert torch.equal(dec.tok, eager[i]), f"token {i}"
+    assert int(dec.pos.item()) == 262
