@@ -13,7 +13,7 @@
 //  * k_silu_mul:    a = silu(gate) ⊙ up from the fused gate|up projection.
 //  * k_lm_head_argmax: the step's tail — final RMSNorm, the fp16 lm_head
 //                   matvec, the logits, the greedy next token and the position
-//                   advance — in one launch (B <= 2).
+//                   advance — in one launch (B <= 8).
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
