@@ -560,7 +560,7 @@ int launch_head(const f16* x, const f16* delta, const f16* w, float eps, const f
 
 extern "C" {
 
-// Return codes as in eptq_hip.h: 0 ok, 1 invalid argument, 3 HIP launch error.
+// Return codes: 0 ok, 1 invalid argument, 2 unsupported shape, 3 HIP launch error.
 
 int eptq_llama_rmsnorm(void* x, const void* delta, const void* w, void* y, int B, int H, float eps,
                        void* stream) {
