@@ -35,6 +35,9 @@ JSON fields beyond the driver contract:
 * ``prefill`` — the MFMA GEMM on the Llama-2-13B shapes at 2048 tokens
   (benchmark configuration 3): TFLOP/s and fraction of the 2.5 PFLOP/s fp16
   dense MFMA peak.
+* ``dequant`` — the bit-exact dequantizer (``eptq_e8d4_dequant``, fp16 W of
+  ``dequantize_layer``) on the Llama-2-7B shapes: algorithmic GB/s (index
+  and scale reads plus the W write) and fraction of HBM peak.
 * ``cpu_baseline`` — the reference CPU path (per-column ``dequantize_layer``
   restatement + fp32 ``torch.matmul``) on one decoder layer's seven Linears at
   batch 1, timed on this host's cores.
@@ -430,6 +433,37 @@ def decode_batches(torch, dev, stream_bytes=320 << 20):
     return out
 
 
+def dequant_layers(torch, dev, reps=10):
+    """Bit-exact dequantization (``eptq_e8d4_dequant``: the fp16 W of the
+    reference's ``dequantize_layer``) of the Llama-2-7B Linear shapes.
+    Algorithmic bytes: Q, g, h and the CSR (16-byte O rows, 4-byte columns,
+    row pointers) read once, W (2 bytes per weight) written once; HBM
+    roofline (the write of W dominates: 16x the index bytes)."""
+    from eptq_amd.kernels import dequant
+    from eptq_amd.kernels.linear import EPTQLinear
+    from eptq_amd.quantizers import E8D4Quantizer
+    from eptq_amd.synthetic import make_layer
+
+    q = E8D4Quantizer(radius=1.75)
+    stream = torch.cuda.current_stream()
+    out = {}
+    for idx, (name, o, i) in enumerate((("4096x4096", 4096, 4096), ("11008x4096", 11008, 4096),
+                                        ("4096x11008", 4096, 11008))):
+        lin = EPTQLinear.from_quantized_data(make_layer(o, i, seed=4000 + idx, percmask=0.001, device=dev),
+                                             q, "e8_d4").to(dev)
+        args = ("e8_d4", lin.Q, lin._table_f32.to(dev), lin.g, lin.h, lin.O_vals, lin.O_col, lin.O_row_ptr)
+        M, N, nnz = lin.Q.shape[0], lin.Q.shape[1], lin.O_col.numel()
+        nbytes = 2 * M * N + 2 * 8 * M + 2 * N + 20 * nnz + 4 * (M + 1) + 2 * 8 * M * N
+        dequant(*args)
+        d, _ = event_timed(torch, [lambda: dequant(*args)] * reps, stream)
+        us = statistics.median(d) * 1e3
+        gbs = nbytes / (us * 1e-6) / 1e9
+        out[name] = {"us": round(us, 2), "gbs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+                     "algorithmic_bytes": nbytes}
+        del lin
+    return out
+
+
 def prefill_gemm(torch, dev, T=2048, reps=10):
     from eptq_amd.kernels import _lib
     from eptq_amd.quantizers import E8D4Quantizer
@@ -474,6 +508,7 @@ def main():
     ap.add_argument("--no-e2e", action="store_true")
     ap.add_argument("--no-batches", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-dequant", action="store_true")
     ap.add_argument("--pmc-timeout", type=int, default=240)
     ap.add_argument("--probe-traffic", action="store_true", help=argparse.SUPPRESS)
     args = ap.parse_args()
@@ -615,6 +650,9 @@ def main():
     if not args.no_prefill:
         rec["prefill"] = prefill_gemm(torch, dev)
         print(f"# prefill: {rec['prefill']}", file=sys.stderr, flush=True)
+    if not args.no_dequant:
+        rec["dequant"] = dequant_layers(torch, dev)
+        print(f"# dequant: {rec['dequant']}", file=sys.stderr, flush=True)
     if not args.no_cpu_baseline:
         rec["cpu_baseline"] = cpu_baseline()
     print(json.dumps(rec), flush=True)

@@ -9,9 +9,12 @@
 // The table must be the fp32 one the reference's loader produces
 // (reconstruct.py:52-62), so the bits match eptq.reconstruct.
 //
-// Layout: one thread per (Q-row m, 4 consecutive columns); it writes 4
-// consecutive fp16 (8 bytes) in each of the 8 output rows.  The kernel is
-// write-bound (16 bytes out per 2-byte index).
+// Layout: a thread takes (Q-row m, 8 consecutive columns) items with a
+// grid stride (consecutive threads, consecutive column chunks of one row):
+// one 16-byte index load and 16-byte g and h loads, and one 16-byte store in
+// each of the 8 output rows.  Workgroups stay resident and stage the E8-D4
+// table in LDS once.  The kernel is write-bound (16 bytes out per 2-byte
+// index).
 
 #include "common.h"
 #include "kernels.h"
@@ -28,99 +31,133 @@ __device__ __forceinline__ int csr_lower_bound(const int32_t* __restrict__ col,
   return lo;
 }
 
+constexpr int kDqPerCu = 8;   // resident workgroups per CU
+
 template <int KIND, bool HAS_S>
 __global__ __launch_bounds__(256) void k_dequant(
     const int16_t* __restrict__ Q, const float* __restrict__ table,
     const f16* __restrict__ g, const f16* __restrict__ h,
     const f16* __restrict__ O, const int32_t* __restrict__ O_col,
     const int32_t* __restrict__ O_row_ptr, const f16* __restrict__ S, int qb,
-    int M, int N, int chunks_per_row, f16* __restrict__ W) {
+    int M, int N, int chunks_per_row, int vec, f16* __restrict__ W) {
   __shared__ f32x4 tab[KIND == KIND_E8D4 ? 512 : 1];
   if (KIND == KIND_E8D4) {
     for (int i = threadIdx.x; i < 512; i += 256) tab[i] = ((const f32x4*)table)[i];
     __syncthreads();
   }
-  const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  const int m = (int)(gid / chunks_per_row);
-  if (m >= M) return;
-  const int n0 = (int)(gid - (int64_t)m * chunks_per_row) * 4;
-  const int r0 = O_row_ptr[m], r1 = O_row_ptr[m + 1];
-
-  float gk[8];
-#pragma unroll
-  for (int k = 0; k < 8; ++k) gk[k] = (float)g[8 * m + k];
-
-  f16 out[8][4];
-#pragma unroll
-  for (int c = 0; c < 4; ++c) {
-    const int n = n0 + c;
-    if (n >= N) {
-#pragma unroll
-      for (int k = 0; k < 8; ++k) out[k][c] = (f16)0.0f;
-      continue;
+  const int64_t items = (int64_t)M * chunks_per_row;
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  // 16-byte path: the next item's index, g and h chunks are requested before
+  // the current item is computed (one item in flight per thread).
+  u16x8 qnext = {};
+  f16x8 hnext = {}, gnext = {};
+  auto fetch = [&](int64_t i) {
+    if (vec && i < items) {
+      const int mm = (int)(i / chunks_per_row);
+      const int nn = (int)(i - (int64_t)mm * chunks_per_row) * 8;
+      qnext = *(const u16x8*)(Q + (size_t)mm * N + nn);
+      hnext = *(const f16x8*)(h + nn);
+      gnext = *(const f16x8*)(g + 8 * mm);
     }
-    const unsigned u = (unsigned)((int)Q[(size_t)m * N + n] + 32768);
-    float v[8];
-    if (u == 65535u) {
-      const int i = csr_lower_bound(O_col, r0, r1, n);
-      const bool hit = (i < r1) && (O_col[i] == n);
+  };
+  fetch((int64_t)blockIdx.x * 256 + threadIdx.x);
+  for (int64_t it = (int64_t)blockIdx.x * 256 + threadIdx.x; it < items; it += stride) {
+    const int m = (int)(it / chunks_per_row);
+    const int n0 = (int)(it - (int64_t)m * chunks_per_row) * 8;
+    // 16-byte accesses when the host found N % 8 == 0 and Q, g, h, W 16-byte
+    // aligned (every chunk then is whole); element by element otherwise.
+    const bool full = vec && n0 + 8 <= N;
+    const int r0 = O_row_ptr[m], r1 = O_row_ptr[m + 1];
+    float gk[8];
+    int16_t q8[8];
+    f16 h8[8];
+    if (vec) {
 #pragma unroll
-      for (int k = 0; k < 8; ++k) v[k] = hit ? (float)O[(size_t)i * 8 + k] : 0.0f;
+      for (int c = 0; c < 8; ++c) {
+        gk[c] = (float)gnext[c];
+        q8[c] = (int16_t)qnext[c];
+        h8[c] = hnext[c];
+      }
+      fetch(it + stride);
     } else {
-      f32x4 a, b;
-      if (KIND == KIND_E8D4) {
-        a = tab[u >> 7];
-        b = tab[((u >> 14) << 7) | (u & 127u)];
-      } else {
-        const f32x4* p = (const f32x4*)(table + (size_t)u * 8);
-        a = p[0];
-        b = p[1];
-      }
-      v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
-      v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
-      if (HAS_S) {
 #pragma unroll
-        for (int k = 0; k < 8; ++k)
-          v[k] = v[k] * (float)S[(size_t)((8 * m + k) / qb) * N + n];
+      for (int k = 0; k < 8; ++k) gk[k] = (float)g[8 * m + k];
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        q8[c] = n0 + c < N ? Q[(size_t)m * N + n0 + c] : (int16_t)0;
+        h8[c] = n0 + c < N ? h[n0 + c] : (f16)0.0f;
       }
     }
-    const float hn = (float)h[n];
+    f16x8 out[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      const int n = n0 + c;
+      const unsigned u = (unsigned)((int)q8[c] + 32768);
+      float v[8];
+      if (u == 65535u) {
+        const int i = csr_lower_bound(O_col, r0, r1, n);
+        const bool hit = (i < r1) && (O_col[i] == n);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) v[k] = hit ? (float)O[(size_t)i * 8 + k] : 0.0f;
+      } else {
+        f32x4 a, b;
+        if (KIND == KIND_E8D4) {
+          a = tab[u >> 7];
+          b = tab[((u >> 14) << 7) | (u & 127u)];
+        } else {
+          const f32x4* p = (const f32x4*)(table + (size_t)u * 8);
+          a = p[0];
+          b = p[1];
+        }
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+        v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+        if (HAS_S) {
+#pragma unroll
+          for (int k = 0; k < 8; ++k)
+            v[k] = n < N ? v[k] * (float)S[(size_t)((8 * m + k) / qb) * N + n] : v[k];
+        }
+      }
+      const float hn = (float)h8[c];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const float t = v[k] * gk[k];
+        float w = t * hn;
+        // The reference rounds twice: to fp32 at the multiply, then to fp16.
+        // Materialize the fp32 product so the compiler cannot fold multiply and
+        // conversion into one single-rounding mix instruction.
+        asm volatile("" : "+v"(w));
+        out[k][c] = (f16)w;
+      }
+    }
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
-      const float t = v[k] * gk[k];
-      float w = t * hn;
-      // The reference rounds twice: to fp32 at the multiply, then to fp16.
-      // Materialize the fp32 product so the compiler cannot fold multiply and
-      // conversion into one single-rounding mix instruction.
-      asm volatile("" : "+v"(w));
-      out[k][c] = (f16)w;
-    }
-  }
-  const bool full = (n0 + 3 < N) && ((N & 3) == 0);
-#pragma unroll
-  for (int k = 0; k < 8; ++k) {
-    f16* dst = W + (size_t)(8 * m + k) * N + n0;
-    if (full) {
-      f16x4 o4 = {out[k][0], out[k][1], out[k][2], out[k][3]};
-      *(f16x4*)dst = o4;
-    } else {
-      for (int c = 0; c < 4 && n0 + c < N; ++c) dst[c] = out[k][c];
+      f16* dst = W + (size_t)(8 * m + k) * N + n0;
+      if (full) {
+        __builtin_nontemporal_store(out[k], (f16x8*)dst);   // streamed out, not re-read here
+      } else {
+        for (int c = 0; c < 8 && n0 + c < N; ++c) dst[c] = out[k][c];
+      }
     }
   }
 }
 
 template <int KIND>
 int launch_dequant(const DequantArgs& a, hipStream_t s) {
-  const int chunks = (a.N + 3) / 4;
-  const int64_t threads = (int64_t)a.M * chunks;
-  const int64_t blocks = (threads + 255) / 256;
-  if (blocks > 0x7fffffff) return -1;
+  const int chunks = (a.N + 7) / 8;
+  const int64_t items = (int64_t)a.M * chunks;
+  int dev = 0, cus = 256;
+  if (hipGetDevice(&dev) == hipSuccess) (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  const int vec = (a.N % 8 == 0) &&
+                  ((((uintptr_t)a.Q | (uintptr_t)a.g | (uintptr_t)a.h | (uintptr_t)a.W) & 15u) == 0);
+  int64_t blocks = (items + 255) / 256;
+  if (blocks > (int64_t)cus * kDqPerCu) blocks = (int64_t)cus * kDqPerCu;
+  if (blocks < 1) return 0;
   if (a.S)
     k_dequant<KIND, true><<<(unsigned)blocks, 256, 0, s>>>(
-        a.Q, a.table, a.g, a.h, a.O, a.O_col, a.O_row_ptr, a.S, a.qb, a.M, a.N, chunks, a.W);
+        a.Q, a.table, a.g, a.h, a.O, a.O_col, a.O_row_ptr, a.S, a.qb, a.M, a.N, chunks, vec, a.W);
   else
     k_dequant<KIND, false><<<(unsigned)blocks, 256, 0, s>>>(
-        a.Q, a.table, a.g, a.h, a.O, a.O_col, a.O_row_ptr, nullptr, 1, a.M, a.N, chunks, a.W);
+        a.Q, a.table, a.g, a.h, a.O, a.O_col, a.O_row_ptr, nullptr, 1, a.M, a.N, chunks, vec, a.W);
   return 0;
 }
 

@@ -34,7 +34,8 @@ def _assert_bits(W, ref):
 @pytest.mark.parametrize("kind,radius", [("e8_d4", 1.75), ("e8_lattice", 1.6)])
 @pytest.mark.parametrize("shape,p,qb", [((64, 256), 0.01, None), ((256, 1000), 0.002, None),
                                         ((512, 4096), 0.001, None), ((256, 512), 0.002, 128),
-                                        ((3072, 768), 0.002, None), ((24, 20), 0.05, 8)])
+                                        ((3072, 768), 0.002, None), ((24, 20), 0.05, 8),
+                                        ((11008, 4096), 0.001, None)])
 def test_dequant_bit_exact(kind, radius, shape, p, qb):
     print(f"dequant {kind} {shape} p={p} qb={qb}", flush=True)
     qd = make_layer(*shape, seed=shape[0] * 7 + shape[1] + len(kind), percmask=p, qb_size=qb)
