@@ -363,8 +363,30 @@ __global__ __launch_bounds__(kGT, 2) void k_gemm_e8(LinearArgs a, int OB) {
   gemm_tile<KIND_E8, HAS_S>(a, OB);
 }
 
+// Up to this many tokens an E8-D4 launch runs as 16-token slices of the
+// matrix-core decode kernel: its 64-row tiles spread a layer over far more
+// workgroups than the GEMM's 128-token tiles can at these token counts (one
+// token tile: 32 workgroups for 4096 rows), and the slices re-read the weight
+// from cache.  Measured at 32 / 128 / 256 tokens on 4096x4096: slices 27 /
+// 106 / 214 us against 112 us for the GEMM; 4096x11008: 59 / 226 / 459 us
+// against 285-290 us.
+constexpr int kSliceMaxTokens = 128;
+
 template <int KIND>
 int launch_gemm(const LinearArgs& a, hipStream_t s) {
+  if (KIND == KIND_E8D4 && a.B <= kSliceMaxTokens && a.prep == 0) {
+    // Eligibility does not depend on the slice (B = 1..16 all qualify), so a
+    // first slice that launches means every slice does.
+    int rc = 0;
+    for (int b0 = 0; b0 < a.B && rc == 0; b0 += kMatvecMaxBatch) {
+      LinearArgs t = a;
+      t.B = a.B - b0 < kMatvecMaxBatch ? a.B - b0 : kMatvecMaxBatch;
+      t.x = a.x + (size_t)b0 * a.ldx;
+      t.y = a.y + (size_t)b0 * a.ldy;
+      rc = launch_decode_mfma_multi(&t, 1, s);
+    }
+    if (rc == 0) return 0;
+  }
   // MFMA path: fp16 activations, fp16 table, whole 16-Q-row tiles, K-steps
   // of 32.  Anything else takes batch tiles of the decode matvec.
   const bool mfma_ok = !a.x_bf16 && !a.codes_f32 && (a.N % kBK) == 0 && (a.M % kBQ) == 0 &&

@@ -1,7 +1,9 @@
-"""GPU parity for the prefill path (batch > 16): the dequant-to-LDS MFMA GEMM
-is within 1e-2 relative L2 of the fp32 reconstruct+matmul reference
-(oracle.matvec.linear_ref), including critical blocks, S_group, bias and
-partial token tiles."""
+"""GPU parity for the prefill path (batch > 16): E8-D4 launches of up to 128
+tokens run as 16-token slices of the matrix-core decode kernel, larger ones
+(and E8) the dequant-to-LDS MFMA GEMM; both within 1e-2 relative L2 of the
+fp32 reconstruct+matmul reference (oracle.matvec.linear_ref), including
+critical blocks, S_group, bias, a ragged last slice and partial token
+tiles."""
 
 import numpy as np
 import pytest
@@ -32,10 +34,11 @@ def _run(qd, x, kind="e8_d4", radius=1.75):
 
 
 @pytest.mark.parametrize("out,inp,T,p,bias,qb", [
-    (1024, 1024, 128, 0.002, False, None),
+    (1024, 1024, 128, 0.002, False, None),     # 8 slices of 16 tokens
+    (1024, 1024, 256, 0.002, False, None),     # GEMM: two whole token tiles
     (1024, 2048, 300, 0.002, True, None),      # partial token tile
     (2048, 1024, 64, 0.01, False, 128),        # S_group, more critical blocks
-    (512, 512, 17, 0.002, False, None),        # just above the matvec range
+    (512, 512, 17, 0.002, False, None),        # just above the matvec range: a 1-token last slice
     (256, 4096, 1000, 0.05, True, 64),         # dense markers: > LDS entry cap per tile
     (1152, 1024, 200, 0.002, True, 128),       # 144 Q-rows: 9 row tiles, S_group and bias
 ])
