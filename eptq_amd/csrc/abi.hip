@@ -277,6 +277,23 @@ int eptq_e8d4_forward_multi(int n_layers, const eptq_layer* layers, const void* 
   }
   if (B == 0) return EPTQ_OK;
   hipStream_t s = (hipStream_t)stream;
+  // 17..128 rows: 16-row slices of the matrix-core decode kernel, every layer
+  // in each slice's launch (its eligibility does not depend on the slice's
+  // row count, so a first slice that launches means every slice does).
+  if (B > eptq::kMatvecMaxBatch && B <= eptq::kSliceMaxTokens && n <= eptq::kMaxLayers) {
+    int rc = 0;
+    for (int b0 = 0; b0 < B && rc == 0; b0 += eptq::kMatvecMaxBatch) {
+      eptq::LinearArgs sl[eptq::kMaxLayers];
+      for (int l = 0; l < n; ++l) {
+        sl[l] = a[l];
+        sl[l].B = B - b0 < eptq::kMatvecMaxBatch ? B - b0 : eptq::kMatvecMaxBatch;
+        sl[l].x = a[l].x + (size_t)b0 * a[l].ldx;
+        sl[l].y = a[l].y + (size_t)b0 * ldy;
+      }
+      rc = eptq::launch_decode_mfma_multi(sl, n, s, work, work ? work_bytes : 0);
+    }
+    if (rc == 0) return check_launch(fn);
+  }
   // One launch when the decode kernel takes them all, else one per layer.
   if (n > eptq::kMaxLayers || eptq::launch_decode_e8d4_multi(a, n, s, work, work ? work_bytes : 0) != 0) {
     for (int l = 0; l < n; ++l) {

@@ -363,15 +363,6 @@ __global__ __launch_bounds__(kGT, 2) void k_gemm_e8(LinearArgs a, int OB) {
   gemm_tile<KIND_E8, HAS_S>(a, OB);
 }
 
-// Up to this many tokens an E8-D4 launch runs as 16-token slices of the
-// matrix-core decode kernel: its 64-row tiles spread a layer over far more
-// workgroups than the GEMM's 128-token tiles can at these token counts (one
-// token tile: 32 workgroups for 4096 rows), and the slices re-read the weight
-// from cache.  Measured at 32 / 128 / 256 tokens on 4096x4096: slices 27 /
-// 106 / 214 us against 112 us for the GEMM; 4096x11008: 59 / 226 / 459 us
-// against 285-290 us.
-constexpr int kSliceMaxTokens = 128;
-
 template <int KIND>
 int launch_gemm(const LinearArgs& a, hipStream_t s) {
   if (KIND == KIND_E8D4 && a.B <= kSliceMaxTokens && a.prep == 0) {

@@ -98,5 +98,13 @@ inline int mfma_min_batch() {
 
 // Largest batch served by the decode matvec; larger batches take the GEMM.
 constexpr int kMatvecMaxBatch = 16;
+// Up to this many rows an E8-D4 launch runs as 16-row slices of the
+// matrix-core decode kernel: its 64-row tiles spread a layer over far more
+// workgroups than the GEMM's 128-token tiles can at these token counts (one
+// token tile: 32 workgroups for 4096 rows), and the slices re-read the weight
+// from cache.  Measured at 32 / 128 / 256 tokens on 4096x4096: slices 27 /
+// 106 / 214 us against 112 us for the GEMM; 4096x11008: 59 / 226 / 459 us
+// against 285-290 us.
+constexpr int kSliceMaxTokens = 128;
 
 }  // namespace eptq

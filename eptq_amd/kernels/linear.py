@@ -68,6 +68,11 @@ class EPTQLinear(nn.Module):
                  S_group: Optional[torch.Tensor] = None,
                  table_f32: Optional[torch.Tensor] = None):
         super().__init__()
+        # Optional decode workspace (``decode_workspace``): E8-D4 calls then go
+        # through the multi-layer entry point, whose matrix-core kernel splits
+        # the columns of layers with few row tiles; calls sharing one must not
+        # overlap in time.
+        self._work: Optional[torch.Tensor] = None
         if quantizer_type not in _KINDS:
             raise ValueError(f"unknown quantizer_type {quantizer_type!r}")
         self.in_features = int(Q.shape[1])
@@ -136,8 +141,13 @@ class EPTQLinear(nn.Module):
             x2 = x2.half()
         if not x2.is_contiguous():
             x2 = x2.contiguous()
-        y = linear_forward(self.quantizer_type, self.Q, self._codebook, self.g, self.h, x2,
-                           self.O_vals, self.O_col, self.O_row_ptr, self.bias, self.S_group)
+        if self._work is not None and self.quantizer_type == "e8_d4":
+            layer = dict(Q=self.Q, g=self.g, h=self.h, O_vals=self.O_vals, O_col=self.O_col,
+                         O_row_ptr=self.O_row_ptr, bias=self.bias, S_group=self.S_group)
+            y = linear_forward_multi([layer], self._codebook, x2, work=self._work)
+        else:
+            y = linear_forward(self.quantizer_type, self.Q, self._codebook, self.g, self.h, x2,
+                               self.O_vals, self.O_col, self.O_row_ptr, self.bias, self.S_group)
         if y.dtype != out_dtype:
             y = y.to(out_dtype)
         return y.reshape(*shape[:-1], self.out_features)
@@ -165,6 +175,7 @@ class EPTQMultiLinear(nn.Module):
 
     def __init__(self, linears):
         super().__init__()
+        self._work: Optional[torch.Tensor] = None   # as EPTQLinear._work
         ls = list(linears)
         if not ls or any(l.quantizer_type != "e8_d4" for l in ls):
             raise ValueError("EPTQMultiLinear takes one or more E8-D4 layers")
@@ -183,7 +194,7 @@ class EPTQMultiLinear(nn.Module):
         x2 = x2.contiguous()
         layers = [dict(Q=l.Q, g=l.g, h=l.h, O_vals=l.O_vals, O_col=l.O_col, O_row_ptr=l.O_row_ptr,
                        bias=l.bias, S_group=l.S_group) for l in self.parts]
-        y = linear_forward_multi(layers, self.parts[0]._codebook, x2)
+        y = linear_forward_multi(layers, self.parts[0]._codebook, x2, work=self._work)
         if y.dtype != out_dtype:
             y = y.to(out_dtype)
         return y.reshape(*shape[:-1], self.out_features)

@@ -239,9 +239,13 @@ class QuantLlama(nn.Module):
         if self.split_attention:
             nbytes = _lib.load().eptq_llama_attn_work_bytes(batch, cfg.heads)
             self.attn_work = torch.zeros(nbytes, dtype=torch.uint8, device=device)
-        # Split-K workspace of the decode Linears (batches of 5..16): the
-        # decode step's launches run one after another on one stream.
+        # Split-K workspace of the decode Linears (batches of 5..16, and the
+        # 16-token slices of short prefills through the modules): the model's
+        # launches run one after another on one stream.
         self.lin_work = decode_workspace(device)
+        for m in self.modules():
+            if isinstance(m, (EPTQLinear, EPTQMultiLinear)):
+                m._work = self.lin_work
         # Workspace of the fused final norm + lm_head + argmax (B <= 8).
         self.head_work = None
         if batch <= 8:

@@ -84,7 +84,8 @@ typedef struct {
  * Several E8-D4 layers that read the same activations x (B, N) — e.g. q, k
  * and v, or gate and up — into one output y (B, ldy), in one launch of the
  * decode matvec when it takes them all (up to 4 layers, B <= 16, fp16 table;
- * fp16 x for B > 8), otherwise one launch per layer.  Each layer keeps its own h, g, CSR, bias
+ * fp16 x for B > 8; B of 17..128 as one such launch per 16 rows, fp16 x),
+ * otherwise one launch per layer.  Each layer keeps its own h, g, CSR, bias
  * and S_group, so unlike a concatenated weight it needs no shared column
  * scales.  No counterpart in the reference, whose decoder calls one
  * EPTQLinear per projection (kernels/linear.py:154-212); its callers are
@@ -92,7 +93,8 @@ typedef struct {
  *
  * work: NULL, or a 16-byte aligned device buffer of work_bytes bytes,
  * zero-filled before its first use (eptq_e8d4_work_bytes() bytes cover every
- * launch).  With it, batches of 5..16 on layers with few 64-row tiles have
+ * launch).  With it, batches (or 16-row slices) of 5..16 rows on layers with
+ * few 64-row tiles have
  * each tile's columns split over up to 4 workgroups, whose fp32 partial sums
  * meet in the buffer; the kernel leaves its counters at zero.  Calls that
  * share a buffer must not run at the same time.

@@ -184,3 +184,33 @@ def test_mfma_decode_tail_tiles_split(shapes, B, qb):
         torch.cuda.synchronize()
         assert torch.equal(yg, y1), rep
     assert int(work[:65536].view(torch.int32).abs().sum()) == 0
+
+
+@pytest.mark.parametrize("B", [17, 40, 128])
+def test_mfma_decode_row_slices(B):
+    """17..128 rows through the multi-layer entry point: 16-row slices of the
+    matrix-core kernel, every layer in each slice's launch, with and without
+    the workspace; each layer within 1e-2 of the oracle, the two runs within
+    fp32 summation order, repeated calls bit-identical, counters at zero."""
+    from eptq_amd.kernels import decode_workspace
+    print(f"mfma decode row slices B={B}", flush=True)
+    q = E8D4Quantizer(radius=1.75)
+    shapes = [(2048, 2048), (512, 2048), (512, 2048)]
+    qds = [make_layer(o, i, seed=700 + k, percmask=0.002, bias=k == 0, qb_size=128) for k, (o, i) in enumerate(shapes)]
+    lins = [EPTQLinear.from_quantized_data(qd, q, "e8_d4").cuda() for qd in qds]
+    layers = [dict(Q=l.Q, g=l.g, h=l.h, O_vals=l.O_vals, O_col=l.O_col, O_row_ptr=l.O_row_ptr,
+                   bias=l.bias, S_group=l.S_group) for l in lins]
+    x = make_x(B, 2048, seed=B).cuda()
+    work = decode_workspace(x.device)
+    y0 = linear_forward_multi(layers, lins[0]._codebook, x)
+    y1 = linear_forward_multi(layers, lins[0]._codebook, x, work=work)
+    torch.cuda.synchronize()
+    off = 0
+    for qd, (o, _) in zip(qds, shapes):
+        want = _ref(qd, x.cpu())
+        assert rel_l2(y0[:, off:off + o].float().cpu().numpy(), want) <= TOL
+        assert rel_l2(y1[:, off:off + o].float().cpu().numpy(), want) <= TOL
+        off += o
+    assert rel_l2(y1.float().cpu().numpy(), y0.float().cpu().numpy()) < 1e-3
+    assert torch.equal(linear_forward_multi(layers, lins[0]._codebook, x, work=work), y1)
+    assert int(work[:65536].view(torch.int32).abs().sum()) == 0
