@@ -43,6 +43,9 @@ CASES = [
     ("e8_d4", 1.75, 1024, 4096, 4, 0.002, False, 128),
     ("e8_d4", 1.75, 4096, 4096, 16, 0.002, False, 128),
     ("e8_d4", 1.75, 512, 14336, 3, 0.002, False, 128),
+    # Llama-3-8B gate/up and down (benchmark configuration 2) at full size.
+    ("e8_d4", 1.75, 14336, 4096, 1, 0.002, False, 128),
+    ("e8_d4", 1.75, 4096, 14336, 16, 0.002, False, 128),
     ("e8_d4", 1.75, 1376 * 8 // 8, 768, 5, 0.01, True, None),
     ("e8_lattice", 1.6, 3072, 768, 1, 0.002, True, None),
     ("e8_lattice", 1.6, 512, 4096, 7, 0.002, False, None),
