@@ -32,9 +32,12 @@ JSON fields beyond the driver contract:
   Llama-3-8B with S_group qb=128 at batch 1, 4 and 16 (configuration 2), one
   launch each with the decode workspace: microseconds and algorithmic GB/s.
   Batches of 5..16 run the matrix-core decode kernel.
-* ``prefill`` — the MFMA GEMM on the Llama-2-13B shapes at 2048 tokens
-  (benchmark configuration 3): TFLOP/s and fraction of the 2.5 PFLOP/s fp16
-  dense MFMA peak.
+* ``prefill`` — the Llama-2-13B shapes at 2048 tokens (benchmark
+  configuration 3), both prefill forms: ``fused`` (the dequantize-into-LDS
+  MFMA GEMM of the C ABI) and ``dequant_gemm`` (what the module forward runs
+  from its token threshold on: the bit-exact dequantization kernel into an
+  fp16 scratch W, then the library fp16 GEMM); TFLOP/s and fraction of the
+  2.5 PFLOP/s fp16 dense MFMA peak.
 * ``dequant`` — the bit-exact dequantizer (``eptq_e8d4_dequant``, fp16 W of
   ``dequantize_layer``) on the Llama-2-7B shapes: algorithmic GB/s (index
   and scale reads plus the W write) and fraction of HBM peak.
@@ -469,7 +472,10 @@ def prefill_gemm(torch, dev, T=2048, reps=10):
     from eptq_amd.quantizers import E8D4Quantizer
     from eptq_amd.synthetic import make_layer, make_x
 
-    codes = E8D4Quantizer(radius=1.75).flat_table().half().to(dev)
+    from eptq_amd.kernels import dequant_linear
+
+    codes32 = E8D4Quantizer(radius=1.75).flat_table().float().to(dev)
+    codes = codes32.half()
     stream = torch.cuda.current_stream()
     out = {}
     for idx, (name, o, i) in enumerate(LLAMA2_13B):
@@ -484,12 +490,19 @@ def prefill_gemm(torch, dev, T=2048, reps=10):
         def f():
             _lib.forward_into("e8_d4", qd.Q, codes, qd.g, qd.h, x, qd.O, cols, rp, None, None,
                               y, stream.cuda_stream)
-        f()
-        d, _ = event_timed(torch, [f] * reps, stream)
-        us = statistics.median(d) * 1e3
-        tflops = 2.0 * T * o * i / (us * 1e-6) / 1e12
-        out[name] = {"shape": f"{o}x{i}", "tokens": T, "us": round(us, 1), "tflops": round(tflops, 1),
-                     "frac_mfma_f16": round(tflops / MFMA_F16_PEAK_TFLOPS, 4)}
+        layer = dict(Q=qd.Q, g=qd.g, h=qd.h, O_vals=qd.O, O_col=cols, O_row_ptr=rp)
+
+        def f2():
+            dequant_linear("e8_d4", [layer], codes32, x)
+        row = {"shape": f"{o}x{i}", "tokens": T}
+        for key, fn in (("fused", f), ("dequant_gemm", f2)):
+            fn()
+            d, _ = event_timed(torch, [fn] * reps, stream)
+            us = statistics.median(d) * 1e3
+            tflops = 2.0 * T * o * i / (us * 1e-6) / 1e12
+            row[key] = {"us": round(us, 1), "tflops": round(tflops, 1),
+                        "frac_mfma_f16": round(tflops / MFMA_F16_PEAK_TFLOPS, 4)}
+        out[name] = row
         del qd, x, y
     return out
 

@@ -27,7 +27,16 @@ from ._lib import EPTQ_BF16, EPTQ_F16, EPTQ_F32, EptqError
 
 __all__ = ["e8_forward", "e8d4_forward", "e8_forward_grouped", "e8d4_forward_grouped",
            "e8_dequant", "e8d4_dequant", "EptqError", "linear_forward", "linear_forward_multi",
-           "dequant", "decode_workspace"]
+           "dequant", "dequant_linear", "decode_workspace", "PREFILL_DEQUANT_MIN_TOKENS"]
+
+# From this many fp16 tokens on, the module forward (``EPTQLinear``,
+# ``EPTQMultiLinear``) computes a prefill as the bit-exact fp16 W of every
+# layer (``dequant``) times x on the library fp16 GEMM (``dequant_linear``):
+# W is written once and read back once, which at these token counts costs far
+# less than the contraction, and the library GEMM runs the contraction faster
+# than the fused dequantize-into-LDS kernel.  Fewer tokens run the fused
+# kernels (no weight is materialized).
+PREFILL_DEQUANT_MIN_TOKENS = 64
 
 
 def _ptr(t: Optional[torch.Tensor]):
@@ -218,11 +227,18 @@ class DecodeChain:
             pass
 
 
-def dequant(kind: str, Q, codes, g, h, O_vals, O_col, O_row_ptr, S_group=None) -> torch.Tensor:
-    """Bit-exact fp16 W (8M, N) on the GPU; ``codes`` must be the fp32 table."""
+def dequant(kind: str, Q, codes, g, h, O_vals, O_col, O_row_ptr, S_group=None,
+            out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Bit-exact fp16 W (8M, N) on the GPU; ``codes`` must be the fp32 table.
+    ``out``: a contiguous fp16 (8M, N) tensor on Q's device to write W into."""
     M, N, n_groups = _check_layer(kind, Q, codes, g, h, O_vals, O_col, O_row_ptr, S_group)
     _require(codes.dtype == torch.float32, "dequant needs the fp32 table for bit-exact W")
-    W = torch.empty((8 * M, N), dtype=torch.float16, device=Q.device)
+    if out is None:
+        W = torch.empty((8 * M, N), dtype=torch.float16, device=Q.device)
+    else:
+        _require(out.dtype == torch.float16 and tuple(out.shape) == (8 * M, N) and out.is_contiguous()
+                 and out.device == Q.device, "out must be a contiguous fp16 (8M, N) tensor on Q's device")
+        W = out
     lib = _lib.load()
     fn = lib.eptq_e8d4_dequant if kind == "e8_d4" else lib.eptq_e8_dequant
     with torch.cuda.device(Q.device):
@@ -231,6 +247,32 @@ def dequant(kind: str, Q, codes, g, h, O_vals, O_col, O_row_ptr, S_group=None) -
                 _ptr(O_row_ptr), _ptr(S_group), n_groups, M, N, _ptr(W), stream)
     _lib.check(rc, fn.__name__)
     return W
+
+
+def dequant_linear(kind: str, layers, codes_f32, x) -> torch.Tensor:
+    """y = x·Wᵀ + bias for one or more layers that read the same x (outputs
+    side by side, as ``linear_forward_multi``), with W the bit-exact fp16
+    weights of ``dequantize_layer``: each layer's W is written by ``dequant``
+    into its rows of one stacked scratch, then one fp16 GEMM on the current
+    stream (torch's, fp32 accumulation).  The reference's dense path over the
+    reconstructed W (``reconstruct.py:229`` then ``F.linear``) computes the
+    same product.  x: (T, N) fp16; ``codes_f32``: the shared fp32 table."""
+    _require(x.dtype == torch.float16 and x.dim() == 2 and x.is_contiguous(),
+             "dequant_linear takes a contiguous fp16 (T, N) activation")
+    outs = [8 * int(l["Q"].shape[0]) for l in layers]
+    N = int(x.shape[1])
+    W = torch.empty((sum(outs), N), dtype=torch.float16, device=x.device)
+    r = 0
+    for l, o in zip(layers, outs):
+        dequant(kind, l["Q"], codes_f32, l["g"], l["h"], l["O_vals"], l["O_col"], l["O_row_ptr"],
+                l.get("S_group"), out=W[r:r + o])
+        r += o
+    bias = None
+    if any(l.get("bias") is not None and l["bias"].numel() for l in layers):
+        bias = torch.cat([l["bias"].to(torch.float16) if l.get("bias") is not None and l["bias"].numel()
+                          else torch.zeros(o, dtype=torch.float16, device=x.device)
+                          for l, o in zip(layers, outs)])
+    return torch.nn.functional.linear(x, W, bias)
 
 
 # ---------------------------------------------------------------------------
