@@ -402,31 +402,6 @@ int eptq_llama_norm_swiglu(const eptq_layer* gate_up, const void* codes, const v
                       8 * gate_up[0].M, stream, true);
 }
 
-long long eptq_llama_attn_o_work_bytes(void) { return 33 * 128; }   // counts, then 32 flag lines
-
-int eptq_llama_attn_o(const void* qkv, const void* pos, const void* cos_tab, const void* sin_tab, void* k_cache,
-                      void* v_cache, void* att, int H, int Hk, int D, int L, const eptq_layer* o, const void* codes,
-                      void* y, void* work, void* stream) {
-  const char* fn = "eptq_llama_attn_o";
-  if (!qkv || !pos || !cos_tab || !sin_tab || !k_cache || !v_cache || !att || !o || !y || !work)
-    return fail(EPTQ_EINVAL, "%s: null pointer", fn);
-  if (H <= 0 || Hk <= 0 || H % Hk || D != 128 || L <= 0 || L > 1024)
-    return fail(EPTQ_EINVAL, "%s: H=%d Hk=%d D=%d L=%d (D 128, H a multiple of Hk, L <= 1024)", fn, H, Hk, D, L);
-  if (((uintptr_t)work & 127) || !aligned16(att))
-    return fail(EPTQ_EINVAL, "%s: work must be 128-byte and att 16-byte aligned", fn);
-  const int N = H * D;
-  eptq::LinearArgs a;
-  int rc = layer_args(fn, eptq::KIND_E8D4, o->Q, codes, EPTQ_F16, o->g, o->h, att, EPTQ_F16, o->O_vals, o->O_col,
-                      o->O_row_ptr, o->bias, o->S_group, o->n_groups, o->M, N, 1, &a);
-  if (rc) return rc;
-  a.y = (uint16_t*)y;
-  a.ldy = 8 * o->M;
-  int* sync = (int*)work;
-  if (eptq::launch_attn_o(a, qkv, pos, cos_tab, sin_tab, k_cache, v_cache, att, H, Hk, L, sync, (hipStream_t)stream))
-    return fail(EPTQ_EUNSUPPORTED, "%s: the fused launch does not take N=%d M=%d here", fn, N, o->M);
-  return check_launch(fn);
-}
-
 int eptq_e8d4_dequant(const void* Q, const void* codes_f32, const void* g, const void* h,
                       const void* O_vals, const void* O_col, const void* O_row_ptr,
                       const void* S_group, int n_groups, int M, int N, void* W, void* stream) {

@@ -83,11 +83,6 @@ int launch_decode_e8d4_multi(const LinearArgs* layers, int n, hipStream_t s, voi
 // shape in one launch, y = silu(gate) ⊙ up written at layers[0].y with
 // layers[0].ldy; -1 when the pair is outside the kernel's range.
 int launch_decode_e8d4_pair(const LinearArgs* layers, hipStream_t s);
-// Rotary + cache + attention (batch 1, H heads of 128) and the o projection
-// `a` (x = att) in one launch (llama_ops.hip); sync: 3 zeroed ints.  0 if
-// launched, -1 outside the kernel's range.
-int launch_attn_o(const LinearArgs& a, const void* qkv, const void* pos, const void* cosv, const void* sinv,
-                  void* kc, void* vc, void* att, int H, int Hk, int L, int* sync, hipStream_t s);
 
 // Matrix-core E8-D4 decode (B <= 16, fp16 x and table, no fused preparation);
 // -1 when the layers are outside its range.

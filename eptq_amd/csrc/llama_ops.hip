@@ -182,9 +182,7 @@ __device__ __forceinline__ void load_rows(__amdgpu_buffer_rsrc_t rk, __amdgpu_bu
     vv[u] = __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(rv, ((c + pg + 16 * u) * 128 + dc * 8) * 2, 0, 0));
 }
 
-// Head h of batch row b, split sp of ns.  COH_OUT: the unsplit output row is
-// stored device-coherently, for other workgroups of the same launch.
-template <bool COH_OUT>
+// Head h of batch row b, split sp of ns.
 __device__ __forceinline__ void rope_attn(const f16* __restrict__ qkv, const int64_t* __restrict__ posp,
                                           const float* __restrict__ cosv, const float* __restrict__ sinv,
                                           f16* __restrict__ kc, f16* __restrict__ vc, f16* __restrict__ out,
@@ -326,11 +324,7 @@ __device__ __forceinline__ void rope_attn(const f16* __restrict__ qkv, const int
   if (ns == 1) {
     if (t < D) {
       const f16 r = ok ? (f16)(o / l) : (f16)0.0f;
-      if constexpr (COH_OUT)
-        __hip_atomic_store((uint16_t*)(orow + t), __builtin_bit_cast(uint16_t, r), __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
-      else
-        orow[t] = r;
+      orow[t] = r;
     }
     return;
   }
@@ -371,154 +365,11 @@ __global__ __launch_bounds__(kT) void k_rope_attn(const f16* __restrict__ qkv, c
                                                  f16* __restrict__ kc, f16* __restrict__ vc, f16* __restrict__ out,
                                                  int H, int Hk, int L, float scale, float* __restrict__ part,
                                                  int* __restrict__ cnt) {
-  rope_attn<false>(qkv, posp, cosv, sinv, kc, vc, out, H, Hk, L, scale, part, cnt, blockIdx.x, blockIdx.y,
+  rope_attn(qkv, posp, cosv, sinv, kc, vc, out, H, Hk, L, scale, part, cnt, blockIdx.x, blockIdx.y,
                    blockIdx.z, gridDim.z);
 }
 
-// Attention and the o projection of a decode step (batch 1) in one launch.
-// Workgroups 0..H-1 first run head h = blockIdx.x of k_rope_attn (unsplit)
-// and publish its output row with device-coherent stores, wait for them
-// (vmcnt) and count themselves in sync[0]; the last of them raises the flag
-// of every group of workgroups (32 flags, one 128-byte line each, so that the
-// polls spread over the memory channels).  Every workgroup requests its
-// table and the o layer's index ring (which do not depend on the attention),
-// waits for its group's flag (thread 0, a bounded spin), then reads the
-// attention output as the layer's x and runs its rows.  Plain loads see the
-// published rows: no workgroup of this launch reads those lines before the
-// flag is up, and lines cached by earlier launches were invalidated at this
-// launch's start.  The heads are the first H workgroup ids, dispatched before
-// any waiting workgroup, so the wait always ends; a spin past its limit sets
-// sync[2] and goes on (the output is then wrong).  The last workgroup past
-// the wait (count in sync[1]) zeroes the counts and flags for the next call.
-struct AttnArgs {
-  const f16* qkv;
-  const int64_t* pos;
-  const float* cosv;
-  const float* sinv;
-  f16* kc;
-  f16* vc;
-  f16* att;
-  int H, Hk, L;
-  float scale;
-};
-
-constexpr int kAttnSpinLimit = 1 << 22;
-constexpr int kAttnFlags = 32, kLineInts = 32;   // flag g at ints kLineInts * (1 + g)
-
-template <int J, int P, int S>
-__global__ __launch_bounds__(kT) void k_attn_o(MultiArgs ma, AttnArgs aa, int* __restrict__ sync) {
-  __shared__ f16x4 tab[512];
-  __shared__ float red[2][dec::kW][8];
-  __shared__ float wmax[dec::kW];
-  extern __shared__ __align__(16) char dyn[];
-  const int tid = threadIdx.x;
-  const int wg = blockIdx.x, G = gridDim.x;
-  if (wg < aa.H) {
-    rope_attn<true>(aa.qkv, aa.pos, aa.cosv, aa.sinv, aa.kc, aa.vc, aa.att, aa.H, aa.Hk, aa.L, aa.scale, nullptr,
-                    nullptr, wg, 0, 0, 1);
-    __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): the output stores are complete
-    __syncthreads();
-    if (tid == 0 && __hip_atomic_fetch_add(sync, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == aa.H - 1) {
-      for (int g = 0; g < kAttnFlags; ++g)
-        __hip_atomic_store(sync + kLineInts * (1 + g), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-  }
-  const LinearArgs a = ma.l[0];
-  using Lay = dec::Layer<1, J, P, S, false, f16, false>;
-  const Lay layer(a, wg, G);
-  const dec::Smem<1> sm{tab, red, wmax, (uint16_t*)dyn, (float*)(dyn + (a.N + 8) * 2)};
-  typename Lay::State st;
-  layer.rows_first(st);
-  f16x4 tload[2];
-#pragma unroll
-  for (int p = 0; p < 2; ++p) tload[p] = ((const f16x4*)a.codes)[tid + kT * p];   // fp16 table
-  layer.issue_ring(st);
-  if (tid == 0) {
-    const int* flag = sync + kLineInts * (1 + wg % kAttnFlags);
-    for (int it = 0;; ++it) {
-      if (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) break;
-      if (it >= kAttnSpinLimit) {
-        __hip_atomic_store(sync + 2, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        break;
-      }
-      __builtin_amdgcn_s_sleep(1);
-    }
-    if (__hip_atomic_fetch_add(sync + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == G - 1) {
-      __hip_atomic_store(sync, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(sync + 1, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      for (int g = 0; g < kAttnFlags; ++g)
-        __hip_atomic_store(sync + kLineInts * (1 + g), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-  }
-  __syncthreads();
-  const float out_scale = layer.build_act(sm);
-  __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-  for (int p = 0; p < 2; ++p) tab[(tid + kT * p) ^ 0x100] = tload[p];
-  __syncthreads();
-  layer.rows(st, sm, out_scale);
-}
-
-template <int J, int S>
-int launch_attn_o_k(const LinearArgs& a, const AttnArgs& aa, int* sync, hipStream_t s) {
-  constexpr int P = 8 / (J > 4 ? 4 : J);
-  constexpr int R = dec::kW / S;
-  auto kern = k_attn_o<J, P, S>;
-  static int reg_cu = 0;
-  static size_t static_lds = 0;
-  if (reg_cu == 0) {
-    hipFuncAttributes fa;
-    int v = 256;
-    if (hipFuncGetAttributes(&fa, (const void*)kern) == hipSuccess) {
-      if (fa.numRegs > 0) v = fa.numRegs;
-      static_lds = fa.sharedSizeBytes;
-    }
-    const int waves = 512 / ((v + 7) / 8 * 8);
-    reg_cu = waves < 1 ? 1 : (waves > 8 ? 8 : waves);
-  }
-  const size_t dyn = dec::act_lds_bytes(a.N, 1);
-  int per_cu = (int)(dec::kLdsPerCu / (static_lds + dyn + 256));
-  if (per_cu > reg_cu) per_cu = reg_cu;
-  if (per_cu < 1) per_cu = 1;
-  const int RG = (a.M + R - 1) / R;
-  int G = dec::cu_count() * per_cu < RG ? dec::cu_count() * per_cu : RG;
-  if (G < aa.H) G = aa.H;   // one workgroup per head (workgroups past the rows only wait)
-  MultiArgs ma;
-  ma.n = 1;
-  ma.start[0] = 0;
-  for (int l = 0; l < kMaxLayers; ++l) {
-    ma.l[l] = a;
-    ma.start[l + 1] = G;
-  }
-  kern<<<G, kT, dyn, s>>>(ma, aa, sync);
-  return 0;
-}
-
 }  // namespace
-
-// Attention + o projection (batch 1): 0 launched, -1 outside the kernel's range.
-int launch_attn_o(const LinearArgs& a, const void* qkv, const void* pos, const void* cosv, const void* sinv,
-                  void* kc, void* vc, void* att, int H, int Hk, int L, int* sync, hipStream_t s) {
-  if (a.B != 1 || a.x_bf16 || a.codes_f32 || a.S || a.prep != 0 || a.N != H * 128) return -1;
-  AttnArgs aa{(const f16*)qkv, (const int64_t*)pos, (const float*)cosv, (const float*)sinv, (f16*)kc, (f16*)vc,
-              (f16*)att, H, Hk, L, 1.0f / sqrtf(128.0f)};
-  const int N = a.N, nch = N >> 3;
-  // The vector decode kernel's row split for one layer (about 8 waves per CU).
-  int S = 4;
-  for (int cand = 1; cand <= 4; cand *= 2) {
-    if (!dec::fits(dec::chunks_for(nch, cand), N, 1)) continue;
-    S = cand;
-    if ((long)a.M * cand >= dec::cu_count() * 8) break;
-  }
-  const int J = dec::chunks_for(nch, S);
-  if (!dec::fits(J, N, 1)) return -1;
-#define EPTQ_AO(J_, S_) \
-  if (J == J_ && S == S_) return launch_attn_o_k<J_, S_>(a, aa, sync, s);
-  EPTQ_AO(2, 1) EPTQ_AO(2, 2) EPTQ_AO(2, 4) EPTQ_AO(4, 1) EPTQ_AO(4, 2) EPTQ_AO(4, 4)
-  EPTQ_AO(8, 1) EPTQ_AO(8, 2) EPTQ_AO(8, 4)
-#undef EPTQ_AO
-  return -1;
-}
 
 namespace {
 

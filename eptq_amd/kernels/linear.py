@@ -25,7 +25,9 @@ Differences, all towards the reference's own reconstruct semantics:
 
 from __future__ import annotations
 
-from typing import Dict, Optional, Tuple
+import hashlib
+import weakref
+from typing import Optional, Tuple
 
 import torch
 import torch.nn as nn
@@ -35,31 +37,57 @@ from . import PREFILL_DEQUANT_MIN_TOKENS, dequant_linear, linear_forward, linear
 
 _KINDS = ("e8_lattice", "e8_d4")
 
-# Tables shared across layers: (id(source), radius, device, dtype) -> tensor.
-_TABLE_CACHE: Dict[Tuple, torch.Tensor] = {}
+# Layers whose tables carry the same bits share one fp32 and one fp16 tensor:
+# (device, kind, sha256 of the fp32 bits) -> (fp32 table, fp16 table).  The
+# entries are private snapshots (never views of a quantizer's codes), so no
+# later radius change of the quantizer can alter a table already handed out;
+# they are dropped once no layer holds them.
+_SHARED: "weakref.WeakValueDictionary[Tuple, torch.Tensor]" = weakref.WeakValueDictionary()
+_SHARED16: "weakref.WeakValueDictionary[Tuple, torch.Tensor]" = weakref.WeakValueDictionary()
 
 
-def _table_for(codebook, quantizer_type: str, chosen_r: Optional[float]) -> torch.Tensor:
-    """fp32 kernel-layout table for one layer (shared when identical)."""
+def _share(tab: torch.Tensor, quantizer_type: str) -> Tuple[torch.Tensor, torch.Tensor]:
+    tab = tab.detach().float().contiguous()
+    digest = hashlib.sha256(tab.cpu().numpy().tobytes()).hexdigest()
+    key = (str(tab.device), quantizer_type, tuple(tab.shape), digest)
+    t32 = _SHARED.get(key)
+    if t32 is None:
+        t32 = tab.clone()
+        _SHARED[key] = t32
+    t16 = _SHARED16.get(key)
+    if t16 is None:
+        t16 = t32.to(torch.float16)
+        _SHARED16[key] = t16
+    return t32, t16
+
+
+def _table_for(codebook, quantizer_type: str, chosen_r: Optional[float]) -> Tuple[torch.Tensor, torch.Tensor]:
+    """(fp32, fp16) kernel-layout tables of one layer.
+
+    With a quantizer, the layer's table is what ``dequantize_layer`` decodes
+    with (``algorithms/eptq.py:430-457``): the quantizer is switched to the
+    layer's ``chosen_r`` when that differs from its radius, the table is read,
+    and the radius is switched back — on the quantizer object itself, so a
+    legacy table (no raw codes: ``set_radius`` rescales in place) drifts from
+    layer to layer exactly as it does when the reference reconstructs the
+    layers in the same order, and a warped table loses its warp at the first
+    such switch as the reference's does (``quantizers/e8_d4.py:90-102``).
+    The table handed to the layer is a copy taken at that point."""
     if isinstance(codebook, torch.Tensor):
         t = codebook.float()
-        return t.reshape(512, 4).contiguous() if quantizer_type == "e8_d4" else t.reshape(-1, 8).contiguous()
+        t = t.reshape(512, 4) if quantizer_type == "e8_d4" else t.reshape(-1, 8)
+        return _share(t, quantizer_type)
     q = codebook
-    r = getattr(q, "_radius", None)
-    key = (id(q), r if chosen_r is None else float(chosen_r), quantizer_type)
-    hit = _TABLE_CACHE.get(key)
-    if hit is not None:
-        return hit
-    if chosen_r is not None and r is not None and chosen_r != r:
+    saved_r = q._radius
+    swap = chosen_r is not None and chosen_r != saved_r
+    if swap:
         q.set_radius(chosen_r)
-        try:
-            tab = q.flat_table().clone()
-        finally:
-            q.set_radius(r)
-    else:
-        tab = q.flat_table()
-    _TABLE_CACHE[key] = tab
-    return tab
+    try:
+        tab = q.flat_table().clone()
+    finally:
+        if swap:
+            q.set_radius(saved_r)
+    return _share(tab, quantizer_type)
 
 
 class EPTQLinear(nn.Module):
@@ -113,16 +141,15 @@ class EPTQLinear(nn.Module):
         if Q.dtype != torch.int16:
             raise ValueError(f"Q must be int16, got {Q.dtype}")
         M = Q.shape[0]
-        tab32 = _table_for(codebook, quantizer_type, quant_data.chosen_r)
-        cb16 = tab32.to(torch.float16)
+        tab32, cb16 = _table_for(codebook, quantizer_type, quant_data.chosen_r)
 
         # Critical blocks — nonzero() on row-major Q is in row-major order.
         mask = Q == 32767
         O_row, O_col = mask.nonzero(as_tuple=True)
         n_masked = int(O_row.shape[0])
         if int(quant_data.O.shape[0]) != n_masked:
-            raise ValueError(f"O shape mismatch: got {quant_data.O.shape[0]} values "
-                             f"but found {n_masked} masked positions in Q")
+            raise ValueError(f"layer data is inconsistent: Q marks {n_masked} critical blocks "
+                             f"(entries equal to 32767) but O holds {quant_data.O.shape[0]} rows")
         counts = torch.bincount(O_row.long(), minlength=M)
         O_row_ptr = torch.cat([torch.zeros(1, dtype=torch.int32, device=O_row.device),
                                counts.cumsum(0).to(torch.int32)])

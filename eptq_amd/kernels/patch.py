@@ -40,10 +40,10 @@ def load_quantized_model(quantized_dir: str, device: str = "cuda") -> Tuple[nn.M
     quant_config = load_quantization_config(quantized_dir)
     quantizer_type = quant_config.get("quantizer_type", "e8_lattice")
 
-    print("Loading codebook...", file=sys.stderr)
+    print(f"eptq_amd: reading the codebook of {quantized_dir}", file=sys.stderr)
     quantizer = load_quantizer(quantized_dir, device=device)
 
-    print("Creating model structure...", file=sys.stderr)
+    print("eptq_amd: building the model skeleton", file=sys.stderr)
     config = AutoConfig.from_pretrained(quantized_dir)
     model_dtype = getattr(config, "torch_dtype", None) or torch.float16
     with init_empty_weights():
@@ -58,15 +58,15 @@ def load_quantized_model(quantized_dir: str, device: str = "cuda") -> Tuple[nn.M
     except Exception:
         model_name = quant_config.get("model_name")
         if not model_name:
-            raise ValueError("Tokenizer not found in quantized_dir/tokenizer and "
-                             "'model_name' missing from quant_config.json.")
-        print(f"Tokenizer not found in {tokenizer_dir}, loading from {model_name}", file=sys.stderr)
+            raise ValueError(f"no tokenizer under {tokenizer_dir}, and quant_config.json names "
+                             "no model_name to fetch one by")
+        print(f"eptq_amd: no tokenizer under {tokenizer_dir}; using the one of {model_name}", file=sys.stderr)
         tokenizer = AutoTokenizer.from_pretrained(model_name)
 
     handler = get_model_handler_by_type(ModelHandler.detect_model_type(model))
     global_params = load_global_non_quantized_params(quantized_dir)
     layers = handler.get_layers(model)
-    print(f"Loading {len(layers)} quantized layers...", file=sys.stderr)
+    print(f"eptq_amd: swapping in {len(layers)} quantized decoder layers", file=sys.stderr)
     for lid, layer in enumerate(layers):
         layer_dir = quantized_dir / f"layer_{lid}"
         for name in list(handler.get_linear_layers(layer).keys()):
@@ -86,5 +86,5 @@ def load_quantized_model(quantized_dir: str, device: str = "cuda") -> Tuple[nn.M
         print(f"WARNING: {len(meta)} meta parameters not loaded: {meta[:5]}", file=sys.stderr)
     model = model.to(device=device)
     model.eval()
-    print("Quantized model loaded.", file=sys.stderr)
+    print("eptq_amd: model ready", file=sys.stderr)
     return model, tokenizer

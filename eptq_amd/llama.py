@@ -92,8 +92,18 @@ def _parts(mod):
     return list(mod.parts) if isinstance(mod, EPTQMultiLinear) else [mod]
 
 
+def _array_key(lins):
+    """Every pointer, dtype and size the layer array carries: a buffer that is
+    reassigned, moved or converted changes the key."""
+    key = []
+    for l in lins:
+        for t in (l.Q, l.g, l.h, l.O_vals, l.O_col, l.O_row_ptr, l.bias, l.S_group, l._codebook):
+            key.append(None if t is None else (t.data_ptr(), t.dtype, tuple(t.shape), str(t.device)))
+    return tuple(key)
+
+
 def _cached_array(mod):
-    key = tuple(l.Q.data_ptr() for l in _parts(mod))
+    key = _array_key(_parts(mod))
     cached = getattr(mod, "_eptq_array", None)
     if cached is None or cached[0] != key:
         cached = (key, *_layer_array(_parts(mod)))
@@ -220,12 +230,6 @@ class QuantLlama(nn.Module):
         # Decode step: the residual add + RMSNorm inside the q|k|v and gate|up
         # launches (6 launches per layer) or as launches of their own (8).
         self.fused_ops = True
-        # Batch 1: attention and the o projection in one launch
-        # (eptq_llama_attn_o) instead of two.  Off by default: the o rows
-        # cannot start before every head is done and the fused kernel runs at
-        # half the o launch's occupancy, so the step measured slower (698
-        # against 780 tok/s on the synthetic Llama-2-7B).
-        self.fuse_attn_o = False
 
     def alloc_cache(self, batch: int, max_len: int, device):
         cfg = self.cfg
@@ -252,11 +256,6 @@ class QuantLlama(nn.Module):
         for m in self.modules():
             if isinstance(m, (EPTQLinear, EPTQMultiLinear)):
                 m._work = self.lin_work
-        # Counters of the fused attention + o launch (batch 1, unsplit attention).
-        self.attn_o_work = None
-        if batch == 1 and not self.split_attention:
-            nbytes = _lib.load().eptq_llama_attn_o_work_bytes()
-            self.attn_o_work = torch.zeros(nbytes, dtype=torch.uint8, device=device)
         # Workspace of the fused final norm + lm_head + argmax (B <= 8).
         self.head_work = None
         if batch <= 8:
@@ -289,31 +288,6 @@ class QuantLlama(nn.Module):
             N, B, y.data_ptr(), width, None if work is None else work.data_ptr(),
             0 if work is None else work.numel(), _stream(x))
         _lib.check(rc, "eptq_e8d4_forward_multi")
-        return y
-
-    def _attn_o(self, mod, qkv, pos, i):
-        """Attention of layer i and its o projection in one launch (batch 1),
-        or None where that launch does not apply (then the caller runs them
-        apart)."""
-        work = getattr(self, "attn_o_work", None)
-        if work is None or not self.fuse_attn_o:
-            return None
-        arr, width = _cached_array(mod)
-        if len(arr) != 1:
-            return None
-        cfg = self.cfg
-        H, Hk, D = cfg.heads, cfg.kv_heads, cfg.head_dim
-        att = torch.empty((1, H * D), dtype=qkv.dtype, device=qkv.device)
-        y = torch.empty((1, width), dtype=qkv.dtype, device=qkv.device)
-        lib = _lib.load()
-        rc = lib.eptq_llama_attn_o(qkv.data_ptr(), pos.data_ptr(), self.cos_tab.data_ptr(), self.sin_tab.data_ptr(),
-                                   self.kc[i].data_ptr(), self.vc[i].data_ptr(), att.data_ptr(), H, Hk, D,
-                                   self.max_len, arr, _parts(mod)[0]._codebook.data_ptr(), y.data_ptr(),
-                                   work.data_ptr(), _stream(qkv))
-        if rc == _lib.EPTQ_EUNSUPPORTED:
-            self.attn_o_work = None
-            return None
-        _lib.check(rc, "eptq_llama_attn_o")
         return y
 
     def _norm_into(self, mod, x, delta, w):
@@ -366,11 +340,6 @@ class QuantLlama(nn.Module):
         for i, layer in enumerate(self.layers):
             ln1, ln2 = layer.input_layernorm.weight, layer.post_attention_layernorm.weight
             qkv, x = self._norm_into(layer.qkv_proj, x, delta, ln1)
-            o = self._attn_o(layer.o_proj, qkv, pos, i) if self.fused_ops and B == 1 else None
-            if o is not None:
-                act, x = self._norm_swiglu(layer.gate_up_proj, x, o, ln2)
-                delta = self._lin(layer.down_proj, act)
-                continue
             att = torch.empty((B, H * D), dtype=x.dtype, device=x.device)
             rc = lib.eptq_llama_rope_attn(qkv.data_ptr(), pos.data_ptr(), self.cos_tab.data_ptr(),
                                           self.sin_tab.data_ptr(), self.kc[i].data_ptr(), self.vc[i].data_ptr(),

@@ -9,7 +9,7 @@ optional ``bias ~ N(0, 0.01)`` and ``S_group ~ lognormal(0, 0.2)``,
 
 from __future__ import annotations
 
-from typing import Optional
+from typing import Optional, Sequence
 
 import torch
 
@@ -59,14 +59,17 @@ def make_x(batch: int, in_features: int, *, seed: int, device="cpu") -> torch.Te
 
 def write_quantized_model(out_dir, hf_config, quantizer_type: str = "e8_d4", radius: float = 1.75,
                           percmask: float = 0.01, seed: int = 0, tokenizer=None,
-                          qb_size: Optional[int] = None) -> None:
+                          qb_size: Optional[int] = None, warp_alpha: float = 1.0,
+                          chosen_r: Optional[Sequence[Optional[float]]] = None) -> None:
     """Write a synthetic quantized-model directory in the reference layout
     (``README.md:127-152``; writers ``quantize.py:36-105,425-433``).
 
     ``hf_config`` is a ``transformers`` config (Llama or OPT architecture);
     every decoder ``nn.Linear`` becomes a seeded ``QuantizedLayerData``, the
     remaining parameters are random.  ``tokenizer``, if given, is saved under
-    ``tokenizer/``.
+    ``tokenizer/``.  ``warp_alpha`` is stored in ``quantizer.pt`` (the loader
+    warps the table, ``reconstruct.py:63-65``); ``chosen_r``, if given, is
+    cycled over the quantized Linears in load order as their ``chosen_r``.
     """
     import json
     from pathlib import Path
@@ -84,6 +87,8 @@ def write_quantized_model(out_dir, hf_config, quantizer_type: str = "e8_d4", rad
         json.dump({"quantizer_type": quantizer_type, "codebook_radius": radius,
                    "model_name": None}, f, indent=2)
     q = E8D4Quantizer(radius=radius) if quantizer_type == "e8_d4" else E8LatticeQuantizer(radius=radius)
+    if warp_alpha != 1.0:
+        q._warp_alpha = warp_alpha      # recorded only: the file keeps the raw codes
     save_quantizer(q, out, quantizer_type)
     hf_config.save_pretrained(out)
     if tokenizer is not None:
@@ -94,12 +99,15 @@ def write_quantized_model(out_dir, hf_config, quantizer_type: str = "e8_d4", rad
     handler = get_model_handler_by_type(ModelHandler.detect_model_type(model))
     gen = torch.Generator().manual_seed(seed)
     quantized = set()
+    n_lin = 0
     for lid, layer in enumerate(handler.get_layers(model)):
         layer_dir = out / f"layer_{lid}"
         layer_dir.mkdir(exist_ok=True)
         for k, (name, lin) in enumerate(handler.get_linear_layers(layer).items()):
+            cr = chosen_r[n_lin % len(chosen_r)] if chosen_r else None
+            n_lin += 1
             qd = make_layer(lin.out_features, lin.in_features, seed=seed + 1000 * lid + k,
-                            percmask=percmask, bias=lin.bias is not None, qb_size=qb_size)
+                            percmask=percmask, bias=lin.bias is not None, qb_size=qb_size, chosen_r=cr)
             qd.save(layer_dir / f"{name}.pt")
             quantized.update({f"{name}.weight", f"{name}.bias"})
         other = {n: (torch.randn(p.shape, generator=gen) * 0.02 + (1.0 if "norm" in n else 0.0)).half()

@@ -71,27 +71,6 @@ int eptq_llama_norm_linear(int n_layers, const eptq_layer* layers, const void* c
 int eptq_llama_norm_swiglu(const eptq_layer* gate_up, const void* codes, const void* resid, const void* delta,
                            const void* w, float eps, void* resid_out, int N, int B, void* out, void* stream);
 
-/* Bytes of the eptq_llama_attn_o workspace (zero-filled before its first
- * use; every call leaves it zeroed but for int 2, its time-out flag). */
-long long eptq_llama_attn_o_work_bytes(void);
-
-/* Attention and the o projection of a decode step in one launch (batch 1):
- * eptq_llama_rope_attn for every head (qkv, pos, cos/sin, caches as there;
- * att (1, H·D) receives the attention output), then y (1, 8·o->M) = the
- * E8-D4 layer o applied to att (codes: fp16 table; o->y_offset ignored).  The
- * first H workgroups compute one head each while every workgroup already
- * streams o's indices; the layer reads att once all heads are published.
- * D = 128, L <= 1024, N = H·D.  work: eptq_llama_attn_o_work_bytes() bytes,
- * 128-byte aligned; calls sharing it must not overlap in time.  If int 2 of
- * work is nonzero after a call, a wait timed out and y is not valid.
- * EPTQ_EUNSUPPORTED when the fused launch does not take the shape (then run
- * eptq_llama_rope_attn and the Linear apart).  No counterpart in the
- * reference, whose decode step runs attention and o_proj as separate ops
- * (bench_decode.py:44-71). */
-int eptq_llama_attn_o(const void* qkv, const void* pos, const void* cos_tab, const void* sin_tab, void* k_cache,
-                      void* v_cache, void* att, int H, int Hk, int D, int L, const eptq_layer* o, const void* codes,
-                      void* y, void* work, void* stream);
-
 /* Bytes of the eptq_llama_lm_head_argmax workspace for B batch rows
  * (zero-filled before its first use; every call leaves it zeroed). */
 long long eptq_llama_lm_head_work_bytes(int B);

@@ -62,6 +62,72 @@ def test_load_quantized_model_logits_match_dense_reconstruction(tiny_dir):
     assert rel_l2(got, want) <= 2e-2
 
 
+@pytest.fixture(scope="module")
+def warped_dir(tmp_path_factory):
+    from transformers import LlamaConfig
+    from eptq_amd.synthetic import write_quantized_model
+    from test_host import _tiny_tokenizer
+    d = tmp_path_factory.mktemp("qmodel_warp")
+    cfg = LlamaConfig(vocab_size=128, hidden_size=128, intermediate_size=256, num_hidden_layers=2,
+                      num_attention_heads=4, num_key_value_heads=2, max_position_embeddings=64)
+    write_quantized_model(d, cfg, percmask=0.02, seed=8, tokenizer=_tiny_tokenizer(), warp_alpha=1.3,
+                          chosen_r=[None, 1.9, None, 1.6, 1.75])
+    return d
+
+
+def test_load_quantized_model_warped_chosen_r(warped_dir):
+    """A warped table (warp_alpha 1.3) and layers with their own chosen_r,
+    loaded through load_quantized_model on the GPU: each layer's table follows
+    the reference's load order (the warp holds until the first radius switch,
+    which drops it — pinned on the CPU by tests/test_loader_golden.py), the
+    GPU dequantization is bit-exact with the oracle on the layer's table, and
+    the logits match a dense fp32 model over the oracle's W."""
+    from transformers import AutoConfig, AutoModelForCausalLM
+    from eptq_amd.kernels.linear import _table_for
+    from eptq_amd.kernels.patch import load_quantized_model
+    from eptq_amd.reconstruct import load_quantized_layer, load_quantizer
+    from eptq_amd.handlers import ModelHandler, get_model_handler_by_type
+    print("warped chosen_r checkpoint: tables, dequant, logits", flush=True)
+    model, _ = load_quantized_model(str(warped_dir), device="cuda")
+    # The same load order replayed on the CPU with the loader pinned by the
+    # golden tests; the GPU's tables come from torch on the GPU (division and
+    # the warp's norm/pow), so they agree to fp32 rounding.
+    qcpu = load_quantizer(warped_dir, device="cpu")
+    handler = get_model_handler_by_type(ModelHandler.detect_model_type(model))
+    n_warped = n_plain = 0
+    for lid, layer in enumerate(handler.get_layers(model)):
+        for name, lin in handler.get_linear_layers(layer).items():
+            qd = load_quantized_layer(warped_dir / f"layer_{lid}", name)
+            want, _ = _table_for(qcpu, "e8_d4", qd.chosen_r)
+            got = lin._table_f32.cpu()
+            assert torch.allclose(got, want, rtol=2e-7, atol=0), (lid, name)
+            plain = torch.equal(want, (qcpu._raw_codes / (qd.chosen_r or 1.75)).reshape(512, 4))
+            n_plain += plain
+            n_warped += not plain
+            W = lin.dequantize().cpu().numpy()
+            ref = dequantize_layer(lin.Q.cpu().numpy(), lin.g.cpu().numpy(), lin.h.cpu().numpy(),
+                                   lin.O_vals.cpu().numpy(), got.numpy(), "e8_d4")
+            assert np.array_equal(W.view(np.uint16), ref.view(np.uint16)), (lid, name)
+    assert n_warped >= 1 and n_plain >= 1, (n_warped, n_plain)
+    ids = torch.tensor([[3, 1, 4, 1, 5, 9, 2, 6]], device="cuda")
+    with torch.no_grad():
+        got = model(ids).logits.float().cpu().numpy()
+    cfg = AutoConfig.from_pretrained(warped_dir)
+    ref = AutoModelForCausalLM.from_config(cfg).float().eval()
+    sd = {}
+    for name, mod in model.named_modules():
+        if isinstance(mod, EPTQLinear):
+            W = dequantize_layer(mod.Q.cpu().numpy(), mod.g.cpu().numpy(), mod.h.cpu().numpy(),
+                                 mod.O_vals.cpu().numpy(), mod._table_f32.cpu().numpy(), "e8_d4")
+            sd[name + ".weight"] = torch.from_numpy(W.astype(np.float32))
+    for name, p in model.named_parameters():
+        sd[name] = p.detach().float().cpu()
+    ref.load_state_dict(sd, strict=False)
+    with torch.no_grad():
+        want = ref(ids.cpu()).logits.numpy()
+    assert rel_l2(got, want) <= 2e-2
+
+
 def test_llama_graph_decode_matches_eager():
     from eptq_amd.llama import GraphDecoder, LlamaConfig, build_synthetic
     print("synthetic llama: graph vs eager decode", flush=True)
