@@ -11,8 +11,8 @@
 
 #include "eptq_hip.h"
 #include "eptq_llama.h"
-#include "chain.h"
 #include "kernels.h"
+#include "step.h"
 
 namespace {
 
@@ -312,81 +312,141 @@ int eptq_e8d4_forward_multi(int n_layers, const eptq_layer* layers, const void* 
 
 long long eptq_e8d4_work_bytes(void) { return eptq::decode_mfma_work_bytes(); }
 
-int eptq_e8d4_chain_create(int n_stages, const eptq_stage* stages, const void* codes,
-                           int codes_dtype, eptq_chain** chain) {
-  const char* fn = "eptq_e8d4_chain_create";
-  if (!chain) return fail(EPTQ_EINVAL, "%s: null chain", fn);
-  *chain = nullptr;
-  if (n_stages <= 0 || !stages) return fail(EPTQ_EINVAL, "%s: n_stages=%d", fn, n_stages);
-  if (codes_dtype != EPTQ_F16) return fail(EPTQ_EUNSUPPORTED, "%s: the chain takes the fp16 table", fn);
-  eptq::ChainStage* cs = new eptq::ChainStage[n_stages];
-  bool has_s = false;
+long long eptq_step_plan_bytes(int n_stages) {
+  return n_stages > 0 ? (long long)n_stages * (long long)sizeof(eptq::step::Stage) : 0;
+}
+
+static long long step_out_bytes(int M_tot) { return ((32LL * M_tot) + 255) & ~255LL; }
+
+long long eptq_step_work_bytes(int n_stages, const eptq_step_stage* stages) {
+  if (n_stages <= 0 || !stages) return 0;
+  long long b = eptq::step::kSyncBytes;
   for (int s = 0; s < n_stages; ++s) {
-    const eptq_stage& S = stages[s];
-    eptq::ChainStage& c = cs[s];
-    c = eptq::ChainStage();
-    if (S.n_layers < 1 || S.n_layers > eptq::kMaxLayers || !S.layers) {
-      delete[] cs;
-      return fail(EPTQ_EINVAL, "%s: stage %d has %d layers (1..%d)", fn, s, S.n_layers, eptq::kMaxLayers);
+    long long M = 0;
+    for (int l = 0; l < stages[s].n_layers && stages[s].layers; ++l) M += stages[s].layers[l].M;
+    b += step_out_bytes((int)M);
+  }
+  return b;
+}
+
+int eptq_step_init(int n_stages, const eptq_step_stage* stages, const void* codes, void* plan, void* work,
+                   eptq_step_launch* launch, void* stream) {
+  const char* fn = "eptq_step_init";
+  using eptq::step::Stage;
+  if (!stages || !codes || !plan || !work || !launch) return fail(EPTQ_EINVAL, "%s: null argument", fn);
+  if (n_stages <= 0 || n_stages > eptq::step::kMaxStages)
+    return fail(EPTQ_EINVAL, "%s: n_stages=%d (1..%d)", fn, n_stages, eptq::step::kMaxStages);
+  if (((uintptr_t)plan & 15) || ((uintptr_t)work & 255) || ((uintptr_t)codes & 7))
+    return fail(EPTQ_EINVAL, "%s: plan must be 16-, work 256- and codes 8-byte aligned", fn);
+  const int grid = eptq::step_grid();
+  Stage* hs = new Stage[n_stages];
+  char* out = (char*)work + eptq::step::kSyncBytes;
+  int rc = EPTQ_OK;
+  for (int s = 0; s < n_stages && rc == EPTQ_OK; ++s) {
+    const eptq_step_stage& in = stages[s];
+    Stage& S = hs[s];
+    memset(&S, 0, sizeof(S));
+    if (in.n_layers < 1 || in.n_layers > eptq::step::kMaxStageLayers || !in.layers) {
+      rc = fail(EPTQ_EINVAL, "%s: stage %d has %d layers (1..%d)", fn, s, in.n_layers, eptq::step::kMaxStageLayers);
+      break;
     }
-    if (!S.x || !S.y) {
-      delete[] cs;
-      return fail(EPTQ_EINVAL, "%s: stage %d: null x/y", fn, s);
+    S.n_layers = in.n_layers;
+    S.N = in.N;
+    S.nch = in.N / 8;
+    S.nseg = (S.nch + 127) / 128;   // items of 128 chunks (two per lane)
+    int M = 0;
+    for (int l = 0; l < in.n_layers && rc == EPTQ_OK; ++l) {
+      const eptq_layer& L = in.layers[l];
+      eptq::LinearArgs a;
+      rc = layer_args(fn, eptq::KIND_E8D4, L.Q, codes, EPTQ_F16, L.g, L.h, nullptr, EPTQ_F16, L.O_vals, L.O_col,
+                      L.O_row_ptr, L.bias, L.S_group, L.n_groups, L.M, in.N, 0, &a);
+      if (rc) break;
+      if (L.S_group) rc = fail(EPTQ_EUNSUPPORTED, "%s: stage %d layer %d: S_group is not supported", fn, s, l);
+      S.l[l] = {a.Q, a.g, a.h, a.bias, a.O, a.O_col, a.O_row_ptr, L.M, M};
+      M += L.M;
     }
-    c.n = S.n_layers;
-    c.wait = S.wait != 0;
-    for (int l = 0; l < S.n_layers; ++l) {
-      const eptq_layer& L = S.layers[l];
-      eptq::LinearArgs t;
-      int rc = layer_args(fn, eptq::KIND_E8D4, L.Q, codes, codes_dtype, L.g, L.h, S.x, EPTQ_F16, L.O_vals,
-                          L.O_col, L.O_row_ptr, L.bias, L.S_group, L.n_groups, L.M, S.N, 1, &t);
-      if (rc) {
-        delete[] cs;
-        return rc;
+    if (rc) break;
+    S.M_tot = M;
+    S.y_ll = (uint64_t*)out;
+    S.y = (uint16_t*)in.y;
+    out += step_out_bytes(M);
+    if ((M + grid - 1) / grid > eptq::step::kRowsMax) {
+      rc = fail(EPTQ_EUNSUPPORTED, "%s: stage %d has %d Q rows, more than %d per compute unit", fn, s, M,
+                eptq::step::kRowsMax);
+      break;
+    }
+    if (in.y && ((uintptr_t)in.y & 3)) { rc = fail(EPTQ_EINVAL, "%s: stage %d y must be 4-byte aligned", fn, s); break; }
+    S.src = in.src;
+    S.col = in.col;
+    if (in.src < 0) {
+      if (!in.x || !aligned16(in.x)) { rc = fail(EPTQ_EINVAL, "%s: stage %d needs a 16-byte aligned x", fn, s); break; }
+      S.x = (const uint16_t*)in.x;
+    } else {
+      if (in.src >= s) { rc = fail(EPTQ_EINVAL, "%s: stage %d reads stage %d (not earlier)", fn, s, in.src); break; }
+      if (in.col < 0 || (in.col & 3) || in.col + in.N > 8 * hs[in.src].M_tot) {
+        rc = fail(EPTQ_EINVAL, "%s: stage %d reads columns [%d, %d) of stage %d's %d outputs (col %% 4 == 0)", fn, s,
+                  in.col, in.col + in.N, in.src, 8 * hs[in.src].M_tot);
+        break;
       }
-      if (L.y_offset < 0 || L.y_offset + 8LL * L.M > (long long)S.ldy || (L.y_offset & 3)) {
-        delete[] cs;
-        return fail(EPTQ_EINVAL, "%s: stage %d layer %d columns [%lld, %lld) outside a y row of %d (offset %% 4 == 0)",
-                    fn, s, l, L.y_offset, L.y_offset + 8LL * L.M, S.ldy);
-      }
-      if (s == 0 && l == 0) has_s = L.S_group != nullptr;
-      if ((L.S_group != nullptr) != has_s) {
-        delete[] cs;
-        return fail(EPTQ_EUNSUPPORTED, "%s: all layers of a chain must have S_group or none", fn);
-      }
-      t.y = (uint16_t*)S.y + L.y_offset;
-      t.ldy = S.ldy;
-      c.l[l] = t;
+      S.x_ll = hs[in.src].y_ll;
+    }
+    if (in.norm_w) {
+      if (!aligned16(in.norm_w)) { rc = fail(EPTQ_EINVAL, "%s: stage %d norm_w must be 16-byte aligned", fn, s); break; }
+      S.prep = 1;
+      S.nw = (const eptq::f16*)in.norm_w;
+      S.eps = in.eps;
+    }
+    int why = 0;
+    if (eptq::step_check_stage(S, &why)) {
+      rc = fail(EPTQ_EUNSUPPORTED, "%s: stage %d (N=%d, %d layers, norm %d) is outside the engine's limits (%d)", fn,
+                s, S.N, S.n_layers, S.prep, why);
+      break;
     }
   }
-  eptq::ChainPlan* plan = nullptr;
-  const int rc = eptq::chain_create(cs, n_stages, &plan);
-  delete[] cs;
-  if (rc == -1) return fail(EPTQ_EUNSUPPORTED, "%s: a stage is outside the decode kernel's range", fn);
-  if (rc) return fail(EPTQ_EHIP, "%s: %s", fn, hipGetErrorString(hipGetLastError()));
-  *chain = (eptq_chain*)plan;
+  int off[4] = {0, 0, 0, 0};
+  size_t dyn = 0;
+  if (rc == EPTQ_OK) {
+    dyn = eptq::step_lds_layout(n_stages, hs, off);
+    if (dyn == 0) rc = fail(EPTQ_EUNSUPPORTED, "%s: the stages' activation side exceeds the LDS", fn);
+    else if (eptq::step_occupancy(dyn) < 1) rc = fail(EPTQ_EUNSUPPORTED, "%s: the engine kernel does not fit a CU", fn);
+  }
+  if (rc == EPTQ_OK) {
+    hipStream_t st = (hipStream_t)stream;
+    const long long wb = eptq_step_work_bytes(n_stages, stages);
+    if (hipMemcpyAsync(plan, hs, sizeof(Stage) * n_stages, hipMemcpyHostToDevice, st) != hipSuccess ||
+        hipMemsetAsync(work, 0, (size_t)wb, st) != hipSuccess || hipStreamSynchronize(st) != hipSuccess)
+      rc = fail(EPTQ_EHIP, "%s: %s", fn, hipGetErrorString(hipGetLastError()));
+  }
+  delete[] hs;
+  if (rc) return rc;
+  launch->n_stages = n_stages;
+  launch->grid = grid;
+  launch->dyn_lds = (int)dyn;
+  for (int i = 0; i < 4; ++i) launch->lds[i] = off[i];
   return EPTQ_OK;
 }
 
-int eptq_e8d4_chain_run(const eptq_chain* chain, void* stream) {
-  if (!chain) return fail(EPTQ_EINVAL, "eptq_e8d4_chain_run: null chain");
-  eptq::chain_run((const eptq::ChainPlan*)chain, (hipStream_t)stream);
-  return check_launch("eptq_e8d4_chain_run");
+int eptq_step_run(const void* plan, const void* codes, void* work, const eptq_step_launch* launch, void* stream) {
+  const char* fn = "eptq_step_run";
+  if (!plan || !codes || !work || !launch) return fail(EPTQ_EINVAL, "%s: null argument", fn);
+  if (launch->n_stages <= 0 || launch->dyn_lds <= 0) return fail(EPTQ_EINVAL, "%s: launch not initialized", fn);
+  if (launch->grid != eptq::step_grid())
+    return fail(EPTQ_EINVAL, "%s: plan made for %d compute units, this device has %d", fn, launch->grid,
+                eptq::step_grid());
+  if (eptq::step_launch((const eptq::step::Stage*)plan, launch->n_stages, (int*)work, codes, launch->lds,
+                        (size_t)launch->dyn_lds, (hipStream_t)stream))
+    return fail(EPTQ_EHIP, "%s: cannot configure the engine kernel", fn);
+  return check_launch(fn);
 }
 
-int eptq_e8d4_chain_check(eptq_chain* chain) {
-  if (!chain) return fail(EPTQ_EINVAL, "eptq_e8d4_chain_check: null chain");
-  const int rc = eptq::chain_check((eptq::ChainPlan*)chain);
-  if (rc == 1) return fail(EPTQ_ETIMEOUT, "eptq_e8d4_chain_check: a stage wait timed out; results are invalid");
-  if (rc) return fail(EPTQ_EHIP, "eptq_e8d4_chain_check: %s", hipGetErrorString(hipGetLastError()));
+int eptq_step_status(const void* work) {
+  if (!work) return fail(EPTQ_EINVAL, "eptq_step_status: null work");
+  int w[4] = {0, 0, 0, 0};
+  if (hipMemcpy(w, work, sizeof(w), hipMemcpyDeviceToHost) != hipSuccess)
+    return fail(EPTQ_EHIP, "eptq_step_status: %s", hipGetErrorString(hipGetLastError()));
+  if (w[eptq::step::kErrorWord]) return fail(EPTQ_ETIMEOUT, "eptq_step_status: a stage input wait gave up");
   return EPTQ_OK;
 }
-
-int eptq_e8d4_chain_grid(const eptq_chain* chain) {
-  return chain ? eptq::chain_grid((const eptq::ChainPlan*)chain) : 0;
-}
-
-void eptq_e8d4_chain_destroy(eptq_chain* chain) { eptq::chain_destroy((eptq::ChainPlan*)chain); }
 
 int eptq_llama_norm_linear(int n_layers, const eptq_layer* layers, const void* codes,
                            const void* resid, const void* delta, const void* w, float eps,

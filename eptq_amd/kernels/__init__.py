@@ -26,7 +26,7 @@ from . import _lib
 from ._lib import EPTQ_BF16, EPTQ_F16, EPTQ_F32, EptqError
 
 __all__ = ["e8_forward", "e8d4_forward", "e8_forward_grouped", "e8d4_forward_grouped",
-           "e8_dequant", "e8d4_dequant", "EptqError", "linear_forward", "linear_forward_multi",
+           "e8_dequant", "e8d4_dequant", "EptqError", "linear_forward", "linear_forward_multi", "DecodeStep",
            "dequant", "dequant_linear", "decode_workspace", "PREFILL_DEQUANT_MIN_TOKENS"]
 
 # From this many fp16 tokens on, the module forward (``EPTQLinear``,
@@ -155,76 +155,92 @@ def linear_forward_multi(layers, codes, x, work: Optional[torch.Tensor] = None) 
     return y
 
 
-class DecodeChain:
-    """A plan for ``eptq_e8d4_chain_*``: batch-1 E8-D4 stages run in order by
-    one persistent launch (a decode step's q|k|v, o, gate|up, down stages).
+class DecodeStep:
+    """A plan for the decode-step engine (``eptq_step_*``): batch-1 E8-D4
+    stages run in order by one persistent launch.
 
-    ``stages``: list of dicts with ``layers`` (1..4 dicts of EPTQLinear
-    buffers as for ``linear_forward_multi``), ``x`` (1, N) fp16, ``y`` (1, ldy)
-    fp16 with the layers' outputs side by side from column 0, and ``wait``
-    (read x only after every earlier stage has written its y; x may then be a
-    prefix of an earlier stage's y).  The plan keeps references to every
-    tensor; ``run`` launches on the current stream and allocates nothing."""
+    ``stages``: list of dicts with ``layers`` (1..3 dicts of EPTQLinear
+    buffers, as for ``linear_forward_multi``; outputs side by side), ``N``,
+    and the input: ``x`` (a (1, N) fp16 tensor) or ``src`` (index of an
+    earlier stage) and ``col`` (its first output column read); optional
+    ``norm_w`` (fp16 (N,), RMSNorm of the input) with ``eps``, and ``y`` (a
+    (1, 8·ΣM) fp16 tensor receiving a plain copy of the output).  The plan
+    keeps references to every tensor; ``run`` launches on the current stream
+    and allocates nothing."""
 
     def __init__(self, stages, codes):
         _require(len(stages) > 0, "no stages")
-        _require(codes.dtype == torch.float16, "the chain takes the fp16 table")
+        _require(codes.dtype == torch.float16 and codes.is_cuda and codes.is_contiguous(),
+                 "the decode step takes the fp16 (512, 4) table on the GPU")
         lib = _lib.load()
+        self.device = codes.device
         self._keep = [codes]
         self._arrs = []
-        st = (_lib.EptqStage * len(stages))()
-        device = codes.device
+        st = (_lib.EptqStepStage * len(stages))()
+        self.widths = []
         for i, S in enumerate(stages):
-            x, y = S["x"], S["y"]
-            _require(x.dtype == torch.float16 and y.dtype == torch.float16 and x.is_contiguous()
-                     and y.is_contiguous() and x.shape[0] == 1 and y.shape[0] == 1,
-                     "chain x and y must be contiguous (1, n) fp16 tensors")
-            N = int(x.shape[1])
+            N = int(S["N"])
             arr = (_lib.EptqLayer * len(S["layers"]))()
             off = 0
             for k, L in enumerate(S["layers"]):
                 M, n2, n_groups = _check_layer("e8_d4", L["Q"], codes, L["g"], L["h"], L["O_vals"], L["O_col"],
                                                L["O_row_ptr"], L.get("S_group"))
-                _require(n2 == N and L["Q"].device == device, "layers must take x's in_features on the table's device")
+                _require(n2 == N and L["Q"].device == self.device, "layers must take N inputs on the table's device")
                 arr[k] = _lib.EptqLayer(_ptr(L["Q"]), _ptr(L["g"]), _ptr(L["h"]), _ptr(L["O_vals"]),
                                         _ptr(L["O_col"]), _ptr(L["O_row_ptr"]), _ptr(L.get("bias")),
                                         _ptr(L.get("S_group")), n_groups, M, off)
                 off += 8 * M
                 self._keep.append(L)
-            _require(off <= y.shape[1], "stage outputs exceed y's width")
-            self._keep += [x, y]
+            self.widths.append(off)
+            x, y, nw = S.get("x"), S.get("y"), S.get("norm_w")
+            for t_ in (x, y, nw):
+                if t_ is not None:
+                    _require(t_.dtype == torch.float16 and t_.is_contiguous() and t_.device == self.device,
+                             "stage x, y and norm_w must be contiguous fp16 tensors on the table's device")
+                    self._keep.append(t_)
+            src = int(S.get("src", -1))
+            st[i] = _lib.EptqStepStage(len(S["layers"]), ctypes.addressof(arr), N, src,
+                                       _ptr(x) if src < 0 else None, int(S.get("col", 0)), _ptr(nw),
+                                       float(S.get("eps", 1e-5)), _ptr(y))
             self._arrs.append(arr)
-            st[i] = _lib.EptqStage(len(S["layers"]), ctypes.addressof(arr), _ptr(x), N, _ptr(y),
-                                   int(y.shape[1]), 1 if S.get("wait", True) else 0)
-        self._handle = ctypes.c_void_p()
-        self.device = device
-        with torch.cuda.device(device):
-            rc = lib.eptq_e8d4_chain_create(len(stages), st, _ptr(codes), EPTQ_F16, ctypes.byref(self._handle))
-        _lib.check(rc, "eptq_e8d4_chain_create")
-        self.n_stages = len(stages)
-        self.grid = lib.eptq_e8d4_chain_grid(self._handle)
+        n = len(stages)
+        with torch.cuda.device(self.device):
+            self.plan = torch.empty(int(lib.eptq_step_plan_bytes(n)), dtype=torch.uint8, device=self.device)
+            self.work = torch.empty(int(lib.eptq_step_work_bytes(n, st)), dtype=torch.uint8, device=self.device)
+            self.launch = _lib.EptqStepLaunch()
+            rc = lib.eptq_step_init(n, st, _ptr(codes), _ptr(self.plan), _ptr(self.work), ctypes.byref(self.launch),
+                                    torch.cuda.current_stream().cuda_stream)
+        _lib.check(rc, "eptq_step_init")
+        self.n_stages = n
+        self._codes = codes
+        # Byte offset of each stage's flagged output in the work area.
+        self._out = []
+        o = 256
+        for w in self.widths:
+            self._out.append(o)
+            o += (4 * w + 255) // 256 * 256
 
     def run(self) -> None:
         with torch.cuda.device(self.device):
-            rc = _lib.load().eptq_e8d4_chain_run(self._handle, torch.cuda.current_stream().cuda_stream)
-        _lib.check(rc, "eptq_e8d4_chain_run")
+            rc = _lib.load().eptq_step_run(_ptr(self.plan), _ptr(self._codes), _ptr(self.work),
+                                           ctypes.byref(self.launch), torch.cuda.current_stream().cuda_stream)
+        _lib.check(rc, "eptq_step_run")
 
-    def check(self) -> None:
-        """Raise if a stage wait timed out since the last check (synchronizes)."""
+    def status(self) -> None:
+        """Raise if a stage input wait gave up in an earlier run (synchronizes)."""
         torch.cuda.synchronize(self.device)
-        _lib.check(_lib.load().eptq_e8d4_chain_check(self._handle), "eptq_e8d4_chain_check")
+        _lib.check(_lib.load().eptq_step_status(_ptr(self.work)), "eptq_step_status")
 
-    def close(self) -> None:
-        if getattr(self, "_handle", None) and self._handle.value:
-            torch.cuda.synchronize(self.device)
-            _lib.load().eptq_e8d4_chain_destroy(self._handle)
-            self._handle = ctypes.c_void_p()
+    def output(self, s: int) -> torch.Tensor:
+        """Stage s's output of the last run as a (1, width) fp16 tensor
+        (a copy without the flags)."""
+        w = self.widths[s]
+        words = self.work[self._out[s]:self._out[s] + 4 * w].view(torch.int32).view(-1, 2)
+        return words[:, 0].contiguous().view(torch.float16).reshape(1, w).clone()
 
-    def __del__(self):
-        try:
-            self.close()
-        except Exception:
-            pass
+    def flags(self, s: int) -> torch.Tensor:
+        w = self.widths[s]
+        return self.work[self._out[s]:self._out[s] + 4 * w].view(torch.int32).view(-1, 2)[:, 1].clone()
 
 
 def dequant(kind: str, Q, codes, g, h, O_vals, O_col, O_row_ptr, S_group=None,

@@ -25,11 +25,11 @@ SIGNATURES = {
     "eptq_e8_forward": ([_P, _P, _I, _P, _P, _P, _I, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _P], _I),
     "eptq_e8d4_forward_multi": ([_I, _P, _P, _I, _P, _I, _I, _I, _P, _I, _P, ctypes.c_longlong, _P], _I),
     "eptq_e8d4_work_bytes": ([], ctypes.c_longlong),
-    "eptq_e8d4_chain_create": ([_I, _P, _P, _I, ctypes.POINTER(_P)], _I),
-    "eptq_e8d4_chain_run": ([_P, _P], _I),
-    "eptq_e8d4_chain_check": ([_P], _I),
-    "eptq_e8d4_chain_grid": ([_P], _I),
-    "eptq_e8d4_chain_destroy": ([_P], None),
+    "eptq_step_plan_bytes": ([_I], ctypes.c_longlong),
+    "eptq_step_work_bytes": ([_I, _P], ctypes.c_longlong),
+    "eptq_step_init": ([_I, _P, _P, _P, _P, _P, _P], _I),
+    "eptq_step_run": ([_P, _P, _P, _P, _P], _I),
+    "eptq_step_status": ([_P], _I),
     "eptq_e8d4_dequant": ([_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _P, _P], _I),
     "eptq_e8_dequant": ([_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _P, _P], _I),
 }
@@ -40,10 +40,15 @@ class EptqLayer(ctypes.Structure):
                 ("bias", _P), ("S_group", _P), ("n_groups", _I), ("M", _I), ("y_offset", ctypes.c_longlong)]
 
 
-class EptqStage(ctypes.Structure):
-    """``eptq_stage`` of include/eptq_hip.h."""
-    _fields_ = [("n_layers", _I), ("layers", _P), ("x", _P), ("N", _I), ("y", _P), ("ldy", _I),
-                ("wait", _I)]
+class EptqStepStage(ctypes.Structure):
+    """``eptq_step_stage`` of include/eptq_hip.h."""
+    _fields_ = [("n_layers", _I), ("layers", _P), ("N", _I), ("src", _I), ("x", _P), ("col", _I),
+                ("norm_w", _P), ("eps", ctypes.c_float), ("y", _P)]
+
+
+class EptqStepLaunch(ctypes.Structure):
+    """``eptq_step_launch`` of include/eptq_hip.h."""
+    _fields_ = [("n_stages", _I), ("grid", _I), ("dyn_lds", _I), ("lds", _I * 4)]
 
 
 # Fused decode-step operators of the Llama harness (include/eptq_llama.h).

@@ -1,0 +1,92 @@
+"""Short eager programs for ``rocprofv3`` (counterpart of the reference's
+``profile_kernel.py``): each case builds seeded synthetic layers on the GPU,
+launches the kernel under study a few times without HIP graphs, and exits.
+
+Counter passes (``rocprofv3 --pmc``) are run over these programs only: a few
+dozen dispatches each, no graph capture.
+
+    python -m eptq_amd.profile_cases decode --shape 4096x4096 --batch 1 --copies 8
+    python -m eptq_amd.profile_cases prefill --shape 5120x5120 --tokens 2048
+    python -m eptq_amd.profile_cases e8 --shape 3072x768 --copies 8
+    python -m eptq_amd.profile_cases step --layers 4
+"""
+
+from __future__ import annotations
+
+import argparse
+import sys
+
+
+def _layer(torch, out, inp, seed, p, dev, qb=None, bias=False):
+    from eptq_amd.synthetic import make_layer
+    qd = make_layer(out, inp, seed=seed, percmask=p, qb_size=qb, bias=bias, device=dev)
+    rows, cols = (qd.Q == 32767).nonzero(as_tuple=True)
+    rp = torch.cat([torch.zeros(1, dtype=torch.int32, device=dev),
+                    torch.bincount(rows, minlength=qd.Q.shape[0]).cumsum(0).to(torch.int32)])
+    return dict(Q=qd.Q, g=qd.g, h=qd.h, O_vals=qd.O, O_col=cols.to(torch.int32), O_row_ptr=rp,
+                bias=qd.bias, S_group=qd.S_group)
+
+
+def main(argv=None) -> None:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("case", choices=["decode", "prefill", "e8", "step"])
+    ap.add_argument("--shape", default="4096x4096", help="out x in")
+    ap.add_argument("--batch", type=int, default=1)
+    ap.add_argument("--tokens", type=int, default=2048)
+    ap.add_argument("--copies", type=int, default=8, help="distinct layers, one launch each")
+    ap.add_argument("--reps", type=int, default=2, help="passes over the copies")
+    ap.add_argument("--layers", type=int, default=4, help="decoder layers (case step)")
+    ap.add_argument("--qb", type=int, default=0)
+    args = ap.parse_args(argv)
+
+    import torch
+    from eptq_amd.kernels import linear_forward, linear_forward_multi, decode_workspace
+    from eptq_amd.quantizers import E8D4Quantizer, E8LatticeQuantizer
+    from eptq_amd.synthetic import make_x
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    out, inp = (int(v) for v in args.shape.split("x"))
+    qb = args.qb or None
+    if args.case in ("decode", "prefill"):
+        codes = E8D4Quantizer(radius=1.75).flat_table().half().to(dev)
+        T = args.batch if args.case == "decode" else args.tokens
+        layers = [_layer(torch, out, inp, 7000 + c, 0.001, dev, qb=qb) for c in range(args.copies)]
+        x = make_x(T, inp, seed=1, device=dev)
+        torch.cuda.synchronize()
+        for _ in range(args.reps):
+            for L in layers:
+                linear_forward("e8_d4", L["Q"], codes, L["g"], L["h"], x, L["O_vals"], L["O_col"],
+                               L["O_row_ptr"], None, L["S_group"])
+    elif args.case == "e8":
+        codes = E8LatticeQuantizer(radius=1.6).flat_table().half().to(dev)
+        layers = [_layer(torch, out, inp, 7100 + c, 0.002, dev, bias=True) for c in range(args.copies)]
+        x = make_x(args.batch, inp, seed=2, device=dev)
+        torch.cuda.synchronize()
+        for _ in range(args.reps):
+            for L in layers:
+                linear_forward("e8_lattice", L["Q"], codes, L["g"], L["h"], x, L["O_vals"], L["O_col"],
+                               L["O_row_ptr"], L["bias"], None)
+    else:
+        # One decode step's Linear units of args.layers Llama-2-7B layers:
+        # q|k|v and gate|up as multi-layer launches, o and down alone.
+        codes = E8D4Quantizer(radius=1.75).flat_table().half().to(dev)
+        work = decode_workspace(dev)
+        units = []
+        for li in range(args.layers):
+            mk = lambda o, i, k: _layer(torch, o, i, 8000 + 10 * li + k, 0.001, dev)
+            units.append([mk(4096, 4096, k) for k in range(3)])
+            units.append([mk(4096, 4096, 3)])
+            units.append([mk(11008, 4096, 4), mk(11008, 4096, 5)])
+            units.append([mk(4096, 11008, 6)])
+        xs = {n: make_x(args.batch, n, seed=n, device=dev) for n in (4096, 11008)}
+        torch.cuda.synchronize()
+        for _ in range(args.reps):
+            for u in units:
+                linear_forward_multi(u, codes, xs[int(u[0]["Q"].shape[1])], work=work)
+    torch.cuda.synchronize()
+    print(f"profile case {args.case} done", flush=True)
+
+
+if __name__ == "__main__":
+    main(sys.argv[1:])

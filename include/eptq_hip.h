@@ -1,10 +1,12 @@
 /*
  * eptq_hip.h — C ABI of the MI355X (gfx950) EPTQ quantized-Linear library.
  *
- * Every entry point takes plain device pointers, sizes and a hipStream_t
- * (passed as void*), launches asynchronously on that stream, allocates
- * nothing, keeps no pointer after returning, and returns EPTQ_OK or an error
- * code; eptq_last_error() then describes the failure (per host thread).
+ * Every entry point takes plain device pointers and sizes, allocates no
+ * device memory, keeps no pointer after returning, and returns EPTQ_OK or an
+ * error code; eptq_last_error() then describes the failure (per host
+ * thread).  The compute entry points take a hipStream_t (passed as void*) and
+ * launch asynchronously on it; the two exceptions, eptq_step_init and
+ * eptq_step_status, synchronize and say so where they are declared.
  *
  * Layer format (reference config.py:98-159, kernels/linear.py:83-152):
  *   Q          int16 (M, N) row-major, stored as index - 32768; 32767 marks a
@@ -37,7 +39,7 @@ enum {
   EPTQ_EINVAL = 1,        /* null pointer / negative size / inconsistent args */
   EPTQ_EUNSUPPORTED = 2,  /* shape or alignment outside what the kernels take */
   EPTQ_EHIP = 3,          /* HIP runtime reported an error at launch */
-  EPTQ_ETIMEOUT = 4       /* a decode chain's stage wait gave up (results invalid) */
+  EPTQ_ETIMEOUT = 4       /* a decode-step stage wait gave up (results invalid) */
 };
 
 enum { EPTQ_F16 = 0, EPTQ_F32 = 1, EPTQ_BF16 = 2 };
@@ -107,46 +109,75 @@ int eptq_e8d4_forward_multi(int n_layers, const eptq_layer* layers, const void* 
 long long eptq_e8d4_work_bytes(void);
 
 /*
- * Decode chain: a sequence of batch-1 E8-D4 stages run by one persistent
- * launch.  A stage is up to 4 layers that read the same x (1, N) fp16 and
- * write columns [y_offset, y_offset + 8M) of y (1, ldy) fp16, as in
- * eptq_e8d4_forward_multi.  With `wait` set, the stage reads x only after
- * every earlier stage of the chain has written its y, so x may be (a prefix
- * of) an earlier stage's y: the stages of a decode step (q|k|v, o, gate|up,
- * down per transformer layer) in one launch, with the index stream of a
- * stage in flight before its input is ready.  No counterpart in the
- * reference, which launches one kernel per Linear (kernels/linear.py:154-212)
- * and captures a decode step in a CUDA graph (bench_decode.py:56-69).
+ * Decode-step engine (batch 1, E8-D4, fp16): a sequence of dependent Linear
+ * stages — a decode step's q|k|v, o, gate|up and down for every transformer
+ * layer — run by ONE persistent launch, one workgroup per compute unit.  The
+ * index stream of later stages is in flight while a stage waits for its
+ * input, so the per-launch fixed cost of eptq_e8d4_forward_multi (launch gap,
+ * first-load latency, drain) is paid once per step instead of once per stage.
  *
- * create validates every stage (fp16 table, the same table and S_group
- * presence for all layers, N within the decode kernel's range), sizes the
- * persistent grid from this device's occupancy, allocates the plan's device
- * memory (stage table and synchronization counters) and copies the stages;
- * it synchronizes the device.  The pointers in `stages` are kept by the plan.
- * run launches the chain on `stream` and allocates nothing (it can be
- * captured in a HIP graph); one plan must not run twice concurrently.
- * check (after the stream is synchronized) returns EPTQ_ETIMEOUT if a stage
- * wait gave up since the last check (e.g. another kernel held the CUs), else
- * EPTQ_OK.  grid returns the plan's workgroup count.
+ * A stage is 1..3 layers that read the same input (outputs side by side in
+ * layer order, as eptq_e8d4_forward_multi with consecutive y_offsets; the
+ * layers' y_offset fields are ignored; no S_group).  Its input is either a
+ * plain fp16 (1, N) vector x (src = -1) or columns [col, col + N) of the
+ * output of an earlier stage src; with norm_w it is RMSNorm'd first:
+ * fp16(x · rsqrt(mean(x²) + eps) · norm_w).  Stage outputs live in the work
+ * area in a flagged form (each 8-byte word: two fp16 outputs and a 32-bit
+ * flag), so a stage boundary costs one store and one poll; y, if given,
+ * receives a plain fp16 copy of the stage's output.
+ *
+ * Limits: N a multiple of 8 and <= 11264; n_layers·N <= 12288; N <= 4096
+ * for a stage with norm_w; col a multiple of 4; at most 16 Q rows of a stage
+ * per compute unit (ΣM <= 16 · CUs); at most 1024 stages.
+ *
+ * No counterpart in the reference, whose decode step calls one Linear per
+ * projection (bench_decode.py:44-71, kernels/linear.py:154-212); its callers
+ * are batch-1 decode loops.
  */
 typedef struct {
-  int n_layers;               /* 1..4 */
+  int n_layers;               /* 1..3 */
   const eptq_layer* layers;
-  const void* x;              /* (1, N) fp16 device */
-  int N;
-  void* y;                    /* (1, ldy) fp16 device */
-  int ldy;
-  int wait;                   /* nonzero: after every earlier stage */
-} eptq_stage;
+  int N;                      /* in_features of the layers */
+  int src;                    /* -1: plain input x; else an earlier stage */
+  const void* x;              /* (1, N) fp16 device, 16-byte aligned (src < 0) */
+  int col;                    /* first input column of stage src's output */
+  const void* norm_w;         /* fp16 (N) RMSNorm weight, or NULL */
+  float eps;
+  void* y;                    /* (1, 8·ΣM) fp16 device copy of the output, or NULL */
+} eptq_step_stage;
 
-typedef struct eptq_chain eptq_chain;
+/* Launch parameters filled by eptq_step_init (host memory). */
+typedef struct {
+  int n_stages;
+  int grid;
+  int dyn_lds;
+  int lds[4];
+} eptq_step_launch;
 
-int eptq_e8d4_chain_create(int n_stages, const eptq_stage* stages, const void* codes,
-                           int codes_dtype, eptq_chain** chain);
-int eptq_e8d4_chain_run(const eptq_chain* chain, void* stream);
-int eptq_e8d4_chain_check(eptq_chain* chain);
-int eptq_e8d4_chain_grid(const eptq_chain* chain);
-void eptq_e8d4_chain_destroy(eptq_chain* chain);
+/* Bytes of the device plan for n_stages stages. */
+long long eptq_step_plan_bytes(int n_stages);
+
+/* Bytes of the device work area (synchronization words and every stage's
+ * flagged output) for these stages. */
+long long eptq_step_work_bytes(int n_stages, const eptq_step_stage* stages);
+
+/* Validate the stages and write the plan (plan: eptq_step_plan_bytes bytes,
+ * 16-byte aligned device memory) and a zeroed work area (work:
+ * eptq_step_work_bytes bytes, 256-byte aligned device memory), both
+ * caller-owned; codes: the fp16 (512, 4) table.  Synchronizes the stream:
+ * call outside graph capture.  Allocates nothing. */
+int eptq_step_init(int n_stages, const eptq_step_stage* stages, const void* codes, void* plan, void* work,
+                   eptq_step_launch* launch, void* stream);
+
+/* One run of every stage of the plan: one launch on the stream, no
+ * allocation, no synchronization (graph-capturable).  Runs that share a work
+ * area must not overlap in time. */
+int eptq_step_run(const void* plan, const void* codes, void* work, const eptq_step_launch* launch,
+                  void* stream);
+
+/* EPTQ_ETIMEOUT if a stage input wait of an earlier run gave up (its outputs
+ * are then invalid), else EPTQ_OK.  Synchronous (reads the work area). */
+int eptq_step_status(const void* work);
 
 /*
  * Fused E8-lattice quantized Linear (same math, 8-vector = codes[u]).

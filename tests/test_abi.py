@@ -134,33 +134,6 @@ def test_llama_ops_reject_invalid_arguments(lib):
     assert lib.eptq_llama_silu_mul(16, 16, 1, 12, None) == 1
 
 
-def test_chain_entry_points_validate_before_any_device_call(lib):
-    L, St = _lib.EptqLayer, _lib.EptqStage
-    layer = L(16, 16, 16, None, None, 16, None, None, 0, 4, 0)
-    layers = (L * 1)(layer)
-    good = St(1, ctypes.addressof(layers), 16, 64, 16, 32, 1)
-    h = ctypes.c_void_p()
-    create = lib.eptq_e8d4_chain_create
-    assert create(1, (St * 1)(good), 16, _lib.EPTQ_F16, None) == _lib.EPTQ_EINVAL
-    assert create(0, (St * 1)(good), 16, _lib.EPTQ_F16, ctypes.byref(h)) == _lib.EPTQ_EINVAL
-    assert create(1, (St * 1)(good), 16, _lib.EPTQ_F32, ctypes.byref(h)) == _lib.EPTQ_EUNSUPPORTED
-    assert "fp16 table" in lib.eptq_last_error().decode()
-    no_layers = St(0, ctypes.addressof(layers), 16, 64, 16, 32, 1)
-    assert create(1, (St * 1)(no_layers), 16, _lib.EPTQ_F16, ctypes.byref(h)) == _lib.EPTQ_EINVAL
-    null_x = St(1, ctypes.addressof(layers), None, 64, 16, 32, 1)
-    assert create(1, (St * 1)(null_x), 16, _lib.EPTQ_F16, ctypes.byref(h)) == _lib.EPTQ_EINVAL
-    narrow = St(1, ctypes.addressof(layers), 16, 64, 16, 24, 1)    # 8M = 32 columns > ldy
-    assert create(1, (St * 1)(narrow), 16, _lib.EPTQ_F16, ctypes.byref(h)) == _lib.EPTQ_EINVAL
-    assert "outside a y row" in lib.eptq_last_error().decode()
-    bad_n = St(1, ctypes.addressof(layers), 16, 60, 16, 32, 1)     # N % 8
-    assert create(1, (St * 1)(bad_n), 16, _lib.EPTQ_F16, ctypes.byref(h)) == _lib.EPTQ_EUNSUPPORTED
-    assert h.value is None
-    assert lib.eptq_e8d4_chain_run(None, None) == _lib.EPTQ_EINVAL
-    assert lib.eptq_e8d4_chain_check(None) == _lib.EPTQ_EINVAL
-    assert lib.eptq_e8d4_chain_grid(None) == 0
-    lib.eptq_e8d4_chain_destroy(None)
-
-
 def test_fused_llama_linears_validate_arguments(lib):
     L = _lib.EptqLayer
     arr = (L * 1)(L(16, 16, 16, None, None, 16, None, None, 0, 4, 0))

@@ -96,11 +96,14 @@ def test_load_quantized_model_warped_chosen_r(warped_dir):
     handler = get_model_handler_by_type(ModelHandler.detect_model_type(model))
     n_warped = n_plain = 0
     for lid, layer in enumerate(handler.get_layers(model)):
-        for name, lin in handler.get_linear_layers(layer).items():
+        # The loader swapped the layer's Linears in named_modules order.
+        for name, lin in [(n, m) for n, m in layer.named_modules() if isinstance(m, EPTQLinear)]:
             qd = load_quantized_layer(warped_dir / f"layer_{lid}", name)
             want, _ = _table_for(qcpu, "e8_d4", qd.chosen_r)
             got = lin._table_f32.cpu()
-            assert torch.allclose(got, want, rtol=2e-7, atol=0), (lid, name)
+            ulps = (got.view(torch.int32).long() - want.view(torch.int32).long()).abs().max().item()
+            print(f"  layer {lid} {name} chosen_r={qd.chosen_r}: table within {ulps} ulp of the CPU replay")
+            assert ulps <= 4, (lid, name, ulps)
             plain = torch.equal(want, (qcpu._raw_codes / (qd.chosen_r or 1.75)).reshape(512, 4))
             n_plain += plain
             n_warped += not plain
