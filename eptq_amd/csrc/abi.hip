@@ -9,10 +9,23 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <atomic>
+#include <mutex>
+
 #include "eptq_hip.h"
 #include "eptq_llama.h"
 #include "kernels.h"
 #include "step.h"
+
+// Scratch of eptq_e8d4_forward_multi_noalloc: the matrix-core decode's
+// split-K workspace (tile counters, then partial sums for up to 256 CUs), a
+// file-scope device array; each GPU holds its own copy until the process
+// ends.  Host code uses only the per-device address from
+// hipGetSymbolAddress (in host code the array's name is a stand-in, not a
+// device address).
+constexpr size_t kNoAllocScratchBytes = eptq::kSplitCounterBytes + 256 * eptq::kSplitPartBytes;
+static_assert(kNoAllocScratchBytes == EPTQ_NOALLOC_SCRATCH_BYTES, "header constant");
+static __device__ __align__(256) char scratch[kNoAllocScratchBytes];
 
 namespace {
 
@@ -224,36 +237,11 @@ int fused_linear(const char* fn, int n, const eptq_layer* layers, const void* co
   return check_launch(fn);
 }
 
-}  // namespace
-
-extern "C" {
-
-int eptq_abi_version(void) { return 1; }
-
-const char* eptq_last_error(void) { return g_err; }
-
-int eptq_e8d4_forward(const void* Q, const void* codes, int codes_dtype, const void* g,
-                      const void* h, const void* x, int x_dtype, const void* O_vals,
-                      const void* O_col, const void* O_row_ptr, const void* bias,
-                      const void* S_group, int n_groups, int M, int N, int B, void* y,
-                      void* stream) {
-  return linear_common(eptq::KIND_E8D4, Q, codes, codes_dtype, g, h, x, x_dtype, O_vals, O_col,
-                       O_row_ptr, bias, S_group, n_groups, M, N, B, y, stream);
-}
-
-int eptq_e8_forward(const void* Q, const void* codes, int codes_dtype, const void* g,
-                    const void* h, const void* x, int x_dtype, const void* O_vals,
-                    const void* O_col, const void* O_row_ptr, const void* bias,
-                    const void* S_group, int n_groups, int M, int N, int B, void* y,
-                    void* stream) {
-  return linear_common(eptq::KIND_E8, Q, codes, codes_dtype, g, h, x, x_dtype, O_vals, O_col,
-                       O_row_ptr, bias, S_group, n_groups, M, N, B, y, stream);
-}
-
-int eptq_e8d4_forward_multi(int n_layers, const eptq_layer* layers, const void* codes,
-                            int codes_dtype, const void* x, int x_dtype, int N, int B, void* y,
-                            int ldy, void* work, long long work_bytes, void* stream) {
-  const char* fn = "eptq_e8d4_forward_multi";
+// Body of eptq_e8d4_forward_multi and of its allocation-free variant, which
+// passes the library's own scratch as `work`.
+int forward_multi(const char* fn, int n_layers, const eptq_layer* layers, const void* codes, int codes_dtype,
+                  const void* x, int x_dtype, int N, int B, void* y, int ldy, void* work, long long work_bytes,
+                  void* stream) {
   if (n_layers <= 0 || !layers) return fail(EPTQ_EINVAL, "%s: n_layers=%d", fn, n_layers);
   if (work && (!aligned16(work) || work_bytes < 0))
     return fail(EPTQ_EINVAL, "%s: work must be 16-byte aligned with work_bytes >= 0", fn);
@@ -308,6 +296,96 @@ int eptq_e8d4_forward_multi(int n_layers, const eptq_layer* layers, const void* 
     }
   }
   return check_launch(fn);
+}
+
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+std::atomic<char*> g_scratch[kMaxDevices];
+
+__global__ void k_clear_words(uint32_t* p, int n) {
+  for (int i = (int)(blockIdx.x * blockDim.x + threadIdx.x); i < n; i += (int)(gridDim.x * blockDim.x)) p[i] = 0u;
+}
+
+// Device address of the current device's scratch.  The first call on a
+// device looks it up (with that device current) and queues on `s` a kernel
+// that zeroes the tile counters; every launch that uses a counter afterwards
+// returns it to zero, so later calls find them cleared.  The partial sums
+// need no clearing (each is written before it is read).
+int scratch_of_device(const char* fn, hipStream_t s, char** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess) return fail(EPTQ_EHIP, "%s: hipGetDevice failed", fn);
+  if (dev < 0 || dev >= kMaxDevices) return fail(EPTQ_EUNSUPPORTED, "%s: device %d (at most %d)", fn, dev, kMaxDevices);
+  char* p = g_scratch[dev].load(std::memory_order_acquire);
+  if (!p) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch[dev].load(std::memory_order_relaxed);
+    if (!p) {
+      void* q = nullptr;
+      const hipError_t e = hipGetSymbolAddress(&q, HIP_SYMBOL(scratch));
+      if (e != hipSuccess || !q)
+        return fail(EPTQ_EHIP, "%s: hipGetSymbolAddress(scratch): %s", fn, hipGetErrorString(e));
+      k_clear_words<<<eptq::kSplitCounters / 256, 256, 0, s>>>((uint32_t*)q, eptq::kSplitCounters);
+      if (const int rc = check_launch(fn)) return rc;
+      p = (char*)q;
+      g_scratch[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return EPTQ_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int eptq_abi_version(void) { return 2; }
+
+const char* eptq_last_error(void) { return g_err; }
+
+int eptq_e8d4_forward(const void* Q, const void* codes, int codes_dtype, const void* g,
+                      const void* h, const void* x, int x_dtype, const void* O_vals,
+                      const void* O_col, const void* O_row_ptr, const void* bias,
+                      const void* S_group, int n_groups, int M, int N, int B, void* y,
+                      void* stream) {
+  return linear_common(eptq::KIND_E8D4, Q, codes, codes_dtype, g, h, x, x_dtype, O_vals, O_col,
+                       O_row_ptr, bias, S_group, n_groups, M, N, B, y, stream);
+}
+
+int eptq_e8_forward(const void* Q, const void* codes, int codes_dtype, const void* g,
+                    const void* h, const void* x, int x_dtype, const void* O_vals,
+                    const void* O_col, const void* O_row_ptr, const void* bias,
+                    const void* S_group, int n_groups, int M, int N, int B, void* y,
+                    void* stream) {
+  return linear_common(eptq::KIND_E8, Q, codes, codes_dtype, g, h, x, x_dtype, O_vals, O_col,
+                       O_row_ptr, bias, S_group, n_groups, M, N, B, y, stream);
+}
+
+int eptq_e8d4_forward_multi(int n_layers, const eptq_layer* layers, const void* codes,
+                            int codes_dtype, const void* x, int x_dtype, int N, int B, void* y,
+                            int ldy, void* work, long long work_bytes, void* stream) {
+  return forward_multi("eptq_e8d4_forward_multi", n_layers, layers, codes, codes_dtype, x, x_dtype, N, B, y, ldy,
+                       work, work_bytes, stream);
+}
+
+int eptq_e8d4_forward_multi_noalloc(int n_layers, const eptq_layer* layers, const void* codes,
+                                    int codes_dtype, const void* x, int x_dtype, int N, int B, void* y,
+                                    int ldy, void* stream) {
+  const char* fn = "eptq_e8d4_forward_multi_noalloc";
+  if (n_layers > 0 && layers) {
+    long long tiles = 0;
+    for (int l = 0; l < n_layers; ++l)
+      tiles += layers[l].M > 0 ? (8LL * layers[l].M + eptq::kSplitTileRows - 1) / eptq::kSplitTileRows : 0;
+    if (tiles > eptq::kSplitCounters)
+      return fail(EPTQ_EUNSUPPORTED,
+                  "%s: %lld tiles of %d output rows exceed the scratch's %d tile counters (at most %lld output "
+                  "rows per call)", fn, tiles, eptq::kSplitTileRows, eptq::kSplitCounters,
+                  (long long)eptq::kSplitCounters * eptq::kSplitTileRows);
+  }
+  char* work = nullptr;
+  if (const int rc = scratch_of_device(fn, (hipStream_t)stream, &work)) return rc;
+  return forward_multi(fn, n_layers, layers, codes, codes_dtype, x, x_dtype, N, B, y, ldy, work,
+                       (long long)kNoAllocScratchBytes, stream);
 }
 
 long long eptq_e8d4_work_bytes(void) { return eptq::decode_mfma_work_bytes(); }

@@ -63,9 +63,10 @@ constexpr int kS = 8;           // column waves per workgroup (one workgroup per
 // Split-K workspace: per-tile arrival counters, then the fp32 partial sums
 // [split tile][part][16][64] of the tiles whose columns are split over P
 // workgroups.
-constexpr int kMaxCounters = 16384;
-constexpr size_t kCntBytes = (size_t)kMaxCounters * 4;
-constexpr size_t kPartBytes = 16 * 64 * 4;
+constexpr int kMaxCounters = kSplitCounters;
+constexpr size_t kCntBytes = kSplitCounterBytes;
+constexpr size_t kPartBytes = kSplitPartBytes;
+static_assert(kTile * 8 == kSplitTileRows, "one counter per tile");
 constexpr int kMaxParts = 4;
 
 __device__ __forceinline__ void st_pair(float* p, float a, float b) {

@@ -100,6 +100,13 @@ int launch_decode_e8d4_pair(const LinearArgs* layers, hipStream_t s);
 // -1 when the layers are outside its range.
 int launch_decode_mfma_multi(const LinearArgs* layers, int n, hipStream_t s, void* work = nullptr,
                              long long work_bytes = 0);
+// Split-K workspace of the matrix-core decode kernel: kSplitCounters int
+// arrival counters (one per 64-row tile of a launch), then fp32 partial sums,
+// kSplitPartBytes per (split tile, part).
+constexpr int kSplitCounters = 16384;
+constexpr size_t kSplitCounterBytes = (size_t)kSplitCounters * 4;
+constexpr size_t kSplitPartBytes = 16 * 64 * 4;
+constexpr int kSplitTileRows = 64;
 // Workspace bytes that let the matrix-core decode split every launch it takes.
 long long decode_mfma_work_bytes();
 namespace dec { int mfma_min_batch_init(); }

@@ -25,6 +25,7 @@ SIGNATURES = {
     "eptq_e8_forward": ([_P, _P, _I, _P, _P, _P, _I, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _P], _I),
     "eptq_e8d4_forward_multi": ([_I, _P, _P, _I, _P, _I, _I, _I, _P, _I, _P, ctypes.c_longlong, _P], _I),
     "eptq_e8d4_work_bytes": ([], ctypes.c_longlong),
+    "eptq_e8d4_forward_multi_noalloc": ([_I, _P, _P, _I, _P, _I, _I, _I, _P, _I, _P], _I),
     "eptq_step_plan_bytes": ([_I], ctypes.c_longlong),
     "eptq_step_work_bytes": ([_I, _P], ctypes.c_longlong),
     "eptq_step_init": ([_I, _P, _P, _P, _P, _P, _P], _I),

@@ -109,6 +109,29 @@ int eptq_e8d4_forward_multi(int n_layers, const eptq_layer* layers, const void* 
 long long eptq_e8d4_work_bytes(void);
 
 /*
+ * eptq_e8d4_forward_multi with no workspace argument and no allocation: the
+ * split-K workspace is the library's own scratch, a static device array of
+ * EPTQ_NOALLOC_SCRATCH_BYTES per GPU (tile counters, then partial sums),
+ * held by each GPU the library runs on until the process ends.  No
+ * counterpart in the reference; for callers that cannot allocate (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Same arguments, checks and results as eptq_e8d4_forward_multi with a
+ * workspace of that size.
+ *
+ * Limit: at most 16384 tiles of 64 output rows (1048576 rows) over all layers
+ * of a call, else EPTQ_EUNSUPPORTED.  The first call on a device looks the
+ * array up and queues a kernel on `stream` that zeroes its counters (make
+ * that call outside graph capture); every launch that uses a counter returns
+ * it to zero.  All calls on one GPU share its array, which keeps the last
+ * call's contents: calls that overlap in time on one GPU race (wrong
+ * results), whatever their streams.
+ */
+#define EPTQ_NOALLOC_SCRATCH_BYTES 1114112
+int eptq_e8d4_forward_multi_noalloc(int n_layers, const eptq_layer* layers, const void* codes,
+                                    int codes_dtype, const void* x, int x_dtype, int N, int B, void* y,
+                                    int ldy, void* stream);
+
+/*
  * Decode-step engine (batch 1, E8-D4, fp16): a sequence of dependent Linear
  * stages — a decode step's q|k|v, o, gate|up and down for every transformer
  * layer — run by ONE persistent launch, one workgroup per compute unit.  The

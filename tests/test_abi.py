@@ -43,7 +43,7 @@ def test_every_declared_symbol_is_exported(lib):
 
 
 def test_abi_version(lib):
-    assert lib.eptq_abi_version() == 1
+    assert lib.eptq_abi_version() == 2
     assert lib.eptq_last_error() is not None
 
 
@@ -162,3 +162,16 @@ def test_fused_llama_linears_validate_arguments(lib):
     assert h(16, None, 16, 1e-5, 16, 100, 4096, 1, 16, 16, None, 20, None) == 1            # work misaligned
     assert h(16, None, 16, 1e-5, 16, 100, 4096, 9, 16, 16, None, 16, None) == 2            # B > 8
     assert h(16, None, 16, 1e-5, 16, 100, 1000, 1, 16, 16, None, 16, None) == 2            # hidden size
+
+
+def test_noalloc_rejects_more_tiles_than_its_scratch_counts(lib):
+    """The allocation-free variant's scratch holds 16384 tile counters (64
+    output rows each); a call over more rows is refused before any device
+    call, with the limit in the message."""
+    L = _lib.EptqLayer
+    four = (L * 4)(*([L(16, 16, 16, None, None, 16, None, None, 0, 32769, 0)] * 4))   # 4 x 4097 tiles
+    rc = lib.eptq_e8d4_forward_multi_noalloc(4, four, 16, _lib.EPTQ_F16, 16, _lib.EPTQ_F16, 64, 1, 16,
+                                             8 * 32769, None)
+    assert rc == _lib.EPTQ_EUNSUPPORTED
+    msg = lib.eptq_last_error().decode()
+    assert "tile counters" in msg and "1048576 output rows" in msg
