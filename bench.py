@@ -41,9 +41,14 @@ JSON fields beyond the driver contract:
 * ``dequant`` — the bit-exact dequantizer (``eptq_e8d4_dequant``, fp16 W of
   ``dequantize_layer``) on the Llama-2-7B shapes: algorithmic GB/s (index
   and scale reads plus the W write) and fraction of HBM peak.
+* ``config0`` — benchmark configuration 0, the E8-lattice Linear at OPT-125m
+  fc1 shape (3072x768) with bias at batch 1: microseconds per launch over
+  distinct copies, algorithmic GB/s and fraction of HBM peak.
 * ``cpu_baseline`` — the reference CPU path (per-column ``dequantize_layer``
-  restatement + fp32 ``torch.matmul``) on one decoder layer's seven Linears at
-  batch 1, timed on this host's cores.
+  restatement + fp32 ``torch.matmul``) on a 4096x4096 and an 11008x4096
+  Linear at batch 1, dequant and matmul timed separately (median of 5), on
+  this host's cores.  ``--cpu-configs`` adds ``cpu_configs``: the same
+  per layer and batch of configurations 0-3.
 """
 
 from __future__ import annotations
@@ -277,38 +282,106 @@ def measure_traffic(args):
 # Side measurements
 # ---------------------------------------------------------------------------
 
-def cpu_baseline(seed=1000):
-    """Reference CPU path on one Llama-2-7B decoder layer's seven Linears at
-    B=1: per-column dequantize_layer restatement (algorithms/eptq.py:406-471)
-    followed by an fp32 torch.matmul, per Linear."""
+def _cpu_threads():
     import torch
-    from eptq_amd.quantizers import E8D4Quantizer
-    from eptq_amd.synthetic import make_layer, make_x
-    from oracle.dequant import dequantize_layer_torch_loop
-
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
-    tab = E8D4Quantizer(radius=1.75).flat_table().numpy()
-    work = []
-    for idx, (name, out, inp) in enumerate(LLAMA2_7B):
-        qd = make_layer(out, inp, seed=seed + idx, percmask=0.001)
-        work.append((qd, make_x(1, inp, seed=seed + 100 + idx), algo_bytes(out, inp, 1, qd.O.shape[0])))
-    total_bytes = sum(w[2] for w in work)
-    times = []
-    for _ in range(3):
+    return torch.get_num_threads()
+
+
+def _median_runs(fn, runs=5):
+    """Wall-clock seconds of ``fn``: one warmup call, then the median of ``runs``."""
+    fn()
+    ts = []
+    for _ in range(runs):
         t0 = time.perf_counter()
-        for qd, x, _ in work:
-            W = dequantize_layer_torch_loop(qd.Q.numpy(), qd.g.numpy(), qd.h.numpy(), qd.O.numpy(),
-                                            tab, "e8_d4")
-            y = torch.matmul(x.float(), W.float().T)
-        times.append(time.perf_counter() - t0)
-    del y
-    t = min(times)
-    return {"value": round(total_bytes / t / 1e9, 6), "unit": "GB/s", "cores": torch.get_num_threads(),
-            "kind": "port",
-            "sample": f"one Llama-2-7B decoder layer (q,k,v,o,gate,up,down; E8-D4 r=1.75, p=0.001) "
-                      f"at B=1: per-column dequantize_layer + fp32 torch.matmul per Linear, "
-                      f"best of 3 = {t:.2f} s for {total_bytes} algorithmic bytes"}
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return statistics.median(ts)
+
+
+def _cpu_dequant_matmul(qd, xs, kind, tab, runs=5):
+    """Reference CPU path on one layer: seconds of the per-column
+    ``dequantize_layer`` restatement (algorithms/eptq.py:406-471) and, for
+    each x of ``xs``, of y = x.float() @ W.float().T (+ bias); each the
+    median of ``runs`` after one warmup."""
+    import torch
+    from oracle.dequant import dequantize_layer_torch_loop
+    S = None if qd.S_group is None else qd.S_group.numpy()
+    args = (qd.Q.numpy(), qd.g.numpy(), qd.h.numpy(), qd.O.numpy(), tab, kind, S)
+    t_dq = _median_runs(lambda: dequantize_layer_torch_loop(*args), runs)
+    Wf = dequantize_layer_torch_loop(*args).float()
+    bf = None if qd.bias is None else qd.bias.float()
+    t_mm = []
+    for x in xs:
+        xf = x.float()
+
+        def mm():
+            y = torch.matmul(xf, Wf.T)
+            return y if bf is None else y + bf
+        t_mm.append(_median_runs(mm, runs))
+    return t_dq, t_mm
+
+
+def cpu_baseline(seed=1000, runs=5):
+    """Reference CPU path (per-column ``dequantize_layer`` restatement +
+    fp32 ``torch.matmul``) on a bounded sample of the benchmark workload: a
+    q/k/v/o-shaped (4096x4096) and a gate/up-shaped (11008x4096) Linear of
+    Llama-2-7B at batch 1, on all of this host's cores (about 20 s)."""
+    from eptq_amd.quantizers import E8D4Quantizer
+    from eptq_amd.synthetic import make_layer, make_x
+
+    cores = _cpu_threads()
+    tab = E8D4Quantizer(radius=1.75).flat_table().numpy()
+    t_dq = t_mm = 0.0
+    nbytes = 0
+    for idx, (out, inp) in enumerate(((4096, 4096), (11008, 4096))):
+        qd = make_layer(out, inp, seed=seed + idx, percmask=0.001)
+        a, b = _cpu_dequant_matmul(qd, [make_x(1, inp, seed=seed + 100 + idx)], "e8_d4", tab, runs)
+        t_dq, t_mm = t_dq + a, t_mm + b[0]
+        nbytes += algo_bytes(out, inp, 1, int(qd.O.shape[0]))
+    t = t_dq + t_mm
+    return {"value": round(nbytes / t / 1e9, 6), "unit": "GB/s", "cores": cores, "kind": "port",
+            "dequant_s": round(t_dq, 4), "matmul_s": round(t_mm, 5),
+            "sample": f"a 4096x4096 and an 11008x4096 Llama-2-7B Linear (E8-D4 r=1.75, p=0.001) at B=1: "
+                      f"per-column dequantize_layer restatement, then fp32 torch.matmul, each timed "
+                      f"separately, median of {runs} after one warmup; {t:.2f} s for {nbytes} algorithmic bytes"}
+
+
+def cpu_configs(seed=2000, runs=5):
+    """The reference CPU path per layer and batch of benchmark configurations
+    0-3 (BASELINE's CPU plan): dequant and matmul timed separately, median of
+    ``runs`` after one warmup, all host cores."""
+    from eptq_amd.quantizers import E8D4Quantizer, E8LatticeQuantizer
+    from eptq_amd.synthetic import make_layer, make_x
+
+    cores = _cpu_threads()
+    e8d4 = E8D4Quantizer(radius=1.75).flat_table().numpy()
+    e8 = E8LatticeQuantizer(radius=1.6).flat_table().numpy()
+    cases = [("0", "e8_lattice", e8, 3072, 768, None, 0.002, True, (1,))]
+    cases += [("1", "e8_d4", e8d4, o, i, None, 0.001, False, (1, 8))
+              for o, i in ((4096, 4096), (11008, 4096), (4096, 11008))]
+    cases += [("2", "e8_d4", e8d4, o, i, LLAMA3_8B_QB, 0.002, False, (1, 4, 16))
+              for o, i in ((4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336))]
+    cases += [("3", "e8_d4", e8d4, o, i, None, 0.002, False, (2048,)) for _, o, i in LLAMA2_13B]
+    rows = []
+    for k, (cfg, kind, tab, out, inp, qb, p, bias, batches) in enumerate(cases):
+        qd = make_layer(out, inp, seed=seed + k, percmask=p, qb_size=qb, bias=bias)
+        nnz = int(qd.O.shape[0])
+        ng = 0 if qd.S_group is None else int(qd.S_group.shape[0])
+        t_dq, t_mms = _cpu_dequant_matmul(qd, [make_x(B, inp, seed=seed + 50 + B) for B in batches], kind, tab,
+                                          runs)
+        for B, t_mm in zip(batches, t_mms):
+            row = {"config": cfg, "shape": f"{out}x{inp}", "B": B, "dequant_s": round(t_dq, 4),
+                   "matmul_s": round(t_mm, 5), "total_s": round(t_dq + t_mm, 4)}
+            if cfg == "3":
+                row["tflops"] = round(2.0 * B * out * inp / (t_dq + t_mm) / 1e12, 4)
+            else:
+                row["gbs"] = round(algo_bytes(out, inp, B, nnz, bias=bias, n_groups=ng) / (t_dq + t_mm) / 1e9, 6)
+            rows.append(row)
+            print(f"# cpu config {cfg} {out}x{inp} B={B}: dequant {t_dq:.3f} s, matmul {t_mm * 1e3:.2f} ms",
+                  file=sys.stderr, flush=True)
+    return {"cores": cores, "kind": "port", "runs": runs, "rows": rows}
 
 
 def e2e_decode(torch, dev, batches=(1, 8), new_tokens=256, prompt_len=128):
@@ -354,13 +427,13 @@ def e2e_decode(torch, dev, batches=(1, 8), new_tokens=256, prompt_len=128):
 LLAMA3_8B_QB = 128
 
 
-def decode_batches(torch, dev, stream_bytes=320 << 20):
+def decode_batches(torch, dev, stream_bytes=576 << 20):
     """Decode-step Linear units at the batch sizes of configurations 1 and 2:
     synthetic Llama-2-7B (B = 1, 8) and Llama-3-8B with S_group qb=128
     (B = 1, 4, 16).  Each unit is one eptq_e8d4_forward_multi launch with the
     decode workspace (q|k|v and gate|up as multi-layer launches).  Every unit
     is built as enough distinct copies (different seeds) to exceed
-    ``stream_bytes`` of indices, more than the 256 MB MALL, and the copies are
+    ``stream_bytes`` of indices (over 512 MB, twice the 256 MB MALL), and the copies are
     launched back to back with HIP events around the whole group, as a decode
     step streams distinct layers.  B = 1..4 run the vector decode kernel,
     5..16 the matrix-core one."""
@@ -434,6 +507,49 @@ def decode_batches(torch, dev, stream_bytes=320 << 20):
                    "back (median of 3); gbs = algorithmic bytes (indices, S_group, CSR, scales, x, y) / time"
                    % (stream_bytes >> 20))
     return out
+
+
+def config0(torch, dev, copies=1024, reps=3):
+    """Benchmark configuration 0: the E8-lattice Linear at OPT-125m fc1 shape
+    (out 3072, in 768) with bias, batch 1, radius 1.6, 0.2% critical blocks.
+    ``copies`` distinct layers (over 512 MB of indices, past the MALL) are
+    launched back to back through ``eptq_e8_forward`` with HIP events around
+    the group and the queue backed up by a device sleep; microseconds per
+    launch, algorithmic GB/s and fraction of HBM peak.  The layer is small
+    enough that the launch's fixed cost dominates."""
+    from eptq_amd.kernels import _lib
+    from eptq_amd.quantizers import E8LatticeQuantizer
+    from eptq_amd.synthetic import make_layer, make_x
+
+    codes = E8LatticeQuantizer(radius=1.6).flat_table().half().to(dev)
+    out_f, in_f = 3072, 768
+    stream = torch.cuda.current_stream()
+    x = make_x(1, in_f, seed=9, device=dev)
+    y = torch.empty((1, out_f), dtype=torch.float16, device=dev)
+    layers = []
+    for c in range(copies):
+        qd = make_layer(out_f, in_f, seed=9000 + c, percmask=0.002, bias=True, device=dev)
+        rows, cols = (qd.Q == 32767).nonzero(as_tuple=True)
+        rp = torch.cat([torch.zeros(1, dtype=torch.int32, device=dev),
+                        torch.bincount(rows, minlength=qd.Q.shape[0]).cumsum(0).to(torch.int32)])
+        layers.append((qd, cols.to(torch.int32), rp))
+
+    def f():
+        for qd, oc, rp in layers:
+            _lib.forward_into("e8_lattice", qd.Q, codes, qd.g, qd.h, x, qd.O, oc, rp, qd.bias, None,
+                              y, stream.cuda_stream)
+    f()
+    d, backed = event_timed(torch, [f] * reps, stream)
+    us = statistics.median(d) * 1e3 / copies
+    nbytes = statistics.mean(algo_bytes(out_f, in_f, 1, int(qd.O.shape[0]), bias=True) for qd, _, _ in layers)
+    gbs = nbytes / (us * 1e-6) / 1e9
+    res = {"shape": f"{out_f}x{in_f}", "B": 1, "codebook": "e8_lattice", "radius": 1.6, "percmask": 0.002,
+           "bias": True, "us": round(us, 3), "gbs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+           "algorithmic_bytes": round(nbytes), "kernel": "k_matvec<E8>", "copies": copies,
+           "events_backed_up": backed}
+    del layers
+    torch.cuda.empty_cache()
+    return res
 
 
 def dequant_layers(torch, dev, reps=10):
@@ -522,6 +638,9 @@ def main():
     ap.add_argument("--no-batches", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-dequant", action="store_true")
+    ap.add_argument("--no-config0", action="store_true")
+    ap.add_argument("--cpu-configs", action="store_true",
+                    help="also time the reference CPU path per layer and batch of configurations 0-3 (minutes)")
     ap.add_argument("--pmc-timeout", type=int, default=240)
     ap.add_argument("--probe-traffic", action="store_true", help=argparse.SUPPRESS)
     args = ap.parse_args()
@@ -666,8 +785,13 @@ def main():
     if not args.no_dequant:
         rec["dequant"] = dequant_layers(torch, dev)
         print(f"# dequant: {rec['dequant']}", file=sys.stderr, flush=True)
+    if not args.no_config0:
+        rec["config0"] = config0(torch, dev)
+        print(f"# config0: {rec['config0']}", file=sys.stderr, flush=True)
     if not args.no_cpu_baseline:
         rec["cpu_baseline"] = cpu_baseline()
+    if args.cpu_configs:
+        rec["cpu_configs"] = cpu_configs()
     print(json.dumps(rec), flush=True)
 
 
