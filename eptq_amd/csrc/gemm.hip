@@ -2,8 +2,14 @@
 //
 // Counterpart of the reference's large-batch path e8d4_wmma_v2_kernel +
 // at::mul(x, h) (csrc/eptq_kernels.cu:309-461, :520-537), rebuilt for gfx950
-// MFMA.  The contraction is a genuine dense GEMM, so the quantized weight is
-// dequantized tile by tile into LDS and fed to v_mfma_f32_16x16x32_f16.
+// MFMA.  The contraction is a genuine dense GEMM on v_mfma_f32_16x16x32_f16.
+// Two kernels:
+//  * k_gemm_rows_e8d4 (E8-D4 without S_group, the Llama prefill case): each
+//    wave decodes its 64 rows of the weight straight into MFMA A operands in
+//    registers and the workgroup shares an activation tile in LDS (its own
+//    comment below);
+//  * k_gemm_e8d4 / k_gemm_e8 (S_group layers, E8, shapes the first does not
+//    take): the weight is dequantized tile by tile into LDS, as below.
 //
 // E8 layers (1 MB table, larger than LDS) gather each index's 16-byte table
 // row from global memory (L2-resident after first use) one K-step ahead,
@@ -31,8 +37,11 @@
 // (Entries beyond the LDS cap, only in very dense layers, are added after the
 // loop from global memory.)  The output is g ⊙ acc + bias, written as fp16.
 
+#include <stdlib.h>
+
 #include "common.h"
 #include "kernels.h"
+#include "mfma_decode.h"
 
 namespace eptq {
 
@@ -353,6 +362,222 @@ __device__ __forceinline__ void gemm_tile(const LinearArgs& a, int OB) {
   }
 }
 
+
+// ---------------------------------------------------------------------------
+// E8-D4 prefill GEMM with the weights decoded in registers (no S_group).
+//
+// A workgroup (kW waves) computes 64·kW output features × 128 tokens; each
+// wave owns 64 features (8 Q-rows) for all 128 tokens.  Per K-step of 32
+// columns a lane decodes its 8 indices straight into v_mfma_f32_16x16x32_f16
+// A operands (the matrix-core decode matvec's mapping: 8 table lookups, 16
+// byte permutes, no lane exchange) and reuses them for the 8 MFMA token
+// tiles, so the decoded weight never goes through LDS.  The B operands are
+// the shared activation tile fp16(x · h·2^-e) in LDS (tokens × 32 columns,
+// double-buffered, written once per step by the whole workgroup; h lives on
+// the activation side, as in the reference's at::mul(x, h) before its WMMA
+// GEMM, csrc/eptq_kernels.cu:520-537), with 2^-e a workgroup-uniform power
+// of two that keeps |x·h·2^-e| <= |x|.  A critical block replaces the
+// lane's four looked-up values with its O values in registers: each lane
+// walks its Q-row's CSR entries (staged in LDS) with a cursor, so the MFMA
+// result needs no correction.  D of MFMA c, token tile j, lane (n, lg),
+// element v is feature 16·lg + 4v + c of the wave's 64 for token 16j + n, so
+// a lane stores 16 consecutive features of one token.
+namespace g2 {
+constexpr int kTok = 128;                  // tokens per workgroup
+constexpr int kJ = kTok / 16;              // MFMA token tiles per wave
+constexpr int kBK = 32;                    // input columns per K-step
+constexpr int kXLd = kBK + 8;              // activation tile row stride in halves (80 bytes)
+constexpr int kEnt = 512;                  // critical blocks staged in LDS per workgroup
+constexpr int kPF = 2;                     // K-steps of indices in flight per lane
+
+__host__ __device__ inline size_t dyn_bytes(int N) { return (size_t)N * 2; }
+}  // namespace g2
+
+template <int kW>
+__global__ __launch_bounds__(64 * kW, 8 / kW) void k_gemm_rows_e8d4(LinearArgs a, int OB) {
+  constexpr int kT = 64 * kW, kQR = 8 * kW;
+  constexpr int kTok = g2::kTok, kJ = g2::kJ, kBK = g2::kBK;
+  constexpr int kXLd = g2::kXLd, kEnt = g2::kEnt, kPF = g2::kPF;
+  constexpr int kXCH = kTok * kBK / 8;   // 16-byte activation chunks per K-step
+  __shared__ f16x4 tab[512];
+  __shared__ __attribute__((aligned(16))) uint16_t Xs[2][kTok][kXLd];
+  __shared__ int ecol[kEnt];
+  __shared__ __attribute__((aligned(16))) u32x4 eov[kEnt];
+  __shared__ int rps[kQR + 1];
+  __shared__ float wmx[kW];
+  extern __shared__ __attribute__((aligned(16))) char dyn[];
+  uint16_t* const hs = (uint16_t*)dyn;   // fp16(h·2^-e), N entries
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int N = a.N, T = a.B, ldx = a.ldx;
+  const int ob = (int)blockIdx.x % OB, tb = (int)blockIdx.x / OB;
+  const int m0 = ob * kQR;      // first Q-row (the launcher requires M % kQR == 0)
+  const int t0 = tb * kTok;     // first token
+  const int nsteps = N / kBK, nch = N / 8;
+
+  // ---- table, h (max |h|), CSR row pointers ----
+  constexpr int kTabP = (512 + kT - 1) / kT;
+  f16x4 tl[kTabP];
+#pragma unroll
+  for (int p = 0; p < kTabP; ++p)
+    if (tid + kT * p < 512) tl[p] = ((const f16x4*)a.codes)[tid + kT * p];
+  if (tid <= kQR) rps[tid] = a.O_row_ptr[m0 + tid];
+  float mx = 0.0f;
+  for (int c = tid; c < nch; c += kT) {
+    const u32x4 hv = ((const u32x4*)a.h)[c];
+    *(u32x4*)(hs + 8 * c) = hv;
+    const f16x8 hf = __builtin_bit_cast(f16x8, hv);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) mx = fmaxf(mx, fabsf((float)hf[e]));
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+  if (lane == 0) wmx[wave] = mx;
+#pragma unroll
+  for (int p = 0; p < kTabP; ++p)
+    if (tid + kT * p < 512) tab[(tid + kT * p) ^ 0x100] = tl[p];
+  __syncthreads();
+  mx = wmx[0];
+#pragma unroll
+  for (int w = 1; w < kW; ++w) mx = fmaxf(mx, wmx[w]);
+  int ex = 0;
+  if (mx > 1.0f) ex = (int)((__builtin_bit_cast(uint32_t, mx) >> 23) & 0xff) - 126;   // 2^ex >= mx
+  const float out_scale = __builtin_ldexpf(1.0f, ex);
+  const f16 down = (f16)__builtin_ldexpf(1.0f, -ex);
+  const uint32_t down2 = __builtin_bit_cast(uint32_t, (h2){down, down});
+  for (int c = tid; c < nch; c += kT) {   // the chunks this thread wrote
+    u32x4 hv = *(const u32x4*)(hs + 8 * c);
+#pragma unroll
+    for (int d = 0; d < 4; ++d) hv[d] = gpk_mul(hv[d], down2);
+    *(u32x4*)(hs + 8 * c) = hv;
+  }
+  const int e0 = rps[0];
+  const int nst = rps[kQR] - e0 < kEnt ? rps[kQR] - e0 : kEnt;
+  for (int e = tid; e < nst; e += kT) {
+    ecol[e] = a.O_col[e0 + e];
+    eov[e] = ((const u32x4*)a.O)[e0 + e];
+  }
+
+  // ---- per-lane roles ----
+  const int i = lane & 15, kg = lane >> 4;
+  const mdec::Half half(i);
+  const int hsel = i & 1;
+  const int lq = 8 * wave + (i >> 1);                          // this lane's Q-row in the workgroup
+  const int16_t* __restrict__ qp = a.Q + (size_t)(m0 + lq) * N + 8 * kg;
+  u32x4 qv[kPF];
+#pragma unroll
+  for (int p = 0; p < kPF; ++p) qv[p] = *(const u32x4*)(qp + (p < nsteps ? p : 0) * kBK);
+  // Activation chunks: chunk c = tid + kT·p is token c/4, columns 8(c%4)..+7.
+  constexpr int kXC = (kXCH + kT - 1) / kT;   // chunks per thread (the last pass partial for kW = 5)
+  static_assert(kPF % 2 == 0, "activation slots follow the step parity");
+  u32x4 xr[2][kXC];   // activation loads two K-steps ahead (slot = step parity)
+  auto load_x = [&](int st, int slot) {
+#pragma unroll
+    for (int p = 0; p < kXC; ++p) {
+      const int c = tid + kT * p;
+      if (kXCH % kT != 0 && c >= kXCH) break;
+      const int tt = t0 + (c >> 2);
+      xr[slot][p] = *(const u32x4*)(a.x + (size_t)(tt < T ? tt : T - 1) * ldx + st * kBK + 8 * (c & 3));
+    }
+  };
+  auto store_x = [&](int buf, int st, int slot) {
+#pragma unroll
+    for (int p = 0; p < kXC; ++p) {
+      const int c = tid + kT * p;
+      if (kXCH % kT != 0 && c >= kXCH) break;
+      const u32x4 hv = *(const u32x4*)(hs + st * kBK + 8 * (c & 3));
+      u32x4 v;
+#pragma unroll
+      for (int d = 0; d < 4; ++d) v[d] = gpk_mul(xr[slot][p][d], hv[d]);
+      *(u32x4*)&Xs[buf][c >> 2][8 * (c & 3)] = v;
+    }
+  };
+  load_x(0, 0);
+  __syncthreads();   // hs scaled, entries staged
+  int ec = rps[lq] - e0;
+  const int ee = rps[lq + 1] - e0;
+  auto col_of = [&](int e) { return e < kEnt ? ecol[e] : a.O_col[e0 + e]; };
+  int ncol = ec < ee ? col_of(ec) : 0x7fffffff;
+  if (nsteps > 1) load_x(1, 1);
+  store_x(0, 0, 0);
+  if (nsteps > 2) load_x(2, 0);
+  __syncthreads();
+
+  f32x4 acc[4][kJ];
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+#pragma unroll
+    for (int j = 0; j < kJ; ++j) acc[c][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  const char* __restrict__ tabB = (const char*)tab;
+
+  for (int s0 = 0; s0 < nsteps; s0 += kPF) {
+#pragma unroll
+    for (int p = 0; p < kPF; ++p) {
+      const int s = s0 + p;
+      if (s >= nsteps) break;
+      const int buf = s & 1;
+      u32x2 lo[4], hi[4];
+      half.lookup(qv[p], tabB, lo, hi);
+      if (s + kPF < nsteps) qv[p] = *(const u32x4*)(qp + (s + kPF) * kBK);
+      u32x4 bf[kJ];
+#pragma unroll
+      for (int j = 0; j < kJ; ++j) bf[j] = *(const u32x4*)&Xs[buf][16 * j + i][8 * kg];
+      // Critical blocks in this lane's 8 columns take the table values' place.
+      const int klo = s * kBK + 8 * kg;
+      while (ncol < klo + 8) {
+        if (ncol >= klo) {
+          const u32x4 o = ec < kEnt ? eov[ec] : ((const u32x4*)a.O)[e0 + ec];
+          const u32x2 oh = hsel ? (u32x2){o[2], o[3]} : (u32x2){o[0], o[1]};
+          const int jc = ncol - klo;
+#pragma unroll
+          for (int d = 0; d < 4; ++d) {
+            if (jc == 2 * d) lo[d] = oh;
+            if (jc == 2 * d + 1) hi[d] = oh;
+          }
+        }
+        ++ec;
+        ncol = ec < ee ? col_of(ec) : 0x7fffffff;
+      }
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const f16x8 aw = __builtin_bit_cast(f16x8, mdec::Half::operand(lo, hi, c));
+#pragma unroll
+        for (int j = 0; j < kJ; ++j)
+          acc[c][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aw, __builtin_bit_cast(f16x8, bf[j]), acc[c][j], 0, 0, 0);
+      }
+      if (s + 1 < nsteps) {   // kPF is even and s0 a multiple of it: slot (s + 1) & 1 = (p + 1) & 1
+        store_x(buf ^ 1, s + 1, (p + 1) & 1);
+        if (s + 3 < nsteps) load_x(s + 3, (p + 1) & 1);
+      }
+      __syncthreads();
+    }
+  }
+
+  // ---- epilogue: y = acc·2^e·g + bias, 16 consecutive features per lane and token ----
+  const int r0 = 8 * m0 + 64 * wave + 16 * kg;
+  const f16x8 g0 = *(const f16x8*)(a.g + r0), g1 = *(const f16x8*)(a.g + r0 + 8);
+  f16x8 b0 = {}, b1 = {};
+  if (a.bias) {
+    b0 = *(const f16x8*)(a.bias + r0);
+    b1 = *(const f16x8*)(a.bias + r0 + 8);
+  }
+#pragma unroll
+  for (int j = 0; j < kJ; ++j) {
+    const int tt = t0 + 16 * j + i;
+    if (tt >= T) continue;
+    f16x8 o0, o1;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      o0[q] = (f16)(acc[q & 3][j][q >> 2] * out_scale * (float)g0[q] + (float)b0[q]);
+      o1[q] = (f16)(acc[q & 3][j][2 + (q >> 2)] * out_scale * (float)g1[q] + (float)b1[q]);
+    }
+    f16* yp = (f16*)a.y + (size_t)tt * a.ldy + r0;
+    *(f16x8*)yp = o0;
+    *(f16x8*)(yp + 8) = o1;
+  }
+}
+
 template <bool HAS_S>
 __global__ __launch_bounds__(kGT, 2) void k_gemm_e8d4(LinearArgs a, int OB) {
   gemm_tile<KIND_E8D4, HAS_S>(a, OB);
@@ -382,6 +607,32 @@ int launch_gemm(const LinearArgs& a, hipStream_t s) {
   // of 32.  Anything else takes batch tiles of the decode matvec.
   const bool mfma_ok = !a.x_bf16 && !a.codes_f32 && (a.N % kBK) == 0 && (a.M % kBQ) == 0 &&
                        (!a.S || (a.qb % 8) == 0);
+  // Rows-in-registers kernel: no S_group, whole 32-Q-row workgroups, y
+  // stored 16 bytes at a time.
+  if (mfma_ok && KIND == KIND_E8D4 && !a.S && a.prep == 0 && (a.M % 32) == 0 && (a.ldy % 8) == 0 &&
+      ((uintptr_t)a.y & 15) == 0 && (a.ldx % 8) == 0) {
+    const int TB = (a.B + g2::kTok - 1) / g2::kTok;
+    const size_t dyn = g2::dyn_bytes(a.N);
+    // Five-wave workgroups (one per CU) when they cover the layer in one
+    // round of the device's CUs; else four-wave workgroups, two per CU.
+    const bool five = (a.M % 40) == 0 && (long)(a.M / 40) * TB <= dec::cu_count();
+    const int OB = five ? a.M / 40 : a.M / 32;
+    const long grid = (long)OB * TB;
+    if (grid <= 0x7fffffff && dyn <= 96 * 1024) {
+      const void* kern = five ? (const void*)k_gemm_rows_e8d4<5> : (const void*)k_gemm_rows_e8d4<4>;
+      static size_t attr[2] = {0, 0};
+      bool ok = true;
+      if (dyn > attr[five]) {
+        ok = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)dyn) == hipSuccess;
+        if (ok) attr[five] = dyn;
+      }
+      if (ok) {
+        if (five) k_gemm_rows_e8d4<5><<<(unsigned)grid, 320, dyn, s>>>(a, OB);
+        else k_gemm_rows_e8d4<4><<<(unsigned)grid, 256, dyn, s>>>(a, OB);
+        return 0;
+      }
+    }
+  }
   if (mfma_ok) {
     const int OB = a.M / kBQ;
     const int TB = (a.B + kBN - 1) / kBN;
