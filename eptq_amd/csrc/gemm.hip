@@ -387,7 +387,7 @@ constexpr int kTok = 128;                  // tokens per workgroup
 constexpr int kJ = kTok / 16;              // MFMA token tiles per wave
 constexpr int kBK = 32;                    // input columns per K-step
 constexpr int kXLd = kBK + 8;              // activation tile row stride in halves (80 bytes)
-constexpr int kEnt = 512;                  // critical blocks staged in LDS per workgroup
+constexpr int kEnt = 1024;                 // critical blocks staged in LDS per workgroup
 constexpr int kPF = 2;                     // K-steps of indices in flight per lane
 
 __host__ __device__ inline size_t dyn_bytes(int N) { return (size_t)N * 2; }
@@ -397,7 +397,10 @@ template <int kW>
 __global__ __launch_bounds__(64 * kW, 8 / kW) void k_gemm_rows_e8d4(LinearArgs a, int OB) {
   constexpr int kT = 64 * kW, kQR = 8 * kW;
   constexpr int kTok = g2::kTok, kJ = g2::kJ, kBK = g2::kBK;
-  constexpr int kXLd = g2::kXLd, kEnt = g2::kEnt, kPF = g2::kPF;
+  constexpr int kXLd = g2::kXLd, kPF = g2::kPF;
+  // Critical blocks staged in LDS: 0.2% of a five-wave workgroup's 40 rows
+  // of 13824 columns is ~1100 (one workgroup per CU leaves the LDS for it).
+  constexpr int kEnt = kW == 5 ? 2 * g2::kEnt : g2::kEnt;
   constexpr int kXCH = kTok * kBK / 8;   // 16-byte activation chunks per K-step
   __shared__ f16x4 tab[512];
   __shared__ __attribute__((aligned(16))) uint16_t Xs[2][kTok][kXLd];
@@ -467,18 +470,23 @@ __global__ __launch_bounds__(64 * kW, 8 / kW) void k_gemm_rows_e8d4(LinearArgs a
   const int16_t* __restrict__ qp = a.Q + (size_t)(m0 + lq) * N + 8 * kg;
   u32x4 qv[kPF];
 #pragma unroll
-  for (int p = 0; p < kPF; ++p) qv[p] = *(const u32x4*)(qp + (p < nsteps ? p : 0) * kBK);
+  for (int p = 0; p < kPF; ++p) qv[p] = *(const u32x4*)(qp + (p < nsteps ? p : nsteps - 1) * kBK);
   // Activation chunks: chunk c = tid + kT·p is token c/4, columns 8(c%4)..+7.
   constexpr int kXC = (kXCH + kT - 1) / kT;   // chunks per thread (the last pass partial for kW = 5)
   static_assert(kPF % 2 == 0, "activation slots follow the step parity");
   u32x4 xr[2][kXC];   // activation loads two K-steps ahead (slot = step parity)
+  // Every load is issued unconditionally (steps past the end and the partial
+  // last pass of a five-wave workgroup reload valid addresses and are never
+  // stored), so the compiler can count the loads in flight and wait for
+  // exactly the one it needs.
   auto load_x = [&](int st, int slot) {
+    const int stc = st < nsteps ? st : nsteps - 1;
 #pragma unroll
     for (int p = 0; p < kXC; ++p) {
-      const int c = tid + kT * p;
-      if (kXCH % kT != 0 && c >= kXCH) break;
+      const int c0 = tid + kT * p;
+      const int c = c0 < kXCH ? c0 : c0 - kT;
       const int tt = t0 + (c >> 2);
-      xr[slot][p] = *(const u32x4*)(a.x + (size_t)(tt < T ? tt : T - 1) * ldx + st * kBK + 8 * (c & 3));
+      xr[slot][p] = *(const u32x4*)(a.x + (size_t)(tt < T ? tt : T - 1) * ldx + stc * kBK + 8 * (c & 3));
     }
   };
   auto store_x = [&](int buf, int st, int slot) {
@@ -495,13 +503,9 @@ __global__ __launch_bounds__(64 * kW, 8 / kW) void k_gemm_rows_e8d4(LinearArgs a
   };
   load_x(0, 0);
   __syncthreads();   // hs scaled, entries staged
-  int ec = rps[lq] - e0;
-  const int ee = rps[lq + 1] - e0;
-  auto col_of = [&](int e) { return e < kEnt ? ecol[e] : a.O_col[e0 + e]; };
-  int ncol = ec < ee ? col_of(ec) : 0x7fffffff;
-  if (nsteps > 1) load_x(1, 1);
+  load_x(1, 1);
   store_x(0, 0, 0);
-  if (nsteps > 2) load_x(2, 0);
+  load_x(2, 0);
   __syncthreads();
 
   f32x4 acc[4][kJ];
@@ -511,6 +515,13 @@ __global__ __launch_bounds__(64 * kW, 8 / kW) void k_gemm_rows_e8d4(LinearArgs a
     for (int j = 0; j < kJ; ++j) acc[c][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
   const char* __restrict__ tabB = (const char*)tab;
 
+  // The cursor reads LDS only (a load from memory in the loop would make the
+  // compiler wait for every index and activation load in flight): entries
+  // past the stage keep the marker's table row in the loop and are
+  // corrected after it.
+  int ec = rps[lq] - e0;
+  const int ee = rps[lq + 1] - e0 < kEnt ? rps[lq + 1] - e0 : kEnt;
+  int ncol = ec < ee ? ecol[ec] : 0x7fffffff;
   for (int s0 = 0; s0 < nsteps; s0 += kPF) {
 #pragma unroll
     for (int p = 0; p < kPF; ++p) {
@@ -519,7 +530,7 @@ __global__ __launch_bounds__(64 * kW, 8 / kW) void k_gemm_rows_e8d4(LinearArgs a
       const int buf = s & 1;
       u32x2 lo[4], hi[4];
       half.lookup(qv[p], tabB, lo, hi);
-      if (s + kPF < nsteps) qv[p] = *(const u32x4*)(qp + (s + kPF) * kBK);
+      qv[p] = *(const u32x4*)(qp + (s + kPF < nsteps ? s + kPF : nsteps - 1) * kBK);
       u32x4 bf[kJ];
 #pragma unroll
       for (int j = 0; j < kJ; ++j) bf[j] = *(const u32x4*)&Xs[buf][16 * j + i][8 * kg];
@@ -527,7 +538,7 @@ __global__ __launch_bounds__(64 * kW, 8 / kW) void k_gemm_rows_e8d4(LinearArgs a
       const int klo = s * kBK + 8 * kg;
       while (ncol < klo + 8) {
         if (ncol >= klo) {
-          const u32x4 o = ec < kEnt ? eov[ec] : ((const u32x4*)a.O)[e0 + ec];
+          const u32x4 o = eov[ec];
           const u32x2 oh = hsel ? (u32x2){o[2], o[3]} : (u32x2){o[0], o[1]};
           const int jc = ncol - klo;
 #pragma unroll
@@ -537,7 +548,7 @@ __global__ __launch_bounds__(64 * kW, 8 / kW) void k_gemm_rows_e8d4(LinearArgs a
           }
         }
         ++ec;
-        ncol = ec < ee ? col_of(ec) : 0x7fffffff;
+        ncol = ec < ee ? ecol[ec] : 0x7fffffff;
       }
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
@@ -546,11 +557,44 @@ __global__ __launch_bounds__(64 * kW, 8 / kW) void k_gemm_rows_e8d4(LinearArgs a
         for (int j = 0; j < kJ; ++j)
           acc[c][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aw, __builtin_bit_cast(f16x8, bf[j]), acc[c][j], 0, 0, 0);
       }
-      if (s + 1 < nsteps) {   // kPF is even and s0 a multiple of it: slot (s + 1) & 1 = (p + 1) & 1
-        store_x(buf ^ 1, s + 1, (p + 1) & 1);
-        if (s + 3 < nsteps) load_x(s + 3, (p + 1) & 1);
-      }
+      // kPF is even and s0 a multiple of it: slot (s + 1) & 1 = (p + 1) & 1.
+      if (s + 1 < nsteps) store_x(buf ^ 1, s + 1, (p + 1) & 1);
+      load_x(s + 3, (p + 1) & 1);
       __syncthreads();
+    }
+  }
+
+  // Entries past the LDS stage (dense critical blocks only): the loop
+  // multiplied table row 511 by fp16(x·h·2^-e) at their columns; add
+  // (O - row 511) times the same operand.  Lane group kg holds Q-rows
+  // 2kg, 2kg + 1 of the wave (features 16kg .. 16kg + 15).
+  if (rps[kQR] - e0 > kEnt) {
+    const f16x4 t5 = tab[511 ^ 0x100];
+#pragma unroll
+    for (int qq = 0; qq < 8; ++qq) {
+      if ((qq >> 1) != kg) continue;
+      const int lqq = 8 * wave + qq;
+      const int elo = rps[lqq] - e0 > kEnt ? rps[lqq] - e0 : kEnt;
+      const int ehi = rps[lqq + 1] - e0;
+      for (int e = elo; e < ehi; ++e) {
+        const int col = a.O_col[e0 + e];
+        const f16x8 o = ((const f16x8*)a.O)[e0 + e];
+        const f16 hc = __builtin_bit_cast(f16, hs[col]);
+        float dv[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) dv[k] = (float)o[k] - (float)t5[k & 3];
+#pragma unroll
+        for (int j = 0; j < kJ; ++j) {
+          const int tt = t0 + 16 * j + i;
+          const f16 xv = __builtin_bit_cast(f16, a.x[(size_t)(tt < T ? tt : T - 1) * ldx + col]);
+          const float xh = (float)(f16)(xv * hc);
+#pragma unroll
+          for (int k = 0; k < 8; ++k) {
+            const int r = 8 * (qq & 1) + k;   // this lane's feature index 4v + c
+            acc[r & 3][j][r >> 2] += dv[k] * xh;
+          }
+        }
+      }
     }
   }
 

@@ -1,14 +1,16 @@
 """GPU parity of the prefill GEMM with the weights decoded in registers
 (``k_gemm_rows_e8d4``: E8-D4, fp16, no S_group, more than 128 tokens,
 out_features a multiple of 256; four-wave workgroups of 256 features, or
-five-wave ones of 320 when the layer fits one round of the CUs) through the C ABI's ``eptq_e8d4_forward``.
+five-wave ones of 320 when the layer fits one round of the CUs) through the
+C ABI's ``eptq_e8d4_forward``.
 
 Every case is within 1e-2 relative L2 of the fp32 reconstruct + matmul
 oracle (``dequantize_layer`` W, then an fp32 product).  The cases cover
 token counts that are not a multiple of the 128-token tile, a bias, an odd
-number of 32-column K-steps (1056 = 33 x 32), rows whose
-critical blocks exceed the 512 entries a workgroup stages in LDS (the cursor
-then reads the rest from memory), and a layer with no critical block at all.
+number of 32-column K-steps (1056 = 33 x 32), workgroups whose critical
+blocks exceed the entries they stage in LDS (1024 for four-wave, 2048 for
+five-wave workgroups; the rest are corrected after the K loop), and a layer
+with no critical block at all.
 """
 
 from __future__ import annotations
@@ -35,6 +37,7 @@ CASES = [
     (256, 4096, 129, 0.0, True),       # no critical blocks
     (2048, 1024, 640, 0.01, False),
     (640, 1024, 300, 0.01, True),      # five-wave workgroups (80 Q-rows: two of 40)
+    (640, 1024, 200, 0.1, False),      # five-wave, ~4000 entries per workgroup: past its 2048 in LDS
 ]
 
 
