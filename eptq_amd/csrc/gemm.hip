@@ -393,7 +393,10 @@ constexpr int kPF = 2;                     // K-steps of indices in flight per l
 __host__ __device__ inline size_t dyn_bytes(int N) { return (size_t)N * 2; }
 }  // namespace g2
 
-template <int kW>
+// kBF: bf16 x and y (the activation operand is still fp16(x·h·2^-e), from
+// the exact fp32 product; the reference casts bf16 x to fp16 for its GEMM,
+// kernels/linear.py:200-203).
+template <int kW, bool kBF>
 __global__ __launch_bounds__(64 * kW, 8 / kW) void k_gemm_rows_e8d4(LinearArgs a, int OB) {
   constexpr int kT = 64 * kW, kQR = 8 * kW;
   constexpr int kTok = g2::kTok, kJ = g2::kJ, kBK = g2::kBK;
@@ -496,8 +499,17 @@ __global__ __launch_bounds__(64 * kW, 8 / kW) void k_gemm_rows_e8d4(LinearArgs a
       if (kXCH % kT != 0 && c >= kXCH) break;
       const u32x4 hv = *(const u32x4*)(hs + st * kBK + 8 * (c & 3));
       u32x4 v;
+      if constexpr (kBF) {
+        const f16x8 hf = __builtin_bit_cast(f16x8, hv);
+        const u16x8 xb = __builtin_bit_cast(u16x8, xr[slot][p]);
+        f16x8 o;
 #pragma unroll
-      for (int d = 0; d < 4; ++d) v[d] = gpk_mul(xr[slot][p][d], hv[d]);
+        for (int e = 0; e < 8; ++e) o[e] = (f16)(Act<bf16>::to_f32(xb[e]) * (float)hf[e]);
+        v = __builtin_bit_cast(u32x4, o);
+      } else {
+#pragma unroll
+        for (int d = 0; d < 4; ++d) v[d] = gpk_mul(xr[slot][p][d], hv[d]);
+      }
       *(u32x4*)&Xs[buf][c >> 2][8 * (c & 3)] = v;
     }
   };
@@ -586,8 +598,10 @@ __global__ __launch_bounds__(64 * kW, 8 / kW) void k_gemm_rows_e8d4(LinearArgs a
 #pragma unroll
         for (int j = 0; j < kJ; ++j) {
           const int tt = t0 + 16 * j + i;
-          const f16 xv = __builtin_bit_cast(f16, a.x[(size_t)(tt < T ? tt : T - 1) * ldx + col]);
-          const float xh = (float)(f16)(xv * hc);
+          const uint16_t xw = a.x[(size_t)(tt < T ? tt : T - 1) * ldx + col];
+          float xh;
+          if constexpr (kBF) xh = (float)(f16)(Act<bf16>::to_f32(xw) * (float)hc);
+          else xh = (float)(f16)(__builtin_bit_cast(f16, xw) * hc);
 #pragma unroll
           for (int k = 0; k < 8; ++k) {
             const int r = 8 * (qq & 1) + k;   // this lane's feature index 4v + c
@@ -610,15 +624,22 @@ __global__ __launch_bounds__(64 * kW, 8 / kW) void k_gemm_rows_e8d4(LinearArgs a
   for (int j = 0; j < kJ; ++j) {
     const int tt = t0 + 16 * j + i;
     if (tt >= T) continue;
-    f16x8 o0, o1;
+    u16x8 o0, o1;
 #pragma unroll
     for (int q = 0; q < 8; ++q) {
-      o0[q] = (f16)(acc[q & 3][j][q >> 2] * out_scale * (float)g0[q] + (float)b0[q]);
-      o1[q] = (f16)(acc[q & 3][j][2 + (q >> 2)] * out_scale * (float)g1[q] + (float)b1[q]);
+      const float y0 = acc[q & 3][j][q >> 2] * out_scale * (float)g0[q] + (float)b0[q];
+      const float y1 = acc[q & 3][j][2 + (q >> 2)] * out_scale * (float)g1[q] + (float)b1[q];
+      if constexpr (kBF) {
+        o0[q] = Act<bf16>::from_f32(y0);
+        o1[q] = Act<bf16>::from_f32(y1);
+      } else {
+        o0[q] = Act<f16>::from_f32(y0);
+        o1[q] = Act<f16>::from_f32(y1);
+      }
     }
-    f16* yp = (f16*)a.y + (size_t)tt * a.ldy + r0;
-    *(f16x8*)yp = o0;
-    *(f16x8*)(yp + 8) = o1;
+    uint16_t* yp = a.y + (size_t)tt * a.ldy + r0;
+    *(u16x8*)yp = o0;
+    *(u16x8*)(yp + 8) = o1;
   }
 }
 
@@ -652,9 +673,10 @@ int launch_gemm(const LinearArgs& a, hipStream_t s) {
   const bool mfma_ok = !a.x_bf16 && !a.codes_f32 && (a.N % kBK) == 0 && (a.M % kBQ) == 0 &&
                        (!a.S || (a.qb % 8) == 0);
   // Rows-in-registers kernel: no S_group, whole 32-Q-row workgroups, y
-  // stored 16 bytes at a time.
-  if (mfma_ok && KIND == KIND_E8D4 && !a.S && a.prep == 0 && (a.M % 32) == 0 && (a.ldy % 8) == 0 &&
-      ((uintptr_t)a.y & 15) == 0 && (a.ldx % 8) == 0) {
+  // stored 16 bytes at a time; fp16 or bf16 activations.
+  const bool rows_ok = KIND == KIND_E8D4 && !a.codes_f32 && !a.S && a.prep == 0 && (a.N % kBK) == 0 &&
+                       (a.M % 32) == 0 && (a.ldy % 8) == 0 && ((uintptr_t)a.y & 15) == 0 && (a.ldx % 8) == 0;
+  if (rows_ok) {
     const int TB = (a.B + g2::kTok - 1) / g2::kTok;
     const size_t dyn = g2::dyn_bytes(a.N);
     // Five-wave workgroups (one per CU) when they cover the layer in one
@@ -663,16 +685,22 @@ int launch_gemm(const LinearArgs& a, hipStream_t s) {
     const int OB = five ? a.M / 40 : a.M / 32;
     const long grid = (long)OB * TB;
     if (grid <= 0x7fffffff && dyn <= 96 * 1024) {
-      const void* kern = five ? (const void*)k_gemm_rows_e8d4<5> : (const void*)k_gemm_rows_e8d4<4>;
-      static size_t attr[2] = {0, 0};
+      const int v = (five ? 1 : 0) | (a.x_bf16 ? 2 : 0);
+      const void* kerns[4] = {(const void*)k_gemm_rows_e8d4<4, false>, (const void*)k_gemm_rows_e8d4<5, false>,
+                              (const void*)k_gemm_rows_e8d4<4, true>, (const void*)k_gemm_rows_e8d4<5, true>};
+      static size_t attr[4] = {0, 0, 0, 0};
       bool ok = true;
-      if (dyn > attr[five]) {
-        ok = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)dyn) == hipSuccess;
-        if (ok) attr[five] = dyn;
+      if (dyn > attr[v]) {
+        ok = hipFuncSetAttribute(kerns[v], hipFuncAttributeMaxDynamicSharedMemorySize, (int)dyn) == hipSuccess;
+        if (ok) attr[v] = dyn;
       }
       if (ok) {
-        if (five) k_gemm_rows_e8d4<5><<<(unsigned)grid, 320, dyn, s>>>(a, OB);
-        else k_gemm_rows_e8d4<4><<<(unsigned)grid, 256, dyn, s>>>(a, OB);
+        switch (v) {
+          case 0: k_gemm_rows_e8d4<4, false><<<(unsigned)grid, 256, dyn, s>>>(a, OB); break;
+          case 1: k_gemm_rows_e8d4<5, false><<<(unsigned)grid, 320, dyn, s>>>(a, OB); break;
+          case 2: k_gemm_rows_e8d4<4, true><<<(unsigned)grid, 256, dyn, s>>>(a, OB); break;
+          default: k_gemm_rows_e8d4<5, true><<<(unsigned)grid, 320, dyn, s>>>(a, OB); break;
+        }
         return 0;
       }
     }

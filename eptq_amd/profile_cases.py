@@ -38,6 +38,7 @@ def main(argv=None) -> None:
     ap.add_argument("--reps", type=int, default=2, help="passes over the copies")
     ap.add_argument("--layers", type=int, default=4, help="decoder layers (case step)")
     ap.add_argument("--qb", type=int, default=0)
+    ap.add_argument("--bf16", action="store_true", help="bf16 activations (cases decode, prefill)")
     args = ap.parse_args(argv)
 
     import torch
@@ -54,6 +55,8 @@ def main(argv=None) -> None:
         T = args.batch if args.case == "decode" else args.tokens
         layers = [_layer(torch, out, inp, 7000 + c, 0.001, dev, qb=qb) for c in range(args.copies)]
         x = make_x(T, inp, seed=1, device=dev)
+        if args.bf16:
+            x = x.bfloat16()
         torch.cuda.synchronize()
         for _ in range(args.reps):
             for L in layers:

@@ -61,3 +61,36 @@ def test_prefill_rows_kernel_matches_oracle(out, inp, T, p, bias):
     print(f"  rel_l2 {e:.2e}", flush=True)
     assert np.isfinite(got).all()
     assert e <= TOL
+
+
+BF16_CASES = [
+    # out, in, tokens, critical-block fraction, bias
+    (1024, 2048, 300, 0.002, True),    # four-wave workgroups
+    (640, 1024, 257, 0.05, False),     # five-wave workgroups, entries past their LDS stage
+]
+
+
+@pytest.mark.parametrize("out,inp,T,p,bias", BF16_CASES, ids=lambda v: str(v))
+def test_prefill_rows_kernel_bf16(out, inp, T, p, bias):
+    """bf16 x and y (the activation operand fp16(x·h·2^-e) from the exact
+    fp32 product): within 2e-2 relative L2 of the fp32 oracle on the same bf16
+    input, the bf16 output rounding included."""
+    print(f"prefill rows kernel bf16 {out}x{inp} T={T} p={p} bias={bias}", flush=True)
+    qd = make_layer(out, inp, seed=800 + out + T, percmask=p, bias=bias)
+    n = layer_np(qd)
+    W = dequantize_layer(n["Q"], n["g"], n["h"], n["O"], table("e8_d4", 1.75), "e8_d4", None).astype(np.float32)
+    x = make_x(T, inp, seed=801).bfloat16()
+    ref = x.float().numpy() @ W.T
+    if qd.bias is not None:
+        ref = ref + qd.bias.float().numpy()
+    ocol, orp = csr_dev(qd.Q)
+    codes = torch.from_numpy(table("e8_d4", 1.75)).half().cuda()
+    y = linear_forward("e8_d4", qd.Q.cuda(), codes, qd.g.cuda(), qd.h.cuda(), x.cuda(), qd.O.cuda(), ocol, orp,
+                       None if qd.bias is None else qd.bias.cuda(), None)
+    torch.cuda.synchronize()
+    assert y.dtype == torch.bfloat16
+    got = y.float().cpu().numpy()
+    e = rel_l2(got, ref)
+    print(f"  rel_l2 {e:.2e}", flush=True)
+    assert np.isfinite(got).all()
+    assert e <= 2e-2
