@@ -54,7 +54,6 @@ using mdec::rsrc;
 constexpr int kTile = 8;        // block rows per tile (64 output rows)
 constexpr int kBlk = 64;        // columns per block: 4 K groups x 16
 constexpr int kDepth = 6;       // blocks of indices and activations in flight per lane
-constexpr int kEarly = 2;       // of which issued before the activation-scale pass
 constexpr int kEntCap = 256;    // critical blocks of a tile prefetched before the column loop
 constexpr int kRedLd = 68;      // floats per batch row of a wave's partial sums
 constexpr int kS = 8;           // column waves per workgroup (one workgroup per CU)
@@ -137,8 +136,10 @@ __global__ __launch_bounds__((S + 1) * 64, 3) void k_decode_mfma(MultiArgs ma, i
   const __amdgpu_buffer_rsrc_t rx = rsrc(a.x, ((B - 1) * ldx + N) * 2);
   const __amdgpu_buffer_rsrc_t rs = rsrc(HAS_S ? a.S + (size_t)grp * N : nullptr, HAS_S ? N * 2 : 0);
 
-  // Table, h and the S row first: their waits then do not include the HBM
-  // index loads (vmcnt counts loads in issue order).
+  // Table, h and the S row first, then the column waves' whole ring: the
+  // prologue's waits for h cover the ring too (a wave with fewer blocks
+  // issues fewer loads, so the compiler cannot count them), but the ring's
+  // round trip then runs under the prologue instead of after it.
   f16x4 tload = {};
   if (tid < 512) tload = ((const f16x4*)a.codes)[tid];
   u32x4 hw[4], sw[4];
@@ -172,7 +173,7 @@ __global__ __launch_bounds__((S + 1) * 64, 3) void k_decode_mfma(MultiArgs ma, i
   int rpv = 0;
   if (wave < S) {
 #pragma unroll
-    for (int d = 0; d < kEarly; ++d) {
+    for (int d = 0; d < kDepth; ++d) {
       if (blo + d < bhi) {
         qv[d][0] = ld16<kNonTemporal>(rq, qo + d * kBlk * 2);
         qv[d][1] = ld16<kNonTemporal>(rq, qo + d * kBlk * 2 + 16);
@@ -284,16 +285,6 @@ __global__ __launch_bounds__((S + 1) * 64, 3) void k_decode_mfma(MultiArgs ma, i
       for (int d = 0; d < kDepth; ++d) {
         const int blk = k + d;
         if (blk >= bhi) break;                     // uniform
-        // First pass: the ring beyond the kEarly blocks issued up front is
-        // filled one block per step, between the blocks' arithmetic, so the
-        // burst does not hold the wave at its issue.
-        if (d + kEarly < kDepth && k == blo && blk + kEarly < bhi) {
-          const int off = (d + kEarly) * kBlk * 2;
-          qv[d + kEarly < kDepth ? d + kEarly : 0][0] = ld16<kNonTemporal>(rq, qo + off);
-          qv[d + kEarly < kDepth ? d + kEarly : 0][1] = ld16<kNonTemporal>(rq, qo + off + 16);
-          xv[d + kEarly < kDepth ? d + kEarly : 0][0] = ld16(rx, xo + off);
-          xv[d + kEarly < kDepth ? d + kEarly : 0][1] = ld16(rx, xo + off + 16);
-        }
         block(qv[d], xv[d], blk);
         if (blk + kDepth < bhi) {
           const int off = (blk - blo + kDepth) * kBlk * 2;
