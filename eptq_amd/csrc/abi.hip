@@ -15,7 +15,6 @@
 #include "eptq_hip.h"
 #include "eptq_llama.h"
 #include "kernels.h"
-#include "step.h"
 
 // Scratch of eptq_e8d4_forward_multi_noalloc: the matrix-core decode's
 // split-K workspace (tile counters, then partial sums for up to 256 CUs), a
@@ -339,7 +338,7 @@ int scratch_of_device(const char* fn, hipStream_t s, char** out) {
 
 extern "C" {
 
-int eptq_abi_version(void) { return 2; }
+int eptq_abi_version(void) { return 3; }
 
 const char* eptq_last_error(void) { return g_err; }
 
@@ -389,142 +388,6 @@ int eptq_e8d4_forward_multi_noalloc(int n_layers, const eptq_layer* layers, cons
 }
 
 long long eptq_e8d4_work_bytes(void) { return eptq::decode_mfma_work_bytes(); }
-
-long long eptq_step_plan_bytes(int n_stages) {
-  return n_stages > 0 ? (long long)n_stages * (long long)sizeof(eptq::step::Stage) : 0;
-}
-
-static long long step_out_bytes(int M_tot) { return ((32LL * M_tot) + 255) & ~255LL; }
-
-long long eptq_step_work_bytes(int n_stages, const eptq_step_stage* stages) {
-  if (n_stages <= 0 || !stages) return 0;
-  long long b = eptq::step::kSyncBytes;
-  for (int s = 0; s < n_stages; ++s) {
-    long long M = 0;
-    for (int l = 0; l < stages[s].n_layers && stages[s].layers; ++l) M += stages[s].layers[l].M;
-    b += step_out_bytes((int)M);
-  }
-  return b;
-}
-
-int eptq_step_init(int n_stages, const eptq_step_stage* stages, const void* codes, void* plan, void* work,
-                   eptq_step_launch* launch, void* stream) {
-  const char* fn = "eptq_step_init";
-  using eptq::step::Stage;
-  if (!stages || !codes || !plan || !work || !launch) return fail(EPTQ_EINVAL, "%s: null argument", fn);
-  if (n_stages <= 0 || n_stages > eptq::step::kMaxStages)
-    return fail(EPTQ_EINVAL, "%s: n_stages=%d (1..%d)", fn, n_stages, eptq::step::kMaxStages);
-  if (((uintptr_t)plan & 15) || ((uintptr_t)work & 255) || ((uintptr_t)codes & 7))
-    return fail(EPTQ_EINVAL, "%s: plan must be 16-, work 256- and codes 8-byte aligned", fn);
-  const int grid = eptq::step_grid();
-  Stage* hs = new Stage[n_stages];
-  char* out = (char*)work + eptq::step::kSyncBytes;
-  int rc = EPTQ_OK;
-  for (int s = 0; s < n_stages && rc == EPTQ_OK; ++s) {
-    const eptq_step_stage& in = stages[s];
-    Stage& S = hs[s];
-    memset(&S, 0, sizeof(S));
-    if (in.n_layers < 1 || in.n_layers > eptq::step::kMaxStageLayers || !in.layers) {
-      rc = fail(EPTQ_EINVAL, "%s: stage %d has %d layers (1..%d)", fn, s, in.n_layers, eptq::step::kMaxStageLayers);
-      break;
-    }
-    S.n_layers = in.n_layers;
-    S.N = in.N;
-    S.nch = in.N / 8;
-    S.nseg = (S.nch + 127) / 128;   // items of 128 chunks (two per lane)
-    int M = 0;
-    for (int l = 0; l < in.n_layers && rc == EPTQ_OK; ++l) {
-      const eptq_layer& L = in.layers[l];
-      eptq::LinearArgs a;
-      rc = layer_args(fn, eptq::KIND_E8D4, L.Q, codes, EPTQ_F16, L.g, L.h, nullptr, EPTQ_F16, L.O_vals, L.O_col,
-                      L.O_row_ptr, L.bias, L.S_group, L.n_groups, L.M, in.N, 0, &a);
-      if (rc) break;
-      if (L.S_group) rc = fail(EPTQ_EUNSUPPORTED, "%s: stage %d layer %d: S_group is not supported", fn, s, l);
-      S.l[l] = {a.Q, a.g, a.h, a.bias, a.O, a.O_col, a.O_row_ptr, L.M, M};
-      M += L.M;
-    }
-    if (rc) break;
-    S.M_tot = M;
-    S.y_ll = (uint64_t*)out;
-    S.y = (uint16_t*)in.y;
-    out += step_out_bytes(M);
-    if ((M + grid - 1) / grid > eptq::step::kRowsMax) {
-      rc = fail(EPTQ_EUNSUPPORTED, "%s: stage %d has %d Q rows, more than %d per compute unit", fn, s, M,
-                eptq::step::kRowsMax);
-      break;
-    }
-    if (in.y && ((uintptr_t)in.y & 3)) { rc = fail(EPTQ_EINVAL, "%s: stage %d y must be 4-byte aligned", fn, s); break; }
-    S.src = in.src;
-    S.col = in.col;
-    if (in.src < 0) {
-      if (!in.x || !aligned16(in.x)) { rc = fail(EPTQ_EINVAL, "%s: stage %d needs a 16-byte aligned x", fn, s); break; }
-      S.x = (const uint16_t*)in.x;
-    } else {
-      if (in.src >= s) { rc = fail(EPTQ_EINVAL, "%s: stage %d reads stage %d (not earlier)", fn, s, in.src); break; }
-      if (in.col < 0 || (in.col & 3) || in.col + in.N > 8 * hs[in.src].M_tot) {
-        rc = fail(EPTQ_EINVAL, "%s: stage %d reads columns [%d, %d) of stage %d's %d outputs (col %% 4 == 0)", fn, s,
-                  in.col, in.col + in.N, in.src, 8 * hs[in.src].M_tot);
-        break;
-      }
-      S.x_ll = hs[in.src].y_ll;
-    }
-    if (in.norm_w) {
-      if (!aligned16(in.norm_w)) { rc = fail(EPTQ_EINVAL, "%s: stage %d norm_w must be 16-byte aligned", fn, s); break; }
-      S.prep = 1;
-      S.nw = (const eptq::f16*)in.norm_w;
-      S.eps = in.eps;
-    }
-    int why = 0;
-    if (eptq::step_check_stage(S, &why)) {
-      rc = fail(EPTQ_EUNSUPPORTED, "%s: stage %d (N=%d, %d layers, norm %d) is outside the engine's limits (%d)", fn,
-                s, S.N, S.n_layers, S.prep, why);
-      break;
-    }
-  }
-  int off[4] = {0, 0, 0, 0};
-  size_t dyn = 0;
-  if (rc == EPTQ_OK) {
-    dyn = eptq::step_lds_layout(n_stages, hs, off);
-    if (dyn == 0) rc = fail(EPTQ_EUNSUPPORTED, "%s: the stages' activation side exceeds the LDS", fn);
-    else if (eptq::step_occupancy(dyn) < 1) rc = fail(EPTQ_EUNSUPPORTED, "%s: the engine kernel does not fit a CU", fn);
-  }
-  if (rc == EPTQ_OK) {
-    hipStream_t st = (hipStream_t)stream;
-    const long long wb = eptq_step_work_bytes(n_stages, stages);
-    if (hipMemcpyAsync(plan, hs, sizeof(Stage) * n_stages, hipMemcpyHostToDevice, st) != hipSuccess ||
-        hipMemsetAsync(work, 0, (size_t)wb, st) != hipSuccess || hipStreamSynchronize(st) != hipSuccess)
-      rc = fail(EPTQ_EHIP, "%s: %s", fn, hipGetErrorString(hipGetLastError()));
-  }
-  delete[] hs;
-  if (rc) return rc;
-  launch->n_stages = n_stages;
-  launch->grid = grid;
-  launch->dyn_lds = (int)dyn;
-  for (int i = 0; i < 4; ++i) launch->lds[i] = off[i];
-  return EPTQ_OK;
-}
-
-int eptq_step_run(const void* plan, const void* codes, void* work, const eptq_step_launch* launch, void* stream) {
-  const char* fn = "eptq_step_run";
-  if (!plan || !codes || !work || !launch) return fail(EPTQ_EINVAL, "%s: null argument", fn);
-  if (launch->n_stages <= 0 || launch->dyn_lds <= 0) return fail(EPTQ_EINVAL, "%s: launch not initialized", fn);
-  if (launch->grid != eptq::step_grid())
-    return fail(EPTQ_EINVAL, "%s: plan made for %d compute units, this device has %d", fn, launch->grid,
-                eptq::step_grid());
-  if (eptq::step_launch((const eptq::step::Stage*)plan, launch->n_stages, (int*)work, codes, launch->lds,
-                        (size_t)launch->dyn_lds, (hipStream_t)stream))
-    return fail(EPTQ_EHIP, "%s: cannot configure the engine kernel", fn);
-  return check_launch(fn);
-}
-
-int eptq_step_status(const void* work) {
-  if (!work) return fail(EPTQ_EINVAL, "eptq_step_status: null work");
-  int w[4] = {0, 0, 0, 0};
-  if (hipMemcpy(w, work, sizeof(w), hipMemcpyDeviceToHost) != hipSuccess)
-    return fail(EPTQ_EHIP, "eptq_step_status: %s", hipGetErrorString(hipGetLastError()));
-  if (w[eptq::step::kErrorWord]) return fail(EPTQ_ETIMEOUT, "eptq_step_status: a stage input wait gave up");
-  return EPTQ_OK;
-}
 
 int eptq_llama_norm_linear(int n_layers, const eptq_layer* layers, const void* codes,
                            const void* resid, const void* delta, const void* w, float eps,

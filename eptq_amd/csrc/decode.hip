@@ -29,7 +29,7 @@ __global__ __launch_bounds__(kT) void k_decode_e8d4(MultiArgs ma) {
   const int wg = (int)blockIdx.x - ma.start[li];
   const int G = ma.start[li + 1] - ma.start[li];
 
-  using L = Layer<BT, J, P, S, HAS_S, XT, false>;
+  using L = Layer<BT, J, P, S, HAS_S, XT>;
   const L layer(a, wg, G);
   const Smem<BT> sm{tab, red, wmax, (uint16_t*)dyn, (float*)(dyn + BT * (a.N + 8) * 2)};
   typename L::State st;
@@ -68,7 +68,7 @@ __global__ __launch_bounds__(kT) void k_decode_e8d4_pair(MultiArgs ma) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const bool up = wave & 1;
   const LinearArgs a = up ? ma.l[1] : ma.l[0];
-  using L = Layer<BT, J, P, 1, HAS_S, f16, false, true>;
+  using L = Layer<BT, J, P, 1, HAS_S, f16, true>;
   const L layer(a, (int)blockIdx.x, (int)gridDim.x);
   const size_t act = pair_table_bytes(a.N, BT);   // the second table 16-byte aligned
   const Smem<BT> sm0{tab, red, wmax[0], (uint16_t*)dyn, (float*)(dyn + BT * (a.N + 8) * 2)};
@@ -126,7 +126,7 @@ int launch_k(const LinearArgs* layers, int n, hipStream_t s) {
   constexpr int P = 8 / (J > 4 ? 4 : J);
   constexpr int R = kW / S;
   // The fused RMSNorm keeps a whole row in the first CAP chunks per thread.
-  if (layers[0].prep == 1 && Layer<BT, J, P, S, HAS_S, XT, false>::CAP * kT * 8 < layers[0].N) return -1;
+  if (layers[0].prep == 1 && Layer<BT, J, P, S, HAS_S, XT>::CAP * kT * 8 < layers[0].N) return -1;
   auto kern = k_decode_e8d4<BT, J, P, S, HAS_S, XT>;
   // As many workgroups per CU as registers and LDS allow (one wave of each
   // workgroup per SIMD): occupancy hides the LDS lookup latency.
@@ -167,7 +167,7 @@ int launch_k(const LinearArgs* layers, int n, hipStream_t s) {
 template <int BT, int J, bool HAS_S>
 int launch_pair_k(const LinearArgs* l, hipStream_t s) {
   constexpr int P = 8 / (J > 4 ? 4 : J);
-  using L = Layer<BT, J, P, 1, HAS_S, f16, false, true>;
+  using L = Layer<BT, J, P, 1, HAS_S, f16, true>;
   // The fused RMSNorm keeps a whole row in the first CAP chunks per thread.
   if (l[0].prep == 1 && L::CAP * kT * 8 < l[0].N) return -1;
   auto kern = k_decode_e8d4_pair<BT, J, P, HAS_S>;

@@ -1,6 +1,5 @@
-// One layer of the E8-D4 decode matvec (batch 1..8) as seen by one workgroup:
-// shared by the one-launch-per-layer kernel (decode.hip) and the persistent
-// chain kernel (chain.hip).
+// One layer of the E8-D4 decode matvec (batch 1..8) as seen by one workgroup
+// of the one-launch-per-layer kernels (decode.hip).
 //
 // Same result as the reference decode kernels (csrc/eptq_kernels.cu:161-292,
 // kernels/triton_e8d4.py:47-157): y = g ⊙ (decode(Q)·(h ⊙ S ⊙ x)ᵀ + CSR(O)) + bias.
@@ -35,10 +34,6 @@
 //   rows 4..7:              same bits 10-11, bits 3-9 = (v & 127) << 3.
 // Critical blocks (v = 32767) decode as table row 511 in both halves; the
 // CSR pass adds O·(h x) minus exactly what the main loop accumulated for them.
-//
-// COH (chain kernel): x is read and y written with device-coherent (sc1)
-// accesses, because x may be the output of another workgroup earlier in the
-// same launch, on another XCD, whose L2 is not coherent with this one.
 #pragma once
 
 #include "common.h"
@@ -51,7 +46,6 @@ constexpr int kT = 256;                    // threads per workgroup
 constexpr int kW = kT / 64;                // waves per workgroup
 constexpr int kBufferWord3 = 0x00020000;   // buffer resource word 3 (gfx9 family)
 constexpr int kNonTemporal = 2;            // buffer load cache policy: nt
-constexpr int kCoherent = 16;              // buffer load cache policy: sc1 (device scope)
 constexpr int kRing = 8;                   // index chunks in flight per lane
 
 typedef f16 h2 __attribute__((ext_vector_type(2)));
@@ -84,21 +78,16 @@ __device__ __forceinline__ uint32_t pk_mul(uint32_t a, uint32_t b) {
   return __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, a) * __builtin_bit_cast(h2, b));
 }
 
-// A layer pointer as a global-memory pointer.  Pointers that reach a kernel
-// through memory other than its argument segment (the chain kernel's stage
-// descriptors) are generic to the compiler, which would access them with
-// flat instructions; those count on both vmcnt and lgkmcnt and make every
-// wait a full one.
+// A layer pointer as a global-memory pointer.  A generic pointer (one the
+// compiler cannot place in the global address space) is accessed with flat
+// instructions, which count on both vmcnt and lgkmcnt and make every wait a
+// full one.
 template <typename T>
 __device__ __forceinline__ __attribute__((address_space(1))) T* gp(T* p) {
   return (__attribute__((address_space(1))) T*)p;
 }
 
-template <bool COH>
-__device__ __forceinline__ void store_y(uint16_t* p, uint16_t v) {
-  if constexpr (COH) __hip_atomic_store(gp(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  else *gp(p) = v;
-}
+__device__ __forceinline__ void store_y(uint16_t* p, uint16_t v) { *gp(p) = v; }
 
 // Dynamic LDS of the activation side: BT padded fp16 rows, plus the per-chunk
 // scales for B = 1.
@@ -146,9 +135,8 @@ struct RowState {
 };
 
 // Where one workgroup's work lies in a layer split S ways with J chunks per
-// lane: the row groups wg, wg + G, ...  Runtime form of the layout, so a
-// persistent kernel can prefetch a stage of any split; with compile-time
-// S and J the arithmetic folds away.
+// lane: the row groups wg, wg + G, ...  (Runtime fields; with compile-time S
+// and J the arithmetic folds away.)
 struct Walk {
   const LinearArgs& a;
   int wg, G, S, J, K, R, slot, seg, lane, tid, V;
@@ -254,11 +242,11 @@ struct Walk {
 // layer w % 2 (gate, up) at row slot w / 2; the output is the SwiGLU product
 // silu(gate) ⊙ up, each factor rounded to the activation type first, as the
 // unfused Linear outputs are.
-template <int BT, int J, int P, int S, bool HAS_S, typename XT, bool COH, bool PAIR = false>
+template <int BT, int J, int P, int S, bool HAS_S, typename XT, bool PAIR = false>
 struct Layer {
   static constexpr int V = BT * 8;
   static constexpr int R = PAIR ? kW / S / 2 : kW / S;   // rows per row group (per layer)
-  static_assert(!PAIR || (S == 1 && !COH), "pairs: whole-row waves, one launch per layer pair");
+  static_assert(!PAIR || S == 1, "pairs: whole-row waves, one launch per layer pair");
   static constexpr int K = J > 4 ? 4 : J;                 // chunks of a row in flight
   static_assert(P * K == kRing, "the ring holds kRing chunks");
   static_assert(J % K == 0, "chunks per row must be a multiple of the chunks in flight");
@@ -311,7 +299,7 @@ struct Layer {
 #pragma unroll
       for (int b = 0; b < BT; ++b)
         xw[b] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-            rx, cv && b < B ? b * ldx * 2 + c * 16 : B * ldx * 2, 0, COH ? kCoherent : 0));
+            rx, cv && b < B ? b * ldx * 2 + c * 16 : B * ldx * 2, 0, 0));
       if (prep != 0) {
 #pragma unroll
         for (int b = 0; b < BT; ++b)
@@ -702,7 +690,7 @@ struct Layer {
           // separate kernel computes it (without this the compiler fuses the
           // multiply and the conversion into one mixed-precision FMA).
           asm volatile("" : "+v"(o));
-          store_y<COH>(a.y + (size_t)wb * a.ldy + 8 * m + wk, Act<XT>::from_f32(o));
+          store_y(a.y + (size_t)wb * a.ldy + 8 * m + wk, Act<XT>::from_f32(o));
         }
         par ^= 1;
       } else if constexpr (S == 1) {
@@ -710,7 +698,7 @@ struct Layer {
         (void)base;
         if (row_ok && WaveReduceOut<V>::writer(lane) && wb < B) {
           const float sum = acc[0] * out_scale * (float)og + (float)ob;
-          store_y<COH>(a.y + (size_t)wb * a.ldy + 8 * m + wk, Act<XT>::from_f32(sum));
+          store_y(a.y + (size_t)wb * a.ldy + 8 * m + wk, Act<XT>::from_f32(sum));
         }
       } else {
         if (WaveReduceOut<V>::writer(lane)) {
@@ -727,7 +715,7 @@ struct Layer {
 #pragma unroll
             for (int w = 0; w < S; ++w) sum += sm.red[par][sl * S + w][wbase];
             sum = sum * out_scale * (float)og + (float)ob;
-            store_y<COH>(a.y + (size_t)wb * a.ldy + 8 * orow + wk, Act<XT>::from_f32(sum));
+            store_y(a.y + (size_t)wb * a.ldy + 8 * orow + wk, Act<XT>::from_f32(sum));
           }
         }
         par ^= 1;

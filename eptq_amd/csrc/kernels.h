@@ -79,18 +79,6 @@ int launch_decode_e8d4(const LinearArgs& a, hipStream_t s);
 int launch_decode_e8d4_multi(const LinearArgs* layers, int n, hipStream_t s, void* work = nullptr,
                              long long work_bytes = 0);
 
-namespace step { struct Stage; }
-// Persistent batch-1 decode-step engine (step.hip).  step_lds_layout: dynamic
-// LDS bytes for the plan's stages (offsets into off[4]), 0 when they do not
-// fit; step_check_stage: 0 when the kernel's budgets take the stage (else -1
-// and a reason code); step_launch: -1 when the kernel cannot be configured.
-size_t step_lds_layout(int n, const step::Stage* stages, int* off);
-int step_check_stage(const step::Stage& S, int* why);
-int step_grid();
-int step_occupancy(size_t dyn);
-int step_launch(const step::Stage* plan, int n, int* sync, const void* codes, const int* off, size_t dyn,
-                hipStream_t s);
-
 // SwiGLU pair (B <= 2, fp16): layers[0] = gate and layers[1] = up of equal
 // shape in one launch, y = silu(gate) ⊙ up written at layers[0].y with
 // layers[0].ldy; -1 when the pair is outside the kernel's range.

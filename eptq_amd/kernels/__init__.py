@@ -16,7 +16,6 @@ and ``eptq::e8d4_dequant`` / ``eptq::e8_dequant`` produce the bit-exact fp16 W o
 
 from __future__ import annotations
 
-import ctypes
 
 from typing import Optional
 
@@ -26,7 +25,7 @@ from . import _lib
 from ._lib import EPTQ_BF16, EPTQ_F16, EPTQ_F32, EptqError
 
 __all__ = ["e8_forward", "e8d4_forward", "e8_forward_grouped", "e8d4_forward_grouped",
-           "e8_dequant", "e8d4_dequant", "EptqError", "linear_forward", "linear_forward_multi", "DecodeStep",
+           "e8_dequant", "e8d4_dequant", "EptqError", "linear_forward", "linear_forward_multi",
            "dequant", "dequant_linear", "decode_workspace", "PREFILL_DEQUANT_MIN_TOKENS"]
 
 # From this many fp16 tokens on, the module forward (``EPTQLinear``,
@@ -153,94 +152,6 @@ def linear_forward_multi(layers, codes, x, work: Optional[torch.Tensor] = None) 
                                          stream)
     _lib.check(rc, "eptq_e8d4_forward_multi")
     return y
-
-
-class DecodeStep:
-    """A plan for the decode-step engine (``eptq_step_*``): batch-1 E8-D4
-    stages run in order by one persistent launch.
-
-    ``stages``: list of dicts with ``layers`` (1..3 dicts of EPTQLinear
-    buffers, as for ``linear_forward_multi``; outputs side by side), ``N``,
-    and the input: ``x`` (a (1, N) fp16 tensor) or ``src`` (index of an
-    earlier stage) and ``col`` (its first output column read); optional
-    ``norm_w`` (fp16 (N,), RMSNorm of the input) with ``eps``, and ``y`` (a
-    (1, 8·ΣM) fp16 tensor receiving a plain copy of the output).  The plan
-    keeps references to every tensor; ``run`` launches on the current stream
-    and allocates nothing."""
-
-    def __init__(self, stages, codes):
-        _require(len(stages) > 0, "no stages")
-        _require(codes.dtype == torch.float16 and codes.is_cuda and codes.is_contiguous(),
-                 "the decode step takes the fp16 (512, 4) table on the GPU")
-        lib = _lib.load()
-        self.device = codes.device
-        self._keep = [codes]
-        self._arrs = []
-        st = (_lib.EptqStepStage * len(stages))()
-        self.widths = []
-        for i, S in enumerate(stages):
-            N = int(S["N"])
-            arr = (_lib.EptqLayer * len(S["layers"]))()
-            off = 0
-            for k, L in enumerate(S["layers"]):
-                M, n2, n_groups = _check_layer("e8_d4", L["Q"], codes, L["g"], L["h"], L["O_vals"], L["O_col"],
-                                               L["O_row_ptr"], L.get("S_group"))
-                _require(n2 == N and L["Q"].device == self.device, "layers must take N inputs on the table's device")
-                arr[k] = _lib.EptqLayer(_ptr(L["Q"]), _ptr(L["g"]), _ptr(L["h"]), _ptr(L["O_vals"]),
-                                        _ptr(L["O_col"]), _ptr(L["O_row_ptr"]), _ptr(L.get("bias")),
-                                        _ptr(L.get("S_group")), n_groups, M, off)
-                off += 8 * M
-                self._keep.append(L)
-            self.widths.append(off)
-            x, y, nw = S.get("x"), S.get("y"), S.get("norm_w")
-            for t_ in (x, y, nw):
-                if t_ is not None:
-                    _require(t_.dtype == torch.float16 and t_.is_contiguous() and t_.device == self.device,
-                             "stage x, y and norm_w must be contiguous fp16 tensors on the table's device")
-                    self._keep.append(t_)
-            src = int(S.get("src", -1))
-            st[i] = _lib.EptqStepStage(len(S["layers"]), ctypes.addressof(arr), N, src,
-                                       _ptr(x) if src < 0 else None, int(S.get("col", 0)), _ptr(nw),
-                                       float(S.get("eps", 1e-5)), _ptr(y))
-            self._arrs.append(arr)
-        n = len(stages)
-        with torch.cuda.device(self.device):
-            self.plan = torch.empty(int(lib.eptq_step_plan_bytes(n)), dtype=torch.uint8, device=self.device)
-            self.work = torch.empty(int(lib.eptq_step_work_bytes(n, st)), dtype=torch.uint8, device=self.device)
-            self.launch = _lib.EptqStepLaunch()
-            rc = lib.eptq_step_init(n, st, _ptr(codes), _ptr(self.plan), _ptr(self.work), ctypes.byref(self.launch),
-                                    torch.cuda.current_stream().cuda_stream)
-        _lib.check(rc, "eptq_step_init")
-        self.n_stages = n
-        self._codes = codes
-        # Byte offset of each stage's flagged output in the work area.
-        self._out = []
-        o = 256
-        for w in self.widths:
-            self._out.append(o)
-            o += (4 * w + 255) // 256 * 256
-
-    def run(self) -> None:
-        with torch.cuda.device(self.device):
-            rc = _lib.load().eptq_step_run(_ptr(self.plan), _ptr(self._codes), _ptr(self.work),
-                                           ctypes.byref(self.launch), torch.cuda.current_stream().cuda_stream)
-        _lib.check(rc, "eptq_step_run")
-
-    def status(self) -> None:
-        """Raise if a stage input wait gave up in an earlier run (synchronizes)."""
-        torch.cuda.synchronize(self.device)
-        _lib.check(_lib.load().eptq_step_status(_ptr(self.work)), "eptq_step_status")
-
-    def output(self, s: int) -> torch.Tensor:
-        """Stage s's output of the last run as a (1, width) fp16 tensor
-        (a copy without the flags)."""
-        w = self.widths[s]
-        words = self.work[self._out[s]:self._out[s] + 4 * w].view(torch.int32).view(-1, 2)
-        return words[:, 0].contiguous().view(torch.float16).reshape(1, w).clone()
-
-    def flags(self, s: int) -> torch.Tensor:
-        w = self.widths[s]
-        return self.work[self._out[s]:self._out[s] + 4 * w].view(torch.int32).view(-1, 2)[:, 1].clone()
 
 
 def dequant(kind: str, Q, codes, g, h, O_vals, O_col, O_row_ptr, S_group=None,

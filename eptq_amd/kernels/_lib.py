@@ -26,11 +26,6 @@ SIGNATURES = {
     "eptq_e8d4_forward_multi": ([_I, _P, _P, _I, _P, _I, _I, _I, _P, _I, _P, ctypes.c_longlong, _P], _I),
     "eptq_e8d4_work_bytes": ([], ctypes.c_longlong),
     "eptq_e8d4_forward_multi_noalloc": ([_I, _P, _P, _I, _P, _I, _I, _I, _P, _I, _P], _I),
-    "eptq_step_plan_bytes": ([_I], ctypes.c_longlong),
-    "eptq_step_work_bytes": ([_I, _P], ctypes.c_longlong),
-    "eptq_step_init": ([_I, _P, _P, _P, _P, _P, _P], _I),
-    "eptq_step_run": ([_P, _P, _P, _P, _P], _I),
-    "eptq_step_status": ([_P], _I),
     "eptq_e8d4_dequant": ([_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _P, _P], _I),
     "eptq_e8_dequant": ([_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _P, _P], _I),
 }
@@ -39,17 +34,6 @@ class EptqLayer(ctypes.Structure):
     """``eptq_layer`` of include/eptq_hip.h."""
     _fields_ = [("Q", _P), ("g", _P), ("h", _P), ("O_vals", _P), ("O_col", _P), ("O_row_ptr", _P),
                 ("bias", _P), ("S_group", _P), ("n_groups", _I), ("M", _I), ("y_offset", ctypes.c_longlong)]
-
-
-class EptqStepStage(ctypes.Structure):
-    """``eptq_step_stage`` of include/eptq_hip.h."""
-    _fields_ = [("n_layers", _I), ("layers", _P), ("N", _I), ("src", _I), ("x", _P), ("col", _I),
-                ("norm_w", _P), ("eps", ctypes.c_float), ("y", _P)]
-
-
-class EptqStepLaunch(ctypes.Structure):
-    """``eptq_step_launch`` of include/eptq_hip.h."""
-    _fields_ = [("n_stages", _I), ("grid", _I), ("dyn_lds", _I), ("lds", _I * 4)]
 
 
 # Fused decode-step operators of the Llama harness (include/eptq_llama.h).

@@ -9,7 +9,6 @@ dozen dispatches each, no graph capture.
     python -m eptq_amd.profile_cases prefill --shape 5120x5120 --tokens 2048
     python -m eptq_amd.profile_cases e8 --shape 3072x768 --copies 8
     python -m eptq_amd.profile_cases step --layers 4
-    python -m eptq_amd.profile_cases engine --layers 32
 """
 
 from __future__ import annotations
@@ -30,7 +29,7 @@ def _layer(torch, out, inp, seed, p, dev, qb=None, bias=False):
 
 def main(argv=None) -> None:
     ap = argparse.ArgumentParser()
-    ap.add_argument("case", choices=["decode", "prefill", "e8", "step", "engine"])
+    ap.add_argument("case", choices=["decode", "prefill", "e8", "step"])
     ap.add_argument("--shape", default="4096x4096", help="out x in")
     ap.add_argument("--batch", type=int, default=1)
     ap.add_argument("--tokens", type=int, default=2048)
@@ -71,37 +70,6 @@ def main(argv=None) -> None:
             for L in layers:
                 linear_forward("e8_lattice", L["Q"], codes, L["g"], L["h"], x, L["O_vals"], L["O_col"],
                                L["O_row_ptr"], L["bias"], None)
-    elif args.case == "engine":
-        # The decode-step engine over args.layers Llama-2-7B layers: per layer
-        # q|k|v (input RMSNorm), o, gate|up (post-attention RMSNorm), down,
-        # each stage reading the previous stage's output.
-        from eptq_amd.kernels import DecodeStep
-        codes = E8D4Quantizer(radius=1.75).flat_table().half().to(dev)
-        gen = torch.Generator(device=dev).manual_seed(5)
-        stages = []
-        for li in range(args.layers):
-            mk = lambda o, i, k: _layer(torch, o, i, 8000 + 10 * li + k, 0.001, dev)
-            qkv = [mk(4096, 4096, k) for k in range(3)]
-            o, gu, dn = [mk(4096, 4096, 3)], [mk(11008, 4096, 4), mk(11008, 4096, 5)], [mk(4096, 11008, 6)]
-            nw1 = (1 + 0.05 * torch.randn(4096, generator=gen, device=dev)).half()
-            nw2 = (1 + 0.05 * torch.randn(4096, generator=gen, device=dev)).half()
-            base = 4 * li
-            st = dict(layers=qkv, N=4096, norm_w=nw1, eps=1e-5)
-            if li == 0:
-                st["x"] = make_x(1, 4096, seed=3, device=dev)
-            else:
-                st.update(src=base - 1, col=0)
-            stages += [st, dict(layers=o, N=4096, src=base, col=0),
-                       dict(layers=gu, N=4096, src=base + 1, col=0, norm_w=nw2, eps=1e-5),
-                       dict(layers=dn, N=11008, src=base + 2, col=0)]
-        for S in stages:
-            S["layers"] = [{k: v for k, v in L.items() if k != "S_group"} for L in S["layers"]]
-        plan = DecodeStep(stages, codes)
-        torch.cuda.synchronize()
-        for _ in range(args.reps):
-            plan.run()
-        torch.cuda.synchronize()
-        plan.status()
     else:
         # One decode step's Linear units of args.layers Llama-2-7B layers:
         # q|k|v and gate|up as multi-layer launches, o and down alone.

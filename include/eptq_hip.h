@@ -5,8 +5,7 @@
  * device memory, keeps no pointer after returning, and returns EPTQ_OK or an
  * error code; eptq_last_error() then describes the failure (per host
  * thread).  The compute entry points take a hipStream_t (passed as void*) and
- * launch asynchronously on it; the two exceptions, eptq_step_init and
- * eptq_step_status, synchronize and say so where they are declared.
+ * launch asynchronously on it and never synchronize.
  *
  * Layer format (reference config.py:98-159, kernels/linear.py:83-152):
  *   Q          int16 (M, N) row-major, stored as index - 32768; 32767 marks a
@@ -39,7 +38,7 @@ enum {
   EPTQ_EINVAL = 1,        /* null pointer / negative size / inconsistent args */
   EPTQ_EUNSUPPORTED = 2,  /* shape or alignment outside what the kernels take */
   EPTQ_EHIP = 3,          /* HIP runtime reported an error at launch */
-  EPTQ_ETIMEOUT = 4       /* a decode-step stage wait gave up (results invalid) */
+  EPTQ_ETIMEOUT = 4       /* reserved: no entry point of this revision returns it */
 };
 
 enum { EPTQ_F16 = 0, EPTQ_F32 = 1, EPTQ_BF16 = 2 };
@@ -130,77 +129,6 @@ long long eptq_e8d4_work_bytes(void);
 int eptq_e8d4_forward_multi_noalloc(int n_layers, const eptq_layer* layers, const void* codes,
                                     int codes_dtype, const void* x, int x_dtype, int N, int B, void* y,
                                     int ldy, void* stream);
-
-/*
- * Decode-step engine (batch 1, E8-D4, fp16): a sequence of dependent Linear
- * stages — a decode step's q|k|v, o, gate|up and down for every transformer
- * layer — run by ONE persistent launch, one workgroup per compute unit.  The
- * index stream of later stages is in flight while a stage waits for its
- * input, so the per-launch fixed cost of eptq_e8d4_forward_multi (launch gap,
- * first-load latency, drain) is paid once per step instead of once per stage.
- *
- * A stage is 1..3 layers that read the same input (outputs side by side in
- * layer order, as eptq_e8d4_forward_multi with consecutive y_offsets; the
- * layers' y_offset fields are ignored; no S_group).  Its input is either a
- * plain fp16 (1, N) vector x (src = -1) or columns [col, col + N) of the
- * output of an earlier stage src; with norm_w it is RMSNorm'd first:
- * fp16(x · rsqrt(mean(x²) + eps) · norm_w).  Stage outputs live in the work
- * area in a flagged form (each 8-byte word: two fp16 outputs and a 32-bit
- * flag), so a stage boundary costs one store and one poll; y, if given,
- * receives a plain fp16 copy of the stage's output.
- *
- * Limits: N a multiple of 8 and <= 11264; n_layers·N <= 12288; N <= 4096
- * for a stage with norm_w; col a multiple of 4; at most 16 Q rows of a stage
- * per compute unit (ΣM <= 16 · CUs); at most 1024 stages.
- *
- * No counterpart in the reference, whose decode step calls one Linear per
- * projection (bench_decode.py:44-71, kernels/linear.py:154-212); its callers
- * are batch-1 decode loops.
- */
-typedef struct {
-  int n_layers;               /* 1..3 */
-  const eptq_layer* layers;
-  int N;                      /* in_features of the layers */
-  int src;                    /* -1: plain input x; else an earlier stage */
-  const void* x;              /* (1, N) fp16 device, 16-byte aligned (src < 0) */
-  int col;                    /* first input column of stage src's output */
-  const void* norm_w;         /* fp16 (N) RMSNorm weight, or NULL */
-  float eps;
-  void* y;                    /* (1, 8·ΣM) fp16 device copy of the output, or NULL */
-} eptq_step_stage;
-
-/* Launch parameters filled by eptq_step_init (host memory). */
-typedef struct {
-  int n_stages;
-  int grid;
-  int dyn_lds;
-  int lds[4];
-} eptq_step_launch;
-
-/* Bytes of the device plan for n_stages stages. */
-long long eptq_step_plan_bytes(int n_stages);
-
-/* Bytes of the device work area (synchronization words and every stage's
- * flagged output) for these stages. */
-long long eptq_step_work_bytes(int n_stages, const eptq_step_stage* stages);
-
-/* Validate the stages and write the plan (plan: eptq_step_plan_bytes bytes,
- * 16-byte aligned device memory) and a zeroed work area (work:
- * eptq_step_work_bytes bytes, 256-byte aligned device memory), both
- * caller-owned; codes: the fp16 (512, 4) table.  Synchronizes the stream:
- * call outside graph capture.  Allocates nothing. */
-int eptq_step_init(int n_stages, const eptq_step_stage* stages, const void* codes, void* plan, void* work,
-                   eptq_step_launch* launch, void* stream);
-
-/* One run of every stage of the plan: one launch on the stream, no
- * allocation, no synchronization (graph-capturable).  Runs that share a work
- * area must not overlap in time. */
-int eptq_step_run(const void* plan, const void* codes, void* work, const eptq_step_launch* launch,
-                  void* stream);
-
-/* EPTQ_ETIMEOUT if a stage input wait of an earlier run gave up (its outputs
- * are then invalid), else EPTQ_OK.  Synchronous (reads the work area). */
-int eptq_step_status(const void* work);
 
 /*
  * Fused E8-lattice quantized Linear (same math, 8-vector = codes[u]).

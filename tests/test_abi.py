@@ -43,7 +43,7 @@ def test_every_declared_symbol_is_exported(lib):
 
 
 def test_abi_version(lib):
-    assert lib.eptq_abi_version() == 2
+    assert lib.eptq_abi_version() == 3
     assert lib.eptq_last_error() is not None
 
 
