@@ -378,8 +378,9 @@ __device__ __forceinline__ void gemm_tile(const LinearArgs& a, int OB) {
 // GEMM, csrc/eptq_kernels.cu:520-537), with 2^-e a workgroup-uniform power
 // of two that keeps |x·h·2^-e| <= |x|.  A critical block replaces the
 // lane's four looked-up values with its O values in registers: each lane
-// walks its Q-row's CSR entries (staged in LDS) with a cursor, so the MFMA
-// result needs no correction.  D of MFMA c, token tile j, lane (n, lg),
+// walks its Q-row's CSR entries (the first kEnt of the workgroup staged in
+// LDS) with a cursor; entries past the stage keep the marker's table row in
+// the K loop and are corrected after it.  D of MFMA c, token tile j, lane (n, lg),
 // element v is feature 16·lg + 4v + c of the wave's 64 for token 16j + n, so
 // a lane stores 16 consecutive features of one token.
 namespace g2 {
