@@ -325,9 +325,9 @@ def _cpu_dequant_matmul(qd, xs, kind, tab, runs=5):
 
 def cpu_baseline(seed=1000, runs=5):
     """Reference CPU path (per-column ``dequantize_layer`` restatement +
-    fp32 ``torch.matmul``) on a bounded sample of the benchmark workload: a
-    q/k/v/o-shaped (4096x4096) and a gate/up-shaped (11008x4096) Linear of
-    Llama-2-7B at batch 1, on all of this host's cores (about 20 s)."""
+    fp32 ``torch.matmul``) on a bounded sample of the benchmark workload: the
+    seven Linears of one Llama-2-7B decoder layer (1/32 of a step) at batch
+    1, on all of this host's cores (about 20 s with the warm-up runs)."""
     from eptq_amd.quantizers import E8D4Quantizer
     from eptq_amd.synthetic import make_layer, make_x
 
@@ -335,17 +335,19 @@ def cpu_baseline(seed=1000, runs=5):
     tab = E8D4Quantizer(radius=1.75).flat_table().numpy()
     t_dq = t_mm = 0.0
     nbytes = 0
-    for idx, (out, inp) in enumerate(((4096, 4096), (11008, 4096))):
+    for idx, (_, out, inp) in enumerate(LLAMA2_7B):
         qd = make_layer(out, inp, seed=seed + idx, percmask=0.001)
         a, b = _cpu_dequant_matmul(qd, [make_x(1, inp, seed=seed + 100 + idx)], "e8_d4", tab, runs)
         t_dq, t_mm = t_dq + a, t_mm + b[0]
         nbytes += algo_bytes(out, inp, 1, int(qd.O.shape[0]))
+        del qd
     t = t_dq + t_mm
     return {"value": round(nbytes / t / 1e9, 6), "unit": "GB/s", "cores": cores, "kind": "port",
             "dequant_s": round(t_dq, 4), "matmul_s": round(t_mm, 5),
-            "sample": f"a 4096x4096 and an 11008x4096 Llama-2-7B Linear (E8-D4 r=1.75, p=0.001) at B=1: "
-                      f"per-column dequantize_layer restatement, then fp32 torch.matmul, each timed "
-                      f"separately, median of {runs} after one warmup; {t:.2f} s for {nbytes} algorithmic bytes"}
+            "sample": f"the seven Linears of one Llama-2-7B decoder layer (q/k/v/o 4096x4096, gate/up "
+                      f"11008x4096, down 4096x11008; E8-D4 r=1.75, p=0.001) at B=1: per-column "
+                      f"dequantize_layer restatement, then fp32 torch.matmul, each timed separately, "
+                      f"median of {runs} after one warmup; {t:.2f} s for {nbytes} algorithmic bytes"}
 
 
 def cpu_configs(seed=2000, runs=5):
