@@ -644,6 +644,295 @@ __global__ __launch_bounds__(64 * kW, 8 / kW) void k_gemm_rows_e8d4(LinearArgs a
   }
 }
 
+// ---------------------------------------------------------------------------
+// E8-D4 prefill GEMM with the weight tile decoded into LDS and the activation
+// tile brought in by LDS DMA (fp16 x, no S_group).
+//
+// A workgroup of 8 waves computes BF output features (BF/8 Q-rows) × 256
+// tokens; wave w owns features (w & 1)·BF/2 .. +BF/2 of tokens 64·(w >> 1)
+// .. +63 as (BF/32) × 4 tiles of v_mfma_f32_16x16x32_f16.  Per K-step of 64
+// columns:
+//  * X: 256 rows × 128 bytes of raw fp16 x, written to LDS by
+//    global_load_lds_dwordx4 (no register staging), double-buffered, rows
+//    XOR-swizzled by 16-byte chunk so the MFMA fragment reads (16 rows at one
+//    chunk) hit distinct banks;
+//  * the index tile (BF/8 Q-rows × 64 columns of int16) and the step's 64 h
+//    values, also by LDS DMA, two steps ahead;
+//  * W: lane (8-column group, half, Q-row) of waves 0 .. BF/32 - 1 decodes 8
+//    indices through the LDS table (8 lookups, the matrix-core decode's
+//    operand mapping), replaces critical blocks from the workgroup's CSR
+//    entries staged in LDS (a per-lane cursor), multiplies by h and writes 4
+//    rows × 8 columns of fp16 W·h·2^-e, one step ahead of the MFMAs, into a
+//    double-buffered tile whose layout spreads each row's chunks over both
+//    halves of a 256-byte bank row (conflict-free writes and reads).
+// h sits on the weight side and the table is scaled by 2^-e once (2^e ≥
+// max|h|, so W·h·2^-e cannot overflow fp16); y = acc·2^e·g + bias.  Entries
+// past the LDS stage keep table row 511 in the loop and are corrected after
+// it.  One workgroup per CU (LDS), one barrier per K-step.
+namespace g3 {
+constexpr int kBK = 64;     // columns per K-step: 128-byte rows
+constexpr int kBT = 256;    // tokens per workgroup
+constexpr int kLds = 160 * 1024;
+__device__ __forceinline__ int xpos(int t, int c) { return t * 128 + ((c ^ ((t >> 1) & 7)) << 4); }
+// Row r's 16-byte chunk c: the chunks of rows r and r ^ 1 alternate across the
+// 256-byte bank row they share, XOR-swizzled by r / 2, so 16 consecutive rows
+// at one chunk and rows c, c + 4 of one 8-row block (the decode's 16-lane
+// write groups) each cover 16 distinct 16-byte bank slots.
+__device__ __forceinline__ int wpos(int r, int c) {
+  const int b = (r ^ (r >> 2)) & 1;
+  return (r >> 1) * 256 + (((2 * c + b) ^ (2 * ((r >> 1) & 7))) << 4);
+}
+template <int BF> struct Lay {
+  static constexpr int QR = BF / 8, QRp = (QR + 7) / 8 * 8;
+  static constexpr int X0 = 0, XS = kBT * 128;                   // 2 stages
+  static constexpr int W0 = 2 * XS, WS = BF * 128;               // 2 stages
+  static constexpr int I0 = W0 + 2 * WS, IS = QRp * 128;         // 2 stages
+  static constexpr int H0 = I0 + 2 * IS, HS = 128;               // 2 stages
+  static constexpr int T0 = H0 + 2 * HS;                         // 4 KB table
+  static constexpr int R0 = T0 + 4096;                           // CSR row pointers
+  static constexpr int M0 = R0 + ((QR + 1) * 4 + 15) / 16 * 16;  // per-wave max |h|
+  static constexpr int C0 = M0 + 64;                             // staged entry columns
+  static constexpr int kEnt = ((kLds - C0) / 20) / 16 * 16;      // 2320 (BF 160), 992 (BF 256)
+  static constexpr int O0 = C0 + kEnt * 4;                       // staged entry O values
+  static constexpr int Bytes = O0 + kEnt * 16;
+  static_assert(Bytes <= kLds, "LDS budget");
+};
+}  // namespace g3
+
+template <int BF>
+__global__ __launch_bounds__(512, 2) void k_gemm_lds_e8d4(LinearArgs a, int OB) {
+  using L = g3::Lay<BF>;
+  constexpr int kBK = g3::kBK, kBT = g3::kBT;
+  constexpr int QR = L::QR, QRp = L::QRp, kEnt = L::kEnt;
+  constexpr int FW = BF / 2, FA = FW / 16, TW = kBT / 4, TB = TW / 16;
+  static_assert(QR % 4 == 0 && FW % 16 == 0, "whole decode waves and MFMA tiles");
+  extern __shared__ __attribute__((aligned(1024))) char smem[];
+  int* const rps = (int*)(smem + L::R0);
+  float* const wmx = (float*)(smem + L::M0);
+  int* const ecol = (int*)(smem + L::C0);
+  u32x4* const eov = (u32x4*)(smem + L::O0);
+  char* const tabB = smem + L::T0;
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int N = a.N, T = a.B, ldx = a.ldx;
+  // Workgroups are dealt to the 8 XCDs round-robin: give each XCD a run of
+  // consecutive tiles (same token tile, neighbouring feature tiles).
+  int blk = blockIdx.x;
+  const int G = gridDim.x;
+  if ((G & 7) == 0) blk = (blk & 7) * (G >> 3) + (blk >> 3);
+  const int ob = blk % OB, tb = blk / OB;
+  const int m0 = ob * QR, f0 = 8 * m0, t0 = tb * kBT;
+  const int nk = N / kBK, nch = N / 8;
+
+  // ---- table scaled by 2^-e (2^e >= max |h|), CSR rows, staged entries ----
+  const f16x4 tl = ((const f16x4*)a.codes)[tid];   // 512 threads, 512 rows
+  if (tid <= QR) rps[tid] = a.O_row_ptr[m0 + tid];
+  float mx = 0.0f;
+  for (int c = tid; c < nch; c += 512) {
+    const f16x8 hf = ((const f16x8*)a.h)[c];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) mx = fmaxf(mx, fabsf((float)hf[e]));
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+  if (lane == 0) wmx[wave] = mx;
+  __syncthreads();
+  mx = wmx[0];
+#pragma unroll
+  for (int w = 1; w < 8; ++w) mx = fmaxf(mx, wmx[w]);
+  int ex = 0;
+  if (mx > 1.0f) ex = (int)((__builtin_bit_cast(uint32_t, mx) >> 23) & 0xff) - 126;
+  const float out_scale = __builtin_ldexpf(1.0f, ex);
+  const f16 down = (f16)__builtin_ldexpf(1.0f, -ex);
+  const uint32_t down2 = __builtin_bit_cast(uint32_t, (h2){down, down});
+  {
+    u32x2 tw = __builtin_bit_cast(u32x2, tl);
+    tw[0] = gpk_mul(tw[0], down2);
+    tw[1] = gpk_mul(tw[1], down2);
+    *(u32x2*)(tabB + 8 * (tid ^ 0x100)) = tw;
+  }
+  const int e0 = rps[0];
+  const int nst = rps[QR] - e0 < kEnt ? rps[QR] - e0 : kEnt;
+  for (int e = tid; e < nst; e += 512) {
+    ecol[e] = a.O_col[e0 + e];
+    eov[e] = ((const u32x4*)a.O)[e0 + e];
+  }
+
+  // ---- LDS DMA.  Wave instruction j of a tile covers rows 8j .. 8j+7; lane
+  // l loads the 16 bytes that land at byte 16l of that kilobyte. ----
+  auto issue_x = [&](int s, int st) {
+    char* base = smem + L::X0 + st * L::XS;
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      const int j = p * 8 + wave;
+      const int r = 8 * j + (lane >> 3);
+      const int c = (lane & 7) ^ ((r >> 1) & 7);
+      const int tt = t0 + r < T ? t0 + r : T - 1;
+      __builtin_amdgcn_global_load_lds((const void*)(a.x + (size_t)tt * ldx + s * kBK + 8 * c),
+                                       (__attribute__((address_space(3))) void*)(base + j * 1024), 16, 0, 0);
+    }
+  };
+  auto issue_i = [&](int s, int st) {
+    if (wave < QRp / 8) {
+      const int r = 8 * wave + (lane >> 3);
+      const int rr = r < QR ? r : QR - 1;   // rows past QR: loaded, never read
+      __builtin_amdgcn_global_load_lds((const void*)(a.Q + (size_t)(m0 + rr) * N + s * kBK + 8 * (lane & 7)),
+                                       (__attribute__((address_space(3))) void*)(smem + L::I0 + st * L::IS + wave * 1024),
+                                       16, 0, 0);
+    } else if (wave == QRp / 8 && lane < 8) {
+      __builtin_amdgcn_global_load_lds((const void*)(a.h + s * kBK + 8 * lane),
+                                       (__attribute__((address_space(3))) void*)(smem + L::H0 + st * L::HS), 16, 0, 0);
+    }
+  };
+
+  // ---- decode: lane (8-column group dg, half dh, Q-row 4·wave + lane/16) of
+  // waves 0 .. QR/4 - 1 ----
+  const int dg = lane & 7, dh = (lane >> 3) & 1;
+  const int dq = 4 * wave + (lane >> 4);
+  const bool dact = 4 * wave < QR;   // wave-uniform
+  const mdec::Half half(dh);
+  int ec = 0, ee = 0, ncol = 0x7fffffff;
+  if (dact) {
+    ec = rps[dq] - e0;
+    ee = rps[dq + 1] - e0 < kEnt ? rps[dq + 1] - e0 : kEnt;
+  }
+  auto decode = [&](int s, int st) {
+    if (!dact) return;
+    const u32x4 qv = *(const u32x4*)(smem + L::I0 + st * L::IS + dq * 128 + 16 * dg);
+    const u32x4 hv = *(const u32x4*)(smem + L::H0 + st * L::HS + 16 * dg);
+    u32x2 lo[4], hi[4];
+    half.lookup(qv, tabB, lo, hi);
+    const int klo = s * kBK + 8 * dg;
+    while (ncol < klo + 8) {   // critical blocks at this lane's 8 columns
+      if (ncol >= klo) {
+        const u32x4 o = eov[ec];
+        u32x2 oh = dh ? (u32x2){o[2], o[3]} : (u32x2){o[0], o[1]};
+        oh[0] = gpk_mul(oh[0], down2);
+        oh[1] = gpk_mul(oh[1], down2);
+        const int jc = ncol - klo;
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+          if (jc == 2 * d) lo[d] = oh;
+          if (jc == 2 * d + 1) hi[d] = oh;
+        }
+      }
+      ++ec;
+      ncol = ec < ee ? ecol[ec] : 0x7fffffff;
+    }
+    char* wb = smem + L::W0 + (s & 1) * L::WS;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      u32x4 aw = mdec::Half::operand(lo, hi, c);
+#pragma unroll
+      for (int d = 0; d < 4; ++d) aw[d] = gpk_mul(aw[d], hv[d]);
+      *(u32x4*)(wb + g3::wpos(8 * dq + 4 * dh + c, dg)) = aw;
+    }
+  };
+
+  const int wf = wave & 1, wt = wave >> 1;
+  const int i = lane & 15, kg = lane >> 4;
+  f32x4 acc[FA][TB];
+#pragma unroll
+  for (int x = 0; x < FA; ++x)
+#pragma unroll
+    for (int q = 0; q < TB; ++q) acc[x][q] = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+  issue_x(0, 0);
+  issue_i(0, 0);
+  if (nk > 1) issue_i(1, 1);
+  __syncthreads();   // table, entries, row pointers
+  if (dact) ncol = ec < ee ? ecol[ec] : 0x7fffffff;
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  decode(0, 0);
+
+  for (int kt = 0; kt < nk; ++kt) {
+    // X(kt), indices(kt+1) and W(kt) are in LDS after this barrier; X(kt-1)
+    // and W(kt-1) are no longer read.
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    if (kt + 1 < nk) issue_x(kt + 1, (kt + 1) & 1);
+    if (kt + 2 < nk) issue_i(kt + 2, kt & 1);
+    if (kt + 1 < nk) decode(kt + 1, (kt + 1) & 1);
+    const char* xb = smem + L::X0 + (kt & 1) * L::XS;
+    const char* wb = smem + L::W0 + (kt & 1) * L::WS;
+    f16x8 af[2][FA], bf[2][TB];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+      for (int x = 0; x < FA; ++x) af[ks][x] = *(const f16x8*)(wb + g3::wpos(wf * FW + 16 * x + i, 4 * ks + kg));
+#pragma unroll
+      for (int q = 0; q < TB; ++q) bf[ks][q] = *(const f16x8*)(xb + g3::xpos(wt * TW + 16 * q + i, 4 * ks + kg));
+    }
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int x = 0; x < FA; ++x)
+#pragma unroll
+        for (int q = 0; q < TB; ++q)
+          acc[x][q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[ks][x], bf[ks][q], acc[x][q], 0, 0, 0);
+  }
+
+  // ---- entries past the LDS stage: the loop used table row 511 at their
+  // columns; add (fp16(O·2^-e·h) - fp16(row511·h)) · x per output row ----
+  if (rps[QR] - e0 > kEnt) {
+    const f16x4 t5 = *(const f16x4*)(tabB + 8 * (511 ^ 0x100));   // scaled by 2^-e
+    const int lg = lane >> 4;
+    for (int q = 0; q < QR; ++q) {
+      const int fl0 = 8 * q - wf * FW;   // the block's first feature in this wave's range
+      if (fl0 < 0 || fl0 >= FW) continue;
+      const int elo = rps[q] - e0 > kEnt ? rps[q] - e0 : kEnt;
+      const int ehi = rps[q + 1] - e0;
+      for (int e = elo; e < ehi; ++e) {
+        const int col = a.O_col[e0 + e];
+        const f16x8 o = ((const f16x8*)a.O)[e0 + e];
+        const f16 hc = __builtin_bit_cast(f16, a.h[col]);
+        float dv[4];   // this lane's 4 features 16·(fl0/16) + 4·lg + v
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int k = 4 * lg + v - (fl0 & 15);
+          float d = 0.0f;
+#pragma unroll
+          for (int kk = 0; kk < 8; ++kk)
+            if (kk == k) d = (float)(f16)((f16)(o[kk] * down) * hc) - (float)(f16)(t5[kk & 3] * hc);
+          dv[v] = d;
+        }
+#pragma unroll
+        for (int x = 0; x < FA; ++x) {
+          if (x != (fl0 >> 4)) continue;
+#pragma unroll
+          for (int q2 = 0; q2 < TB; ++q2) {
+            const int tt = t0 + wt * TW + 16 * q2 + i < T ? t0 + wt * TW + 16 * q2 + i : T - 1;
+            const float xv = (float)__builtin_bit_cast(f16, a.x[(size_t)tt * ldx + col]);
+#pragma unroll
+            for (int v = 0; v < 4; ++v) acc[x][q2][v] += dv[v] * xv;
+          }
+        }
+      }
+    }
+  }
+
+  // ---- y = acc·2^e·g + bias: lane (n, lg) holds 4 consecutive features of token n ----
+#pragma unroll
+  for (int x = 0; x < FA; ++x) {
+    const int f = f0 + wf * FW + 16 * x + 4 * kg;
+    const f16x4 g4 = *(const f16x4*)(a.g + f);
+    f16x4 b4 = {};
+    if (a.bias) b4 = *(const f16x4*)(a.bias + f);
+#pragma unroll
+    for (int q = 0; q < TB; ++q) {
+      const int tt = t0 + wt * TW + 16 * q + i;
+      if (tt >= T) continue;
+      f16x4 o;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) o[v] = (f16)(acc[x][q][v] * out_scale * (float)g4[v] + (float)b4[v]);
+      *(f16x4*)(a.y + (size_t)tt * a.ldy + f) = o;
+    }
+  }
+}
+
 template <bool HAS_S>
 __global__ __launch_bounds__(kGT, 2) void k_gemm_e8d4(LinearArgs a, int OB) {
   gemm_tile<KIND_E8D4, HAS_S>(a, OB);
@@ -668,6 +957,33 @@ int launch_gemm(const LinearArgs& a, hipStream_t s) {
       rc = launch_decode_mfma_multi(&t, 1, s);
     }
     if (rc == 0) return 0;
+  }
+  // LDS-decode kernel: fp16 x and table, no S_group, K-steps of 64, whole
+  // 20- or 32-Q-row tiles, 16-byte x rows and 8-byte y stores.  Of the two
+  // tile widths, the one with less work per CU (rounds of the CUs × tile
+  // width) wins; on a tie the wider tile.
+  if (KIND == KIND_E8D4 && !a.x_bf16 && !a.codes_f32 && !a.S && a.prep == 0 && (a.N % g3::kBK) == 0 &&
+      (a.ldx % 8) == 0 && ((uintptr_t)a.x & 15) == 0 && (a.ldy % 4) == 0 && ((uintptr_t)a.y & 7) == 0) {
+    const long TB = (a.B + g3::kBT - 1) / g3::kBT;
+    const long cus = dec::cu_count();
+    long cost160 = -1, cost256 = -1;
+    if (a.M % 20 == 0) cost160 = ((a.M / 20) * TB + cus - 1) / cus * 160;
+    if (a.M % 32 == 0) cost256 = ((a.M / 32) * TB + cus - 1) / cus * 256;
+    const int bf = cost160 < 0 ? (cost256 < 0 ? 0 : 256) : (cost256 < 0 || cost160 < cost256 ? 160 : 256);
+    const long grid = bf ? (a.M / (bf / 8)) * TB : 0;
+    if (bf && grid <= 0x7fffffff) {
+      const void* k = bf == 160 ? (const void*)k_gemm_lds_e8d4<160> : (const void*)k_gemm_lds_e8d4<256>;
+      const int bytes = bf == 160 ? g3::Lay<160>::Bytes : g3::Lay<256>::Bytes;
+      static bool attr[2] = {false, false};
+      bool& set = attr[bf == 160 ? 0 : 1];
+      if (!set) set = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, bytes) == hipSuccess;
+      if (set) {
+        const int OB = a.M / (bf / 8);
+        if (bf == 160) k_gemm_lds_e8d4<160><<<(unsigned)grid, 512, bytes, s>>>(a, OB);
+        else k_gemm_lds_e8d4<256><<<(unsigned)grid, 512, bytes, s>>>(a, OB);
+        return 0;
+      }
+    }
   }
   // MFMA path: fp16 activations, fp16 table, whole 16-Q-row tiles, K-steps
   // of 32.  Anything else takes batch tiles of the decode matvec.

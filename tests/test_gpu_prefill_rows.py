@@ -1,8 +1,9 @@
 """GPU parity of the prefill GEMM with the weights decoded in registers
-(``k_gemm_rows_e8d4``: E8-D4, fp16, no S_group, more than 128 tokens,
-out_features a multiple of 256; four-wave workgroups of 256 features, or
-five-wave ones of 320 when the layer fits one round of the CUs) through the
-C ABI's ``eptq_e8d4_forward``.
+(``k_gemm_rows_e8d4``: E8-D4, no S_group, more than 128 tokens, out_features
+a multiple of 256; four-wave workgroups of 256 features, or five-wave ones of
+320 when the layer fits one round of the CUs) through the C ABI's
+``eptq_e8d4_forward``.  fp16 layers reach it when in_features is not a
+multiple of 64 (the LDS-decode kernel takes the rest); bf16 layers always.
 
 Every case is within 1e-2 relative L2 of the fp32 reconstruct + matmul
 oracle (``dequantize_layer`` W, then an fp32 product).  The cases cover
@@ -31,13 +32,13 @@ pytestmark = pytest.mark.gpu
 TOL = 1e-2
 
 CASES = [
-    # out, in, tokens, critical-block fraction, bias
-    (1024, 2048, 300, 0.002, True),
+    # out, in (an odd number of 32-column steps), tokens, critical-block fraction, bias
+    (1024, 2080, 300, 0.002, True),
     (512, 1056, 257, 0.15, False),     # ~5000 entries per workgroup: past the LDS stage
-    (256, 4096, 129, 0.0, True),       # no critical blocks
-    (2048, 1024, 640, 0.01, False),
-    (640, 1024, 300, 0.01, True),      # five-wave workgroups (80 Q-rows: two of 40)
-    (640, 1024, 200, 0.1, False),      # five-wave, ~4000 entries per workgroup: past its 2048 in LDS
+    (256, 4128, 129, 0.0, True),       # no critical blocks
+    (2048, 1056, 640, 0.01, False),
+    (640, 1056, 300, 0.01, True),      # five-wave workgroups (80 Q-rows: two of 40)
+    (640, 1056, 200, 0.1, False),      # five-wave, ~4200 entries per workgroup: past its 2048 in LDS
 ]
 
 
