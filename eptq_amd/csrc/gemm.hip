@@ -3,12 +3,15 @@
 // Counterpart of the reference's large-batch path e8d4_wmma_v2_kernel +
 // at::mul(x, h) (csrc/eptq_kernels.cu:309-461, :520-537), rebuilt for gfx950
 // MFMA.  The contraction is a genuine dense GEMM on v_mfma_f32_16x16x32_f16.
-// Two kernels:
-//  * k_gemm_rows_e8d4 (E8-D4 without S_group, the Llama prefill case): each
-//    wave decodes its 64 rows of the weight straight into MFMA A operands in
-//    registers and the workgroup shares an activation tile in LDS (its own
-//    comment below);
-//  * k_gemm_e8d4 / k_gemm_e8 (S_group layers, E8, shapes the first does not
+// Three kernels (each with its own comment below):
+//  * k_gemm_lds_e8d4 (E8-D4 without S_group, fp16 x, in_features a multiple
+//    of 64: the Llama prefill case): producer waves decode the weight tile
+//    into LDS and bring the activation tile in by LDS DMA while eight waves
+//    run the MFMAs;
+//  * k_gemm_rows_e8d4 (E8-D4 without S_group, bf16 x or in_features an odd
+//    multiple of 32): each wave decodes its 64 rows of the weight straight
+//    into MFMA A operands in registers;
+//  * k_gemm_e8d4 / k_gemm_e8 (S_group layers, E8, shapes the others do not
 //    take): the weight is dequantized tile by tile into LDS, as below.
 //
 // E8 layers (1 MB table, larger than LDS) gather each index's 16-byte table
@@ -648,30 +651,32 @@ __global__ __launch_bounds__(64 * kW, 8 / kW) void k_gemm_rows_e8d4(LinearArgs a
 // E8-D4 prefill GEMM with the weight tile decoded into LDS and the activation
 // tile brought in by LDS DMA (fp16 x, no S_group).
 //
-// A workgroup of 8 waves computes BF output features (BF/8 Q-rows) × 256
-// tokens; wave w owns features (w & 1)·BF/2 .. +BF/2 of tokens 64·(w >> 1)
-// .. +63 as (BF/32) × 4 tiles of v_mfma_f32_16x16x32_f16.  Per K-step of 64
-// columns:
-//  * X: 256 rows × 128 bytes of raw fp16 x, written to LDS by
-//    global_load_lds_dwordx4 (no register staging), double-buffered, rows
-//    XOR-swizzled by 16-byte chunk so the MFMA fragment reads (16 rows at one
-//    chunk) hit distinct banks;
-//  * the index tile (BF/8 Q-rows × 64 columns of int16) and the step's 64 h
-//    values, also by LDS DMA, two steps ahead;
-//  * W: lane (8-column group, half, Q-row) of waves 0 .. BF/32 - 1 decodes 8
-//    indices through the LDS table (8 lookups, the matrix-core decode's
-//    operand mapping), replaces critical blocks from the workgroup's CSR
-//    entries staged in LDS (a per-lane cursor), multiplies by h and writes 4
-//    rows × 8 columns of fp16 W·h·2^-e, one step ahead of the MFMAs, into a
-//    double-buffered tile whose layout spreads each row's chunks over both
-//    halves of a 256-byte bank row (conflict-free writes and reads).
-// h sits on the weight side and the table is scaled by 2^-e once (2^e ≥
-// max|h|, so W·h·2^-e cannot overflow fp16); y = acc·2^e·g + bias.  Entries
-// past the LDS stage keep table row 511 in the loop and are corrected after
-// it.  One workgroup per CU (LDS), one barrier per K-step.
+// A workgroup of 12 waves computes BF output features (BF/8 Q-rows) × 256
+// tokens.  Waves 0-7 only multiply: wave w owns features (w & 1)·BF/2 ..
+// +BF/2 of tokens 64·(w >> 1) .. +63 as (BF/32) × 4 tiles of
+// v_mfma_f32_16x16x32_f16, reading both operands from LDS.  Waves 8-11 (one
+// per SIMD) produce, one K-step of 64 columns ahead:
+//  * X: 256 rows × 128 bytes of raw fp16 x written to LDS by
+//    global_load_lds_dwordx4 (no register staging), rows XOR-swizzled by
+//    16-byte chunk so the MFMA fragment reads (16 rows at one chunk) hit
+//    distinct banks; the index tile (BF/8 Q-rows × 64 int16) and the step's
+//    64 h values the same way;
+//  * W: each lane decodes units of 8 indices × one half (rows 0-3 or 4-7) of
+//    an 8-row block through the LDS table (8 lookups, the matrix-core decode's
+//    operand mapping), multiplies by h and writes 4 rows × 8 columns of fp16
+//    W·h·2^-e into a tile whose layout spreads each row's chunks over both
+//    halves of a 256-byte bank row (conflict-free writes and reads); critical
+//    blocks are then patched in from the workgroup's CSR entries staged in
+//    LDS (a per-lane cursor).
+// X, W, indices and h are double-buffered; one barrier per K-step.  h sits on
+// the weight side and the table is scaled by 2^-e once (2^e ≥ max|h|, so
+// W·h·2^-e cannot overflow fp16); y = acc·2^e·g + bias.  Entries past the LDS
+// stage keep table row 511 in the loop and are corrected after it.  One
+// workgroup per CU (LDS).
 namespace g3 {
-constexpr int kBK = 64;     // columns per K-step: 128-byte rows
-constexpr int kBT = 256;    // tokens per workgroup
+constexpr int kBK = 64;      // columns per K-step: 128-byte rows
+constexpr int kBT = 256;     // tokens per workgroup
+constexpr int kThreads = 768;
 constexpr int kLds = 160 * 1024;
 __device__ __forceinline__ int xpos(int t, int c) { return t * 128 + ((c ^ ((t >> 1) & 7)) << 4); }
 // Row r's 16-byte chunk c: the chunks of rows r and r ^ 1 alternate across the
@@ -685,14 +690,14 @@ __device__ __forceinline__ int wpos(int r, int c) {
 template <int BF> struct Lay {
   static constexpr int QR = BF / 8, QRp = (QR + 7) / 8 * 8;
   static constexpr int X0 = 0, XS = kBT * 128;                   // 2 stages
-  static constexpr int W0 = 2 * XS, WS = BF * 128;               // 2 stages
-  static constexpr int I0 = W0 + 2 * WS, IS = QRp * 128;         // 2 stages
+  static constexpr int W0 = 2 * XS, WS = BF * 128;               // 2 stages, then 1 KB for idle lanes' writes
+  static constexpr int I0 = W0 + 2 * WS + 1024, IS = QRp * 128;  // 2 stages
   static constexpr int H0 = I0 + 2 * IS, HS = 128;               // 2 stages
   static constexpr int T0 = H0 + 2 * HS;                         // 4 KB table
   static constexpr int R0 = T0 + 4096;                           // CSR row pointers
   static constexpr int M0 = R0 + ((QR + 1) * 4 + 15) / 16 * 16;  // per-wave max |h|
   static constexpr int C0 = M0 + 64;                             // staged entry columns
-  static constexpr int kEnt = ((kLds - C0) / 20) / 16 * 16;      // 2320 (BF 160), 992 (BF 256)
+  static constexpr int kEnt = ((kLds - C0) / 20) / 16 * 16;      // 2272 (BF 160), 944 (BF 256)
   static constexpr int O0 = C0 + kEnt * 4;                       // staged entry O values
   static constexpr int Bytes = O0 + kEnt * 16;
   static_assert(Bytes <= kLds, "LDS budget");
@@ -700,12 +705,12 @@ template <int BF> struct Lay {
 }  // namespace g3
 
 template <int BF>
-__global__ __launch_bounds__(512, 2) void k_gemm_lds_e8d4(LinearArgs a, int OB) {
+__global__ __launch_bounds__(g3::kThreads, 3) void k_gemm_lds_e8d4(LinearArgs a, int OB) {
   using L = g3::Lay<BF>;
-  constexpr int kBK = g3::kBK, kBT = g3::kBT;
+  constexpr int kBK = g3::kBK, kBT = g3::kBT, kNT = g3::kThreads;
   constexpr int QR = L::QR, QRp = L::QRp, kEnt = L::kEnt;
   constexpr int FW = BF / 2, FA = FW / 16, TW = kBT / 4, TB = TW / 16;
-  static_assert(QR % 4 == 0 && FW % 16 == 0, "whole decode waves and MFMA tiles");
+  static_assert(FW % 16 == 0 && QRp <= 32, "whole MFMA tiles, index tile in 4 DMA rows of waves");
   extern __shared__ __attribute__((aligned(1024))) char smem[];
   int* const rps = (int*)(smem + L::R0);
   float* const wmx = (float*)(smem + L::M0);
@@ -726,10 +731,10 @@ __global__ __launch_bounds__(512, 2) void k_gemm_lds_e8d4(LinearArgs a, int OB) 
   const int nk = N / kBK, nch = N / 8;
 
   // ---- table scaled by 2^-e (2^e >= max |h|), CSR rows, staged entries ----
-  const f16x4 tl = ((const f16x4*)a.codes)[tid];   // 512 threads, 512 rows
+  const f16x4 tl = ((const f16x4*)a.codes)[tid & 511];
   if (tid <= QR) rps[tid] = a.O_row_ptr[m0 + tid];
   float mx = 0.0f;
-  for (int c = tid; c < nch; c += 512) {
+  for (int c = tid; c < nch; c += kNT) {
     const f16x8 hf = ((const f16x8*)a.h)[c];
 #pragma unroll
     for (int e = 0; e < 8; ++e) mx = fmaxf(mx, fabsf((float)hf[e]));
@@ -740,13 +745,13 @@ __global__ __launch_bounds__(512, 2) void k_gemm_lds_e8d4(LinearArgs a, int OB) 
   __syncthreads();
   mx = wmx[0];
 #pragma unroll
-  for (int w = 1; w < 8; ++w) mx = fmaxf(mx, wmx[w]);
+  for (int w = 1; w < kNT / 64; ++w) mx = fmaxf(mx, wmx[w]);
   int ex = 0;
   if (mx > 1.0f) ex = (int)((__builtin_bit_cast(uint32_t, mx) >> 23) & 0xff) - 126;
   const float out_scale = __builtin_ldexpf(1.0f, ex);
   const f16 down = (f16)__builtin_ldexpf(1.0f, -ex);
   const uint32_t down2 = __builtin_bit_cast(uint32_t, (h2){down, down});
-  {
+  if (tid < 512) {
     u32x2 tw = __builtin_bit_cast(u32x2, tl);
     tw[0] = gpk_mul(tw[0], down2);
     tw[1] = gpk_mul(tw[1], down2);
@@ -754,82 +759,127 @@ __global__ __launch_bounds__(512, 2) void k_gemm_lds_e8d4(LinearArgs a, int OB) 
   }
   const int e0 = rps[0];
   const int nst = rps[QR] - e0 < kEnt ? rps[QR] - e0 : kEnt;
-  for (int e = tid; e < nst; e += 512) {
+  for (int e = tid; e < nst; e += kNT) {
     ecol[e] = a.O_col[e0 + e];
     eov[e] = ((const u32x4*)a.O)[e0 + e];
   }
 
-  // ---- LDS DMA.  Wave instruction j of a tile covers rows 8j .. 8j+7; lane
-  // l loads the 16 bytes that land at byte 16l of that kilobyte. ----
-  auto issue_x = [&](int s, int st) {
-    char* base = smem + L::X0 + st * L::XS;
+  if (wave >= 8) {
+    // ================= producer waves 8-11 =================
+    const int dw = wave - 8;
+    // LDS DMA: wave instruction j of a tile covers rows 8j .. 8j+7; lane l
+    // loads the 16 bytes that land at byte 16l of that kilobyte.
+    auto issue_x = [&](int s, int st) {
+      char* base = smem + L::X0 + st * L::XS;
 #pragma unroll
-    for (int p = 0; p < 4; ++p) {
-      const int j = p * 8 + wave;
-      const int r = 8 * j + (lane >> 3);
-      const int c = (lane & 7) ^ ((r >> 1) & 7);
-      const int tt = t0 + r < T ? t0 + r : T - 1;
-      __builtin_amdgcn_global_load_lds((const void*)(a.x + (size_t)tt * ldx + s * kBK + 8 * c),
-                                       (__attribute__((address_space(3))) void*)(base + j * 1024), 16, 0, 0);
-    }
-  };
-  auto issue_i = [&](int s, int st) {
-    if (wave < QRp / 8) {
-      const int r = 8 * wave + (lane >> 3);
-      const int rr = r < QR ? r : QR - 1;   // rows past QR: loaded, never read
-      __builtin_amdgcn_global_load_lds((const void*)(a.Q + (size_t)(m0 + rr) * N + s * kBK + 8 * (lane & 7)),
-                                       (__attribute__((address_space(3))) void*)(smem + L::I0 + st * L::IS + wave * 1024),
-                                       16, 0, 0);
-    } else if (wave == QRp / 8 && lane < 8) {
-      __builtin_amdgcn_global_load_lds((const void*)(a.h + s * kBK + 8 * lane),
-                                       (__attribute__((address_space(3))) void*)(smem + L::H0 + st * L::HS), 16, 0, 0);
-    }
-  };
-
-  // ---- decode: lane (8-column group dg, half dh, Q-row 4·wave + lane/16) of
-  // waves 0 .. QR/4 - 1 ----
-  const int dg = lane & 7, dh = (lane >> 3) & 1;
-  const int dq = 4 * wave + (lane >> 4);
-  const bool dact = 4 * wave < QR;   // wave-uniform
-  const mdec::Half half(dh);
-  int ec = 0, ee = 0, ncol = 0x7fffffff;
-  if (dact) {
-    ec = rps[dq] - e0;
-    ee = rps[dq + 1] - e0 < kEnt ? rps[dq + 1] - e0 : kEnt;
-  }
-  auto decode = [&](int s, int st) {
-    if (!dact) return;
-    const u32x4 qv = *(const u32x4*)(smem + L::I0 + st * L::IS + dq * 128 + 16 * dg);
-    const u32x4 hv = *(const u32x4*)(smem + L::H0 + st * L::HS + 16 * dg);
-    u32x2 lo[4], hi[4];
-    half.lookup(qv, tabB, lo, hi);
-    const int klo = s * kBK + 8 * dg;
-    while (ncol < klo + 8) {   // critical blocks at this lane's 8 columns
-      if (ncol >= klo) {
-        const u32x4 o = eov[ec];
-        u32x2 oh = dh ? (u32x2){o[2], o[3]} : (u32x2){o[0], o[1]};
-        oh[0] = gpk_mul(oh[0], down2);
-        oh[1] = gpk_mul(oh[1], down2);
-        const int jc = ncol - klo;
+      for (int p = 0; p < 8; ++p) {
+        const int j = 4 * p + dw;
+        const int r = 8 * j + (lane >> 3);
+        const int c = (lane & 7) ^ ((r >> 1) & 7);
+        const int tt = t0 + r < T ? t0 + r : T - 1;
+        __builtin_amdgcn_global_load_lds((const void*)(a.x + (size_t)tt * ldx + s * kBK + 8 * c),
+                                         (__attribute__((address_space(3))) void*)(base + j * 1024), 16, 0, 0);
+      }
+    };
+    auto issue_i = [&](int s, int st) {
+      if (dw < QRp / 8) {
+        const int r = 8 * dw + (lane >> 3);
+        const int rr = r < QR ? r : QR - 1;   // rows past QR: loaded, never read
+        __builtin_amdgcn_global_load_lds((const void*)(a.Q + (size_t)(m0 + rr) * N + s * kBK + 8 * (lane & 7)),
+                                         (__attribute__((address_space(3))) void*)(smem + L::I0 + st * L::IS + dw * 1024),
+                                         16, 0, 0);
+      }
+      if (dw == 3 && lane < 8) {
+        __builtin_amdgcn_global_load_lds((const void*)(a.h + s * kBK + 8 * lane),
+                                         (__attribute__((address_space(3))) void*)(smem + L::H0 + st * L::HS), 16, 0, 0);
+      }
+    };
+    // Decode units (Q-row, 8-column group, half): 4·QR per producer wave in NP
+    // passes of 64 lanes; lanes past a wave's units repeat one of its units
+    // (same LDS addresses, so no extra bank conflicts) and write to a
+    // scratch slot.
+    constexpr int UPD = 4 * QR, NP = (UPD + 63) / 64;
+    int dq[NP], dg[NP], dh[NP], ec[NP], ee[NP], ncol[NP];
+    bool twin[NP];
 #pragma unroll
-        for (int d = 0; d < 4; ++d) {
-          if (jc == 2 * d) lo[d] = oh;
-          if (jc == 2 * d + 1) hi[d] = oh;
+    for (int p = 0; p < NP; ++p) {
+      const int l = 64 * p + lane;
+      twin[p] = l >= UPD;
+      const int u = dw * UPD + (twin[p] ? 64 * p + (lane & 15) : l);
+      dq[p] = u >> 4; dh[p] = (u >> 3) & 1; dg[p] = u & 7;
+      ec[p] = 0; ee[p] = 0;
+      if (!twin[p]) {
+        ec[p] = rps[dq[p]] - e0;
+        ee[p] = rps[dq[p] + 1] - e0 < kEnt ? rps[dq[p] + 1] - e0 : kEnt;
+      }
+    }
+    // All passes' index/h reads and table lookups first (one dependency chain
+    // per wave), then the arithmetic and writes, then the rare critical blocks
+    // patched in after the lane's own writes.
+    auto decode = [&](int s, int st) {
+      u32x2 lo[NP][4], hi[NP][4];
+      u32x4 hv[NP];
+#pragma unroll
+      for (int p = 0; p < NP; ++p) {
+        const u32x4 qv = *(const u32x4*)(smem + L::I0 + st * L::IS + dq[p] * 128 + 16 * dg[p]);
+        hv[p] = *(const u32x4*)(smem + L::H0 + st * L::HS + 16 * dg[p]);
+        const mdec::Half half(dh[p]);
+        half.lookup(qv, tabB, lo[p], hi[p]);
+      }
+      char* wb = smem + L::W0 + st * L::WS;
+#pragma unroll
+      for (int p = 0; p < NP; ++p) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          u32x4 aw = mdec::Half::operand(lo[p], hi[p], c);
+#pragma unroll
+          for (int d = 0; d < 4; ++d) aw[d] = gpk_mul(aw[d], hv[p][d]);
+          const int off = twin[p] ? (2 - st) * L::WS + 16 * lane : g3::wpos(8 * dq[p] + 4 * dh[p] + c, dg[p]);
+          *(u32x4*)(wb + off) = aw;
         }
       }
-      ++ec;
-      ncol = ec < ee ? ecol[ec] : 0x7fffffff;
-    }
-    char* wb = smem + L::W0 + (s & 1) * L::WS;
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      u32x4 aw = mdec::Half::operand(lo, hi, c);
+      for (int p = 0; p < NP; ++p) {
+        const int klo = s * kBK + 8 * dg[p];
+        while (ncol[p] < klo + 8) {
+          if (ncol[p] >= klo) {
+            const int jc = ncol[p] - klo;
+            const f16 hc = *(const f16*)(smem + L::H0 + st * L::HS + 2 * (8 * dg[p] + jc));
+            const f16x8 o = __builtin_bit_cast(f16x8, eov[ec[p]]);
 #pragma unroll
-      for (int d = 0; d < 4; ++d) aw[d] = gpk_mul(aw[d], hv[d]);
-      *(u32x4*)(wb + g3::wpos(8 * dq + 4 * dh + c, dg)) = aw;
-    }
-  };
+            for (int c = 0; c < 4; ++c)
+              *(f16*)(wb + g3::wpos(8 * dq[p] + 4 * dh[p] + c, dg[p]) + 2 * jc) =
+                  (f16)((f16)(o[4 * dh[p] + c] * down) * hc);
+          }
+          ++ec[p];
+          ncol[p] = ec[p] < ee[p] ? ecol[ec[p]] : 0x7fffffff;
+        }
+      }
+    };
 
+    issue_i(0, 0);
+    if (nk > 1) issue_i(1, 1);
+    issue_x(0, 0);
+    __syncthreads();   // table, entries, row pointers
+#pragma unroll
+    for (int p = 0; p < NP; ++p) ncol[p] = ec[p] < ee[p] ? ecol[ec[p]] : 0x7fffffff;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    decode(0, 0);
+    for (int kt = 0; kt < nk; ++kt) {
+      // Before the barrier: X(kt), indices(kt+1) landed, W(kt) written.
+      asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      if (kt + 2 < nk) issue_i(kt + 2, kt & 1);
+      if (kt + 1 < nk) {
+        issue_x(kt + 1, (kt + 1) & 1);
+        decode(kt + 1, (kt + 1) & 1);
+      }
+    }
+    return;
+  }
+
+  // ================= MFMA waves 0-7 =================
   const int wf = wave & 1, wt = wave >> 1;
   const int i = lane & 15, kg = lane >> 4;
   f32x4 acc[FA][TB];
@@ -837,25 +887,11 @@ __global__ __launch_bounds__(512, 2) void k_gemm_lds_e8d4(LinearArgs a, int OB) 
   for (int x = 0; x < FA; ++x)
 #pragma unroll
     for (int q = 0; q < TB; ++q) acc[x][q] = (f32x4){0.f, 0.f, 0.f, 0.f};
-
-  issue_x(0, 0);
-  issue_i(0, 0);
-  if (nk > 1) issue_i(1, 1);
-  __syncthreads();   // table, entries, row pointers
-  if (dact) ncol = ec < ee ? ecol[ec] : 0x7fffffff;
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
-  decode(0, 0);
-
+  __syncthreads();   // the producers' first barrier
   for (int kt = 0; kt < nk; ++kt) {
-    // X(kt), indices(kt+1) and W(kt) are in LDS after this barrier; X(kt-1)
-    // and W(kt-1) are no longer read.
-    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
-    if (kt + 1 < nk) issue_x(kt + 1, (kt + 1) & 1);
-    if (kt + 2 < nk) issue_i(kt + 2, kt & 1);
-    if (kt + 1 < nk) decode(kt + 1, (kt + 1) & 1);
     const char* xb = smem + L::X0 + (kt & 1) * L::XS;
     const char* wb = smem + L::W0 + (kt & 1) * L::WS;
     f16x8 af[2][FA], bf[2][TB];
@@ -979,8 +1015,8 @@ int launch_gemm(const LinearArgs& a, hipStream_t s) {
       if (!set) set = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, bytes) == hipSuccess;
       if (set) {
         const int OB = a.M / (bf / 8);
-        if (bf == 160) k_gemm_lds_e8d4<160><<<(unsigned)grid, 512, bytes, s>>>(a, OB);
-        else k_gemm_lds_e8d4<256><<<(unsigned)grid, 512, bytes, s>>>(a, OB);
+        if (bf == 160) k_gemm_lds_e8d4<160><<<(unsigned)grid, g3::kThreads, bytes, s>>>(a, OB);
+        else k_gemm_lds_e8d4<256><<<(unsigned)grid, g3::kThreads, bytes, s>>>(a, OB);
         return 0;
       }
     }
