@@ -66,3 +66,29 @@ def test_prefill_lds_kernel_matches_oracle(out, inp, T, p, bias, hs):
     print(f"  rel_l2 {e:.2e}", flush=True)
     assert np.isfinite(got).all()
     assert e <= TOL
+
+
+def test_prefill_lds_kernel_graph_replays_match_eager():
+    """Captured in a HIP graph, the kernel's replays (with new x copied in and
+    eager launches between them) equal eager launches bit for bit: it keeps no
+    state between calls and records no memset."""
+    out, inp, T = 1280, 1024, 300
+    print(f"prefill lds kernel graph replay {out}x{inp} T={T}", flush=True)
+    qd = make_layer(out, inp, seed=950, percmask=0.01, bias=True)
+    ocol, orp = csr_dev(qd.Q)
+    codes = torch.from_numpy(table("e8_d4", 1.75)).half().cuda()
+    args = [qd.Q.cuda(), codes, qd.g.cuda(), qd.h.cuda()]
+    rest = [qd.O.cuda(), ocol, orp, qd.bias.cuda(), None]
+    x_static = make_x(T, inp, seed=951).cuda()
+    linear_forward("e8_d4", *args, x_static, *rest)   # first call sets the LDS attribute
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        y_static = linear_forward("e8_d4", *args, x_static, *rest)
+    for rep in range(3):
+        x_new = make_x(T, inp, seed=960 + rep).cuda()
+        x_static.copy_(x_new)
+        g.replay()
+        eager = linear_forward("e8_d4", *args, x_new, *rest)
+        torch.cuda.synchronize()
+        assert torch.equal(y_static, eager), f"replay {rep} differs from the eager launch"
