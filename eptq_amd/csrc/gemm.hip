@@ -668,8 +668,7 @@ __global__ __launch_bounds__(64 * kW, 8 / kW) void k_gemm_rows_e8d4(LinearArgs a
 //    halves of a 256-byte bank row (conflict-free writes and reads); critical
 //    blocks are then patched in from the workgroup's CSR entries staged in
 //    LDS (a per-lane cursor).
-// W, indices and h are double-buffered, x double- or triple-buffered (XST;
-// with three stages x is requested two steps ahead); one barrier per K-step.  h sits on
+// X, W, indices and h are double-buffered; one barrier per K-step.  h sits on
 // the weight side and the table is scaled by 2^-e once (2^e ≥ max|h|, so
 // W·h·2^-e cannot overflow fp16); y = acc·2^e·g + bias.  Entries past the LDS
 // stage keep table row 511 in the loop and are corrected after it.  One
@@ -687,30 +686,30 @@ __device__ __forceinline__ int wpos(int r, int c) {
   const int b = (r ^ (r >> 2)) & 1;
   return (r >> 1) * 256 + (((2 * c + b) ^ (2 * ((r >> 1) & 7))) << 4);
 }
-template <int BF, int XST> struct Lay {
+template <int BF> struct Lay {
   static constexpr int QR = BF / 8, QRp = (QR + 7) / 8 * 8;
-  static constexpr int X0 = 0, XS = kBT * 128;                   // XST stages
-  static constexpr int W0 = XST * XS, WS = BF * 128;             // 2 stages, then 1 KB for idle lanes' writes
+  static constexpr int X0 = 0, XS = kBT * 128;                   // 2 stages
+  static constexpr int W0 = 2 * XS, WS = BF * 128;             // 2 stages, then 1 KB for idle lanes' writes
   static constexpr int I0 = W0 + 2 * WS + 1024, IS = QRp * 128;  // 2 stages
   static constexpr int H0 = I0 + 2 * IS, HS = 128;               // 2 stages
   static constexpr int T0 = H0 + 2 * HS;                         // 4 KB table
   static constexpr int R0 = T0 + 4096;                           // CSR row pointers
   static constexpr int M0 = R0 + ((QR + 1) * 4 + 15) / 16 * 16;  // per-wave max |h|
   static constexpr int C0 = M0 + 64;                             // staged entry columns
-  static constexpr int kEnt = ((kLds - C0) / 20) / 16 * 16;      // 2272 / 640 (BF 160, 2 / 3 X stages), 944 (BF 256)
+  static constexpr int kEnt = ((kLds - C0) / 20) / 16 * 16;      // 2272 (BF 160), 944 (BF 256)
   static constexpr int O0 = C0 + kEnt * 4;                       // staged entry O values
   static constexpr int Bytes = O0 + kEnt * 16;
   static_assert(Bytes <= kLds, "LDS budget");
 };
 }  // namespace g3
 
-// NPW producer waves (4 or 8; 8 when the MFMA waves' registers allow four
-// waves per SIMD), XST x stages (3: x requested two steps ahead).
-template <int BF, int NPW, int XST>
+// NPW producer waves: 4, or 8 when the MFMA waves' registers allow four
+// waves per SIMD.
+template <int BF, int NPW>
 __global__ __launch_bounds__(64 * (8 + NPW), (8 + NPW) / 4) void k_gemm_lds_e8d4(LinearArgs a, int OB) {
-  using L = g3::Lay<BF, XST>;
+  using L = g3::Lay<BF>;
   constexpr int kBK = g3::kBK, kBT = g3::kBT, kNT = 64 * (8 + NPW);
-  static_assert((NPW == 4 || NPW == 8) && (XST == 2 || XST == 3), "producer waves, x stages");
+  static_assert(NPW == 4 || NPW == 8, "producer waves");
   constexpr int QR = L::QR, QRp = L::QRp, kEnt = L::kEnt;
   constexpr int FW = BF / 2, FA = FW / 16, TW = kBT / 4, TB = TW / 16;
   static_assert(FW % 16 == 0 && QRp <= 32, "whole MFMA tiles, index tile in 4 DMA rows of waves");
@@ -865,23 +864,21 @@ __global__ __launch_bounds__(64 * (8 + NPW), (8 + NPW) / 4) void k_gemm_lds_e8d4
     issue_i(0, 0);
     if (nk > 1) issue_i(1, 1);
     issue_x(0, 0);
-    if (XST == 3 && nk > 1) issue_x(1, 1);
     __syncthreads();   // table, entries, row pointers
 #pragma unroll
     for (int p = 0; p < NP; ++p) ncol[p] = ec[p] < ee[p] ? ecol[ec[p]] : 0x7fffffff;
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     decode(0, 0);
     for (int kt = 0; kt < nk; ++kt) {
-      // Before the barrier: X(kt), indices(kt+1) landed, W(kt) written.  A
-      // step's indices go out before its x tile, so with three x stages the
-      // x tile issued last step (kXI instructions) may still be in flight.
-      if (XST == 3 && kt + 1 < nk) asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(kXI) : "memory");
-      else asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+      // Before the barrier: X(kt), indices(kt+1) landed, W(kt) written.
+      asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
       __builtin_amdgcn_s_barrier();
       asm volatile("" ::: "memory");
       if (kt + 2 < nk) issue_i(kt + 2, kt & 1);
-      if (kt + XST - 1 < nk) issue_x(kt + XST - 1, (kt + XST - 1) % XST);
-      if (kt + 1 < nk) decode(kt + 1, (kt + 1) & 1);
+      if (kt + 1 < nk) {
+        issue_x(kt + 1, (kt + 1) & 1);
+        decode(kt + 1, (kt + 1) & 1);
+      }
     }
     return;
   }
@@ -899,7 +896,7 @@ __global__ __launch_bounds__(64 * (8 + NPW), (8 + NPW) / 4) void k_gemm_lds_e8d4
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
-    const char* xb = smem + L::X0 + (kt % XST) * L::XS;
+    const char* xb = smem + L::X0 + (kt & 1) * L::XS;
     const char* wb = smem + L::W0 + (kt & 1) * L::WS;
     f16x8 af[2][FA], bf[2][TB];
 #pragma unroll
@@ -1016,20 +1013,16 @@ int launch_gemm(const LinearArgs& a, hipStream_t s) {
     const long grid = bf ? (a.M / (bf / 8)) * TB : 0;
     if (bf && grid <= 0x7fffffff) {
       // 160-feature tiles: 8 producer waves (the MFMA waves fit four waves per
-      // SIMD) and, up to 8192 columns, x two steps ahead (the third x stage
-      // leaves room for 640 staged critical blocks, 0.39% of 20 rows of 8192
-      // columns); 256-feature tiles: 4 producer waves, two x stages.
-      const int v = bf == 256 ? 0 : (a.N <= 8192 ? 2 : 1);
-      const void* kerns[3] = {(const void*)k_gemm_lds_e8d4<256, 4, 2>, (const void*)k_gemm_lds_e8d4<160, 8, 2>,
-                              (const void*)k_gemm_lds_e8d4<160, 8, 3>};
-      const int bytes[3] = {g3::Lay<256, 2>::Bytes, g3::Lay<160, 2>::Bytes, g3::Lay<160, 3>::Bytes};
-      static bool attr[3] = {false, false, false};
+      // SIMD); 256-feature tiles: 4.
+      const int v = bf == 256 ? 0 : 1;
+      const void* kerns[2] = {(const void*)k_gemm_lds_e8d4<256, 4>, (const void*)k_gemm_lds_e8d4<160, 8>};
+      const int bytes[2] = {g3::Lay<256>::Bytes, g3::Lay<160>::Bytes};
+      static bool attr[2] = {false, false};
       if (!attr[v]) attr[v] = hipFuncSetAttribute(kerns[v], hipFuncAttributeMaxDynamicSharedMemorySize, bytes[v]) == hipSuccess;
       if (attr[v]) {
         const int OB = a.M / (bf / 8);
-        if (v == 0) k_gemm_lds_e8d4<256, 4, 2><<<(unsigned)grid, 768, bytes[0], s>>>(a, OB);
-        else if (v == 1) k_gemm_lds_e8d4<160, 8, 2><<<(unsigned)grid, 1024, bytes[1], s>>>(a, OB);
-        else k_gemm_lds_e8d4<160, 8, 3><<<(unsigned)grid, 1024, bytes[2], s>>>(a, OB);
+        if (v == 0) k_gemm_lds_e8d4<256, 4><<<(unsigned)grid, 768, bytes[0], s>>>(a, OB);
+        else k_gemm_lds_e8d4<160, 8><<<(unsigned)grid, 1024, bytes[1], s>>>(a, OB);
         return 0;
       }
     }

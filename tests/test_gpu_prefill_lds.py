@@ -8,10 +8,9 @@ oracle (``dequantize_layer`` W, then an fp32 product).  The cases cover both
 tile widths (160 features when out_features / 160 gives fewer rounds of the
 CUs, else 256), token counts that are not a multiple of the 256-token tile,
 one and two K-steps, a bias, a layer with no critical block, workgroups whose
-critical blocks exceed the entries they stage in LDS (160-feature tiles: 640
-with the third x stage used up to 8192 columns, 2272 above; 256-feature
-tiles: 944; the rest are corrected after the K loop), and h below and far
-above 1 (the 2^-e scaling of the table).
+critical blocks exceed the entries they stage in LDS (2272 for 160-feature,
+944 for 256-feature tiles; the rest are corrected after the K loop), and h
+below and far above 1 (the 2^-e scaling of the table).
 """
 
 from __future__ import annotations
@@ -36,8 +35,8 @@ CASES = [
     (1280, 2048, 512, 0.002, True, 1.0),     # 160-feature tiles (8 of them beat 5 of 256)
     (1024, 2048, 300, 0.002, True, 1.0),     # 256-feature tiles (1024 / 160 is not whole)
     (512, 1024, 257, 0.15, False, 1.0),      # 256: ~4900 entries per workgroup, past its 944
-    (640, 1024, 200, 0.15, False, 1.0),      # 160, 3 x stages: ~3100 entries per workgroup, past its 640
-    (160, 8256, 129, 0.02, True, 1.0),       # 160, 2 x stages (past 8192 columns): ~3300 entries, past its 2272
+    (640, 1024, 200, 0.15, False, 1.0),      # 160: ~3100 entries per workgroup, past its 2272
+    (160, 8256, 129, 0.02, True, 1.0),       # 160, 129 K-steps: ~3300 entries, past its 2272
     (2560, 1024, 129, 0.0, True, 1.0),       # no critical blocks, one token past a tile
     (256, 64, 300, 0.01, False, 1.0),        # one K-step
     (160, 128, 1000, 0.01, True, 1.0),       # two K-steps, four token tiles
