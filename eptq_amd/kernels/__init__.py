@@ -26,16 +26,7 @@ from ._lib import EPTQ_BF16, EPTQ_F16, EPTQ_F32, EptqError
 
 __all__ = ["e8_forward", "e8d4_forward", "e8_forward_grouped", "e8d4_forward_grouped",
            "e8_dequant", "e8d4_dequant", "EptqError", "linear_forward", "linear_forward_multi",
-           "dequant", "dequant_linear", "decode_workspace", "PREFILL_DEQUANT_MIN_TOKENS"]
-
-# From this many fp16 tokens on, the module forward (``EPTQLinear``,
-# ``EPTQMultiLinear``) computes a prefill as the bit-exact fp16 W of every
-# layer (``dequant``) times x on the library fp16 GEMM (``dequant_linear``):
-# W is written once and read back once, which at these token counts costs far
-# less than the contraction, and the library GEMM runs the contraction faster
-# than the fused dequantize-into-LDS kernel.  Fewer tokens run the fused
-# kernels (no weight is materialized).
-PREFILL_DEQUANT_MIN_TOKENS = 64
+           "dequant", "decode_workspace"]
 
 
 def _ptr(t: Optional[torch.Tensor]):
@@ -174,32 +165,6 @@ def dequant(kind: str, Q, codes, g, h, O_vals, O_col, O_row_ptr, S_group=None,
                 _ptr(O_row_ptr), _ptr(S_group), n_groups, M, N, _ptr(W), stream)
     _lib.check(rc, fn.__name__)
     return W
-
-
-def dequant_linear(kind: str, layers, codes_f32, x) -> torch.Tensor:
-    """y = x·Wᵀ + bias for one or more layers that read the same x (outputs
-    side by side, as ``linear_forward_multi``), with W the bit-exact fp16
-    weights of ``dequantize_layer``: each layer's W is written by ``dequant``
-    into its rows of one stacked scratch, then one fp16 GEMM on the current
-    stream (torch's, fp32 accumulation).  The reference's dense path over the
-    reconstructed W (``reconstruct.py:229`` then ``F.linear``) computes the
-    same product.  x: (T, N) fp16; ``codes_f32``: the shared fp32 table."""
-    _require(x.dtype == torch.float16 and x.dim() == 2 and x.is_contiguous(),
-             "dequant_linear takes a contiguous fp16 (T, N) activation")
-    outs = [8 * int(l["Q"].shape[0]) for l in layers]
-    N = int(x.shape[1])
-    W = torch.empty((sum(outs), N), dtype=torch.float16, device=x.device)
-    r = 0
-    for l, o in zip(layers, outs):
-        dequant(kind, l["Q"], codes_f32, l["g"], l["h"], l["O_vals"], l["O_col"], l["O_row_ptr"],
-                l.get("S_group"), out=W[r:r + o])
-        r += o
-    bias = None
-    if any(l.get("bias") is not None and l["bias"].numel() for l in layers):
-        bias = torch.cat([l["bias"].to(torch.float16) if l.get("bias") is not None and l["bias"].numel()
-                          else torch.zeros(o, dtype=torch.float16, device=x.device)
-                          for l, o in zip(layers, outs)])
-    return torch.nn.functional.linear(x, W, bias)
 
 
 # ---------------------------------------------------------------------------

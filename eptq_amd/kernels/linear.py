@@ -14,11 +14,12 @@ Differences, all towards the reference's own reconstruct semantics:
   (``algorithms/eptq.py:432-457``) — the reference kernel path ignores it.
 * ``S_group`` layers stay compressed and run the fused grouped kernel instead
   of a materialized fp16 W (``kernels/linear.py:97-120,158-164``).
-* every batch size runs a HIP kernel (decode matvec for ≤16 rows, GEMM above);
-  ``EPTQ_CUDA_DECODE`` / ``EPTQ_FORCE_TRITON`` are accepted and ignored.  From
-  ``PREFILL_DEQUANT_MIN_TOKENS`` fp16 rows on, the forward is the bit-exact
-  dequantization kernel into an fp16 scratch W followed by the library fp16
-  GEMM (``dequant_linear``), faster than the fused prefill kernel there.
+* every batch size runs a hand-written HIP kernel of this library: the decode
+  matvec for ≤16 rows, 16-row slices of the matrix-core decode up to 128 rows,
+  the prefill GEMM that decodes weight tiles into LDS above (the reference's
+  ``csrc/eptq_kernels.cu:520-537`` route); no weight matrix is materialized
+  and no library GEMM runs.  ``EPTQ_CUDA_DECODE`` / ``EPTQ_FORCE_TRITON`` are
+  accepted and ignored.
 * ``dequantize()`` returns the bit-exact fp16 W of ``dequantize_layer`` from the
   GPU (needs the fp32 table, kept alongside the fp16 kernel table).
 """
@@ -33,7 +34,7 @@ import torch
 import torch.nn as nn
 
 from . import dequant as _dequant
-from . import PREFILL_DEQUANT_MIN_TOKENS, dequant_linear, linear_forward, linear_forward_multi
+from . import linear_forward, linear_forward_multi
 
 _KINDS = ("e8_lattice", "e8_d4")
 
@@ -173,9 +174,7 @@ class EPTQLinear(nn.Module):
             x2 = x2.contiguous()
         layer = dict(Q=self.Q, g=self.g, h=self.h, O_vals=self.O_vals, O_col=self.O_col,
                      O_row_ptr=self.O_row_ptr, bias=self.bias, S_group=self.S_group)
-        if x2.dtype == torch.float16 and x2.shape[0] >= PREFILL_DEQUANT_MIN_TOKENS:
-            y = dequant_linear(self.quantizer_type, [layer], self._table_f32, x2)
-        elif self._work is not None and self.quantizer_type == "e8_d4":
+        if self._work is not None and self.quantizer_type == "e8_d4":
             y = linear_forward_multi([layer], self._codebook, x2, work=self._work)
         else:
             y = linear_forward(self.quantizer_type, self.Q, self._codebook, self.g, self.h, x2,
@@ -226,10 +225,7 @@ class EPTQMultiLinear(nn.Module):
         x2 = x2.contiguous()
         layers = [dict(Q=l.Q, g=l.g, h=l.h, O_vals=l.O_vals, O_col=l.O_col, O_row_ptr=l.O_row_ptr,
                        bias=l.bias, S_group=l.S_group) for l in self.parts]
-        if x2.dtype == torch.float16 and x2.shape[0] >= PREFILL_DEQUANT_MIN_TOKENS:
-            y = dequant_linear("e8_d4", layers, self.parts[0]._table_f32, x2)
-        else:
-            y = linear_forward_multi(layers, self.parts[0]._codebook, x2, work=self._work)
+        y = linear_forward_multi(layers, self.parts[0]._codebook, x2, work=self._work)
         if y.dtype != out_dtype:
             y = y.to(out_dtype)
         return y.reshape(*shape[:-1], self.out_features)
