@@ -26,7 +26,7 @@ from ._lib import EPTQ_BF16, EPTQ_F16, EPTQ_F32, EptqError
 
 __all__ = ["e8_forward", "e8d4_forward", "e8_forward_grouped", "e8d4_forward_grouped",
            "e8_dequant", "e8d4_dequant", "EptqError", "linear_forward", "linear_forward_multi",
-           "dequant", "decode_workspace"]
+           "dequant", "decode_workspace", "stream_workspace"]
 
 
 def _ptr(t: Optional[torch.Tensor]):
@@ -103,6 +103,26 @@ def decode_workspace(device) -> torch.Tensor:
     with torch.cuda.device(device):
         n = int(_lib.load().eptq_e8d4_work_bytes())
     return torch.zeros(n, dtype=torch.uint8, device=device)
+
+
+# One split-K workspace per (device, stream): launches on one stream run one
+# after another, so modules that share their stream's workspace never overlap
+# on it.  Created on first use (zero-filled on that stream).
+_STREAM_WORK: dict = {}
+
+
+def stream_workspace(device) -> torch.Tensor:
+    """The decode workspace of the current stream on ``device`` (see
+    ``decode_workspace``), created on first use."""
+    device = torch.device(device)
+    stream = torch.cuda.current_stream(device)
+    key = (device.index if device.index is not None else torch.cuda.current_device(), stream.cuda_stream)
+    w = _STREAM_WORK.get(key)
+    if w is None:
+        with torch.cuda.device(device), torch.cuda.stream(stream):
+            w = decode_workspace(device)
+        _STREAM_WORK[key] = w
+    return w
 
 
 def linear_forward_multi(layers, codes, x, work: Optional[torch.Tensor] = None) -> torch.Tensor:

@@ -34,7 +34,7 @@ import torch
 import torch.nn as nn
 
 from . import dequant as _dequant
-from . import linear_forward, linear_forward_multi
+from . import linear_forward, linear_forward_multi, stream_workspace
 
 _KINDS = ("e8_lattice", "e8_d4")
 
@@ -100,10 +100,11 @@ class EPTQLinear(nn.Module):
                  S_group: Optional[torch.Tensor] = None,
                  table_f32: Optional[torch.Tensor] = None):
         super().__init__()
-        # Optional decode workspace (``decode_workspace``): E8-D4 calls then go
-        # through the multi-layer entry point, whose matrix-core kernel splits
-        # the columns of layers with few row tiles; calls sharing one must not
-        # overlap in time.
+        # Decode workspace of E8-D4 calls (``decode_workspace``): the
+        # matrix-core kernel splits the columns of layers with few row tiles
+        # over several workgroups through it.  None = the current stream's
+        # own (``stream_workspace``); calls sharing one must not overlap in
+        # time.
         self._work: Optional[torch.Tensor] = None
         if quantizer_type not in _KINDS:
             raise ValueError(f"unknown quantizer_type {quantizer_type!r}")
@@ -174,8 +175,9 @@ class EPTQLinear(nn.Module):
             x2 = x2.contiguous()
         layer = dict(Q=self.Q, g=self.g, h=self.h, O_vals=self.O_vals, O_col=self.O_col,
                      O_row_ptr=self.O_row_ptr, bias=self.bias, S_group=self.S_group)
-        if self._work is not None and self.quantizer_type == "e8_d4":
-            y = linear_forward_multi([layer], self._codebook, x2, work=self._work)
+        if self.quantizer_type == "e8_d4":
+            work = self._work if self._work is not None else stream_workspace(x2.device)
+            y = linear_forward_multi([layer], self._codebook, x2, work=work)
         else:
             y = linear_forward(self.quantizer_type, self.Q, self._codebook, self.g, self.h, x2,
                                self.O_vals, self.O_col, self.O_row_ptr, self.bias, self.S_group)
@@ -225,7 +227,8 @@ class EPTQMultiLinear(nn.Module):
         x2 = x2.contiguous()
         layers = [dict(Q=l.Q, g=l.g, h=l.h, O_vals=l.O_vals, O_col=l.O_col, O_row_ptr=l.O_row_ptr,
                        bias=l.bias, S_group=l.S_group) for l in self.parts]
-        y = linear_forward_multi(layers, self.parts[0]._codebook, x2, work=self._work)
+        work = self._work if self._work is not None else stream_workspace(x2.device)
+        y = linear_forward_multi(layers, self.parts[0]._codebook, x2, work=work)
         if y.dtype != out_dtype:
             y = y.to(out_dtype)
         return y.reshape(*shape[:-1], self.out_features)

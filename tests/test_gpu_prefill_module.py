@@ -9,7 +9,8 @@ rows, the prefill GEMMs that decode weight tiles into LDS or registers above
 * within 1e-2 relative L2 of the fp32 reconstruct + matmul oracle (the
   north-star tolerance) at both sides of the 128-row switch;
 * no torch GEMM runs inside the forward (``F.linear`` / ``torch.matmul``
-  raise while the module is called), and no fp16 W is materialized;
+  raise while the module is called), and no fp16 W is materialized (the
+  forward leaves only its output allocated);
 * multi-layer stacking (GQA q|k|v with a bias on one layer only), S_group,
   E8 layers, dense critical blocks, bf16 input.
 """
@@ -19,6 +20,7 @@ import pytest
 import torch
 import torch.nn.functional as F
 
+from eptq_amd.kernels import stream_workspace
 from eptq_amd.kernels.linear import EPTQLinear, EPTQMultiLinear
 from eptq_amd.quantizers import E8D4Quantizer, E8LatticeQuantizer
 from eptq_amd.synthetic import make_layer, make_x
@@ -53,6 +55,7 @@ class _NoTorchGemm:
 
 def _check(mod, qds, kind, r, T, seed, dtype=torch.float16):
     x = make_x(T, qds[0].Q.shape[1], seed=seed).to(dtype)
+    stream_workspace("cuda")          # the stream's split-K workspace exists before the count
     torch.cuda.synchronize()
     before = torch.cuda.memory_allocated()
     with torch.no_grad(), _NoTorchGemm():
