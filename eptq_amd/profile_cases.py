@@ -9,6 +9,7 @@ dozen dispatches each, no graph capture.
     python -m eptq_amd.profile_cases prefill --shape 5120x5120 --tokens 2048
     python -m eptq_amd.profile_cases e8 --shape 3072x768 --copies 8
     python -m eptq_amd.profile_cases step --layers 4
+    python -m eptq_amd.profile_cases module --tokens 2048
 """
 
 from __future__ import annotations
@@ -29,7 +30,7 @@ def _layer(torch, out, inp, seed, p, dev, qb=None, bias=False):
 
 def main(argv=None) -> None:
     ap = argparse.ArgumentParser()
-    ap.add_argument("case", choices=["decode", "prefill", "e8", "step"])
+    ap.add_argument("case", choices=["decode", "prefill", "e8", "step", "module"])
     ap.add_argument("--shape", default="4096x4096", help="out x in")
     ap.add_argument("--batch", type=int, default=1)
     ap.add_argument("--tokens", type=int, default=2048)
@@ -70,6 +71,26 @@ def main(argv=None) -> None:
             for L in layers:
                 linear_forward("e8_lattice", L["Q"], codes, L["g"], L["h"], x, L["O_vals"], L["O_col"],
                                L["O_row_ptr"], L["bias"], None)
+    elif args.case == "module":
+        # One Llama-2-13B decoder layer's Linears through the drop-in modules
+        # (EPTQMultiLinear q|k|v and gate|up, EPTQLinear o and down) at
+        # --tokens rows: the kernels the module forward runs.
+        from eptq_amd.kernels.linear import EPTQLinear, EPTQMultiLinear
+        from eptq_amd.synthetic import make_layer
+        q = E8D4Quantizer(radius=1.75)
+
+        def mod(o, i, k):
+            return EPTQLinear.from_quantized_data(make_layer(o, i, seed=9000 + k, percmask=0.002, device=dev),
+                                                  q, "e8_d4").to(dev)
+        d = 5120
+        mods = [EPTQMultiLinear([mod(d, d, k) for k in range(3)]), mod(d, d, 3),
+                EPTQMultiLinear([mod(13824, d, 4), mod(13824, d, 5)]), mod(d, 13824, 6)]
+        xs = {n: make_x(args.tokens, n, seed=n, device=dev) for n in (d, 13824)}
+        torch.cuda.synchronize()
+        with torch.no_grad():
+            for _ in range(args.reps):
+                for m in mods:
+                    m(xs[m.in_features])
     else:
         # One decode step's Linear units of args.layers Llama-2-7B layers:
         # q|k|v and gate|up as multi-layer launches, o and down alone.
