@@ -419,12 +419,26 @@ class GraphDecoder:
         self.fused = fused
         self.device = torch.device(device)
         model.alloc_cache(batch, max_len, self.device)
+        # The buffers this decoder's launches address (held, so a captured
+        # graph never addresses freed memory).  A later GraphDecoder on the
+        # same model replaces them in the model; this one then refuses to run.
+        self._bufs = self._model_bufs()
         self.tok = torch.zeros((batch, 1), dtype=torch.long, device=self.device)
         self.pos = torch.zeros((1,), dtype=torch.long, device=self.device)
         self.graph = None
 
+    def _model_bufs(self):
+        m = self.model
+        return (m.kc, m.vc, m.cos_tab, m.sin_tab, m.attn_work, m.lin_work, m.head_work)
+
+    def _check_owner(self):
+        if any(a is not b for a, b in zip(self._model_bufs(), self._bufs)):
+            raise RuntimeError("the model's caches and workspaces now belong to a newer GraphDecoder; "
+                               "this decoder (and its captured graph) can no longer run")
+
     @torch.no_grad()
     def prefill(self, prompt: torch.Tensor) -> torch.Tensor:
+        self._check_owner()
         T = prompt.shape[1]
         pos = torch.arange(T, device=self.device)
         logits = self.model.forward_tokens(prompt, pos)
@@ -444,6 +458,7 @@ class GraphDecoder:
 
     @torch.no_grad()
     def capture(self):
+        self._check_owner()
         # Warm up on a side stream (allocator and kernels), then capture.
         saved_tok, saved_pos = self.tok.clone(), self.pos.clone()
         side = torch.cuda.Stream(device=self.device)
@@ -462,6 +477,7 @@ class GraphDecoder:
         torch.cuda.synchronize(self.device)
 
     def step(self):
+        self._check_owner()
         if self.graph is None:
             self._step()
         else:

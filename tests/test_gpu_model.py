@@ -276,3 +276,26 @@ def test_split_attention_matches_single_workgroup():
             assert torch.equal(caches[0][0], caches[1][0]) and torch.equal(caches[0][1], caches[1][1])
         cnt = work[lib.eptq_llama_attn_work_bytes(B, H) - 4 * B * H:].view(torch.int32)
         assert int(cnt.abs().sum()) == 0, "counters are left at zero"
+
+
+def test_graph_decoder_refuses_after_model_retargeted():
+    """A second GraphDecoder on the same model takes over its caches and
+    workspaces; the first then raises instead of launching (its captured
+    graph addresses buffers the model no longer uses)."""
+    from eptq_amd.llama import GraphDecoder, LlamaConfig, build_synthetic
+    print("GraphDecoder: stale decoder refuses to run", flush=True)
+    cfg = LlamaConfig(hidden=512, ffn=1024, layers=1, heads=4, kv_heads=4, vocab=256)
+    model = build_synthetic(cfg, device="cuda", seed=5)
+    prompt = torch.randint(0, cfg.vocab, (2, 8), device="cuda", generator=torch.Generator("cuda").manual_seed(5))
+    d1 = GraphDecoder(model, 2, 32, device="cuda")
+    d1.prefill(prompt)
+    d1.capture()
+    d1.step()
+    torch.cuda.synchronize()
+    d2 = GraphDecoder(model, 2, 32, device="cuda")
+    for call in (d1.step, d1.capture, lambda: d1.prefill(prompt)):
+        with pytest.raises(RuntimeError, match="newer GraphDecoder"):
+            call()
+    d2.prefill(prompt)
+    d2.step()
+    torch.cuda.synchronize()
