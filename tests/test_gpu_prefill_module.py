@@ -110,3 +110,24 @@ def test_module_prefill_bf16_and_row_consistency():
         y_small = mod(x[:8])           # decode kernel
     torch.cuda.synchronize()
     assert rel_l2(y_small.float().cpu().numpy(), y16[:8].float().cpu().numpy()) < 2e-3
+
+
+@pytest.mark.parametrize("out,inp,T,dtype", [
+    (1024, 2048, 17, torch.float16),      # first row past the decode kernels
+    (1024, 2048, 129, torch.float16),     # first row past the 16-row slices
+    (1280, 2048, 257, torch.float16),     # a 256-token tile plus one row
+    (1024, 2048, 100, torch.bfloat16),    # bf16 at mid counts (no matrix-core slices)
+    (1024, 2080, 200, torch.float16),     # in_features an odd multiple of 32
+    (512, 1000, 150, torch.float16),      # in_features not a multiple of 32
+    (1024, 2048, 0, torch.float16),       # empty batch
+])
+def test_module_prefill_edges(out, inp, T, dtype):
+    print(f"module prefill edge {out}x{inp} T={T} {dtype}", flush=True)
+    qd = make_layer(out, inp, seed=out + inp + T, percmask=0.002, bias=True)
+    mod = EPTQLinear.from_quantized_data(qd, E8D4Quantizer(radius=1.75), "e8_d4").cuda()
+    if T == 0:
+        with torch.no_grad():
+            y = mod(torch.empty((0, inp), dtype=dtype, device="cuda"))
+        assert y.shape == (0, out) and y.dtype == dtype
+        return
+    _check(mod, [qd], "e8_d4", 1.75, T, seed=T + 1, dtype=dtype)
