@@ -999,7 +999,7 @@ int launch_gemm(const LinearArgs& a, hipStream_t s) {
     if (rc == 0) return 0;
   }
   // LDS-decode kernel: fp16 x and table, no S_group, K-steps of 64, whole
-  // 16-, 20- or 32-Q-row tiles, 16-byte x rows and 8-byte y stores.  Of the two
+  // 8-, 16-, 20- or 32-Q-row tiles, 16-byte x rows and 8-byte y stores.  Of the two
   // tile widths, the one with less work per CU (rounds of the CUs × tile
   // width) wins; on a tie the wider tile.
   if (KIND == KIND_E8D4 && !a.x_bf16 && !a.codes_f32 && !a.S && a.prep == 0 && (a.N % g3::kBK) == 0 &&
@@ -1016,22 +1016,27 @@ int launch_gemm(const LinearArgs& a, hipStream_t s) {
     if (bf != 160 && a.M % 16 == 0) {
       const long r128 = ((a.M / 16) * TB + cus - 1) / cus, r256 = ((a.M / 32) * TB + cus - 1) / cus;
       if (bf == 0 || 4 * r128 < 5 * r256) bf = 128;
+      // 64-feature tiles when they still fit one round of the CUs: a launch
+      // with few token tiles is bound by each workgroup's serial K-steps,
+      // and narrower tiles shorten each step.
+      if (bf == 128 && (long)(a.M / 8) * TB <= cus) bf = 64;
     }
     const long grid = bf ? (a.M / (bf / 8)) * TB : 0;
     if (bf && grid <= 0x7fffffff) {
       // 160-feature tiles: 8 producer waves (the MFMA waves fit four waves per
       // SIMD); 256-feature tiles: 4.
-      const int v = bf == 256 ? 0 : bf == 160 ? 1 : 2;
-      const void* kerns[3] = {(const void*)k_gemm_lds_e8d4<256, 4>, (const void*)k_gemm_lds_e8d4<160, 8>,
-                              (const void*)k_gemm_lds_e8d4<128, 8>};
-      const int bytes[3] = {g3::Lay<256>::Bytes, g3::Lay<160>::Bytes, g3::Lay<128>::Bytes};
-      static bool attr[3] = {false, false, false};
+      const int v = bf == 256 ? 0 : bf == 160 ? 1 : bf == 128 ? 2 : 3;
+      const void* kerns[4] = {(const void*)k_gemm_lds_e8d4<256, 4>, (const void*)k_gemm_lds_e8d4<160, 8>,
+                              (const void*)k_gemm_lds_e8d4<128, 8>, (const void*)k_gemm_lds_e8d4<64, 8>};
+      const int bytes[4] = {g3::Lay<256>::Bytes, g3::Lay<160>::Bytes, g3::Lay<128>::Bytes, g3::Lay<64>::Bytes};
+      static bool attr[4] = {false, false, false, false};
       if (!attr[v]) attr[v] = hipFuncSetAttribute(kerns[v], hipFuncAttributeMaxDynamicSharedMemorySize, bytes[v]) == hipSuccess;
       if (attr[v]) {
         const int OB = a.M / (bf / 8);
         if (v == 0) k_gemm_lds_e8d4<256, 4><<<(unsigned)grid, 768, bytes[0], s>>>(a, OB);
         else if (v == 1) k_gemm_lds_e8d4<160, 8><<<(unsigned)grid, 1024, bytes[1], s>>>(a, OB);
-        else k_gemm_lds_e8d4<128, 8><<<(unsigned)grid, 1024, bytes[2], s>>>(a, OB);
+        else if (v == 2) k_gemm_lds_e8d4<128, 8><<<(unsigned)grid, 1024, bytes[2], s>>>(a, OB);
+        else k_gemm_lds_e8d4<64, 8><<<(unsigned)grid, 1024, bytes[3], s>>>(a, OB);
         return 0;
       }
     }

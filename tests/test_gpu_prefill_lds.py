@@ -1,18 +1,19 @@
 """GPU parity of the prefill GEMM that decodes the weight tile into LDS
 (``k_gemm_lds_e8d4``: E8-D4, fp16 x, no S_group, more than 128 tokens,
-in_features a multiple of 64, out_features a multiple of 128 or 160) through
+in_features a multiple of 64, out_features a multiple of 64 or 160) through
 the C ABI's ``eptq_e8d4_forward``.
 
 Every case is within 1e-2 relative L2 of the fp32 reconstruct + matmul
 oracle (``dequantize_layer`` W, then an fp32 product).  The cases cover the
-three tile widths (160 features when out_features / 160 gives fewer rounds
+four tile widths (160 features when out_features / 160 gives fewer rounds
 of the CUs; else 128 when 0.8 x its rounds is below the 256-feature tiles'
-rounds; else 256), token counts that are not a multiple of the 256-token
-tile, one and two K-steps, a bias, a layer with no critical block,
-workgroups whose critical blocks exceed the entries they stage in LDS (2272
-for 160-feature, 2784 for 128-feature, 944 for 256-feature tiles; the rest
-are corrected after the K loop), and h below and far above 1 (the 2^-e
-scaling of the table).
+rounds, and 64 in its place when that is still one round; else 256), token
+counts that are not a multiple of the 256-token tile, one and two K-steps,
+a bias, a layer with no critical block, workgroups whose critical blocks
+exceed the entries they stage in LDS (2272 for 160-feature, 3712 for
+64-feature, 2784 for 128-feature, 944 for 256-feature tiles; the rest are
+corrected after the K loop), and h below and far above 1 (the 2^-e scaling
+of the table).
 """
 
 from __future__ import annotations
@@ -35,9 +36,11 @@ TOL = 1e-2
 CASES = [
     # out, in, tokens, critical-block fraction, bias, h scale
     (1280, 2048, 512, 0.002, True, 1.0),     # 160-feature tiles (8 of them beat 5 of 256)
-    (1024, 2048, 300, 0.002, True, 1.0),     # 128-feature tiles (1024 / 160 is not whole; one round)
-    (512, 1024, 257, 0.15, False, 1.0),      # 128: ~2500 entries per workgroup
-    (256, 4096, 300, 0.05, False, 1.0),      # 128: ~3300 entries per workgroup, past its 2784
+    (1024, 2048, 300, 0.002, True, 1.0),     # 64-feature tiles (1024 / 160 is not whole; one round)
+    (512, 1024, 257, 0.15, False, 1.0),      # 64: ~1200 entries per workgroup
+    (256, 4096, 300, 0.15, False, 1.0),      # 64: ~4900 entries per workgroup, past its 3712
+    (4096, 1024, 1280, 0.002, True, 1.0),    # 128: 320 tiles of 64 would take two rounds
+    (4096, 1024, 1280, 0.2, False, 1.0),     # 128: ~3300 entries per workgroup, past its 2784
     (1024, 2048, 12800, 0.002, True, 1.0),   # 256: 200 tiles (one round) against 400 of 128 (two)
     (1024, 2048, 12800, 0.15, False, 1.0),   # 256: ~9800 entries per workgroup, past its 944
     (640, 1024, 200, 0.15, False, 1.0),      # 160: ~3100 entries per workgroup, past its 2272
