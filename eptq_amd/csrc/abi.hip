@@ -236,68 +236,6 @@ int fused_linear(const char* fn, int n, const eptq_layer* layers, const void* co
   return check_launch(fn);
 }
 
-// Body of eptq_e8d4_forward_multi and of its allocation-free variant, which
-// passes the library's own scratch as `work`.
-int forward_multi(const char* fn, int n_layers, const eptq_layer* layers, const void* codes, int codes_dtype,
-                  const void* x, int x_dtype, int N, int B, void* y, int ldy, void* work, long long work_bytes,
-                  void* stream) {
-  if (n_layers <= 0 || !layers) return fail(EPTQ_EINVAL, "%s: n_layers=%d", fn, n_layers);
-  if (work && (!aligned16(work) || work_bytes < 0))
-    return fail(EPTQ_EINVAL, "%s: work must be 16-byte aligned with work_bytes >= 0", fn);
-  if (B < 0) return fail(EPTQ_EINVAL, "%s: B=%d", fn, B);
-  if (B > 0 && (!x || !y)) return fail(EPTQ_EINVAL, "%s: null x/y", fn);
-  eptq::LinearArgs a[eptq::kMaxLayers];
-  const int n = n_layers;
-  // Validate every layer first; each writes columns [y_offset, y_offset + 8M) of y.
-  for (int l = 0; l < n; ++l) {
-    const eptq_layer& L = layers[l];
-    eptq::LinearArgs t;
-    int rc = layer_args(fn, eptq::KIND_E8D4, L.Q, codes, codes_dtype, L.g, L.h, x, x_dtype, L.O_vals,
-                        L.O_col, L.O_row_ptr, L.bias, L.S_group, L.n_groups, L.M, N, B, &t);
-    if (rc) return rc;
-    if (L.y_offset < 0 || L.y_offset + 8LL * L.M > (long long)ldy || (L.y_offset & 3))
-      return fail(EPTQ_EINVAL, "%s: layer %d columns [%lld, %lld) outside a y row of %d (offset %% 4 == 0)",
-                  fn, l, L.y_offset, L.y_offset + 8LL * L.M, ldy);
-    t.y = (uint16_t*)y + L.y_offset;
-    t.ldy = ldy;
-    if (l < eptq::kMaxLayers) a[l] = t;
-  }
-  if (B == 0) return EPTQ_OK;
-  hipStream_t s = (hipStream_t)stream;
-  // 17..128 rows: 16-row slices of the matrix-core decode kernel, every layer
-  // in each slice's launch (its eligibility does not depend on the slice's
-  // row count, so a first slice that launches means every slice does).
-  if (B > eptq::kMatvecMaxBatch && B <= eptq::kSliceMaxTokens && n <= eptq::kMaxLayers) {
-    int rc = 0;
-    for (int b0 = 0; b0 < B && rc == 0; b0 += eptq::kMatvecMaxBatch) {
-      eptq::LinearArgs sl[eptq::kMaxLayers];
-      for (int l = 0; l < n; ++l) {
-        sl[l] = a[l];
-        sl[l].B = B - b0 < eptq::kMatvecMaxBatch ? B - b0 : eptq::kMatvecMaxBatch;
-        sl[l].x = a[l].x + (size_t)b0 * a[l].ldx;
-        sl[l].y = a[l].y + (size_t)b0 * ldy;
-      }
-      rc = eptq::launch_decode_mfma_multi(sl, n, s, work, work ? work_bytes : 0);
-    }
-    if (rc == 0) return check_launch(fn);
-  }
-  // One launch when the decode kernel takes them all, else one per layer.
-  if (n > eptq::kMaxLayers || eptq::launch_decode_e8d4_multi(a, n, s, work, work ? work_bytes : 0) != 0) {
-    for (int l = 0; l < n; ++l) {
-      eptq::LinearArgs t;
-      const eptq_layer& L = layers[l];
-      layer_args(fn, eptq::KIND_E8D4, L.Q, codes, codes_dtype, L.g, L.h, x, x_dtype, L.O_vals, L.O_col,
-                 L.O_row_ptr, L.bias, L.S_group, L.n_groups, L.M, N, B, &t);
-      t.y = (uint16_t*)y + L.y_offset;
-      t.ldy = ldy;
-      const int rc = dispatch(fn, eptq::KIND_E8D4, t, s);
-      if (rc) return rc;
-    }
-  }
-  return check_launch(fn);
-}
-
-
 constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mu;
 std::atomic<char*> g_scratch[kMaxDevices];
@@ -333,6 +271,75 @@ int scratch_of_device(const char* fn, hipStream_t s, char** out) {
   *out = p;
   return EPTQ_OK;
 }
+
+// Body of eptq_e8d4_forward_multi and of its allocation-free variant
+// (use_scratch: `work` is the library's own scratch, looked up once every
+// argument has passed the same checks).
+int forward_multi(const char* fn, int n_layers, const eptq_layer* layers, const void* codes, int codes_dtype,
+                  const void* x, int x_dtype, int N, int B, void* y, int ldy, void* work, long long work_bytes,
+                  void* stream, bool use_scratch = false) {
+  if (n_layers <= 0 || !layers) return fail(EPTQ_EINVAL, "%s: n_layers=%d", fn, n_layers);
+  if (work && (!aligned16(work) || work_bytes < 0))
+    return fail(EPTQ_EINVAL, "%s: work must be 16-byte aligned with work_bytes >= 0", fn);
+  if (B < 0) return fail(EPTQ_EINVAL, "%s: B=%d", fn, B);
+  if (B > 0 && (!x || !y)) return fail(EPTQ_EINVAL, "%s: null x/y", fn);
+  eptq::LinearArgs a[eptq::kMaxLayers];
+  const int n = n_layers;
+  // Validate every layer first; each writes columns [y_offset, y_offset + 8M) of y.
+  for (int l = 0; l < n; ++l) {
+    const eptq_layer& L = layers[l];
+    eptq::LinearArgs t;
+    int rc = layer_args(fn, eptq::KIND_E8D4, L.Q, codes, codes_dtype, L.g, L.h, x, x_dtype, L.O_vals,
+                        L.O_col, L.O_row_ptr, L.bias, L.S_group, L.n_groups, L.M, N, B, &t);
+    if (rc) return rc;
+    if (L.y_offset < 0 || L.y_offset + 8LL * L.M > (long long)ldy || (L.y_offset & 3))
+      return fail(EPTQ_EINVAL, "%s: layer %d columns [%lld, %lld) outside a y row of %d (offset %% 4 == 0)",
+                  fn, l, L.y_offset, L.y_offset + 8LL * L.M, ldy);
+    t.y = (uint16_t*)y + L.y_offset;
+    t.ldy = ldy;
+    if (l < eptq::kMaxLayers) a[l] = t;
+  }
+  if (B == 0) return EPTQ_OK;
+  hipStream_t s = (hipStream_t)stream;
+  if (use_scratch) {
+    char* p = nullptr;
+    if (const int rc = scratch_of_device(fn, s, &p)) return rc;
+    work = p;
+    work_bytes = (long long)kNoAllocScratchBytes;
+  }
+  // 17..128 rows: 16-row slices of the matrix-core decode kernel, every layer
+  // in each slice's launch (its eligibility does not depend on the slice's
+  // row count, so a first slice that launches means every slice does).
+  if (B > eptq::kMatvecMaxBatch && B <= eptq::kSliceMaxTokens && n <= eptq::kMaxLayers) {
+    int rc = 0;
+    for (int b0 = 0; b0 < B && rc == 0; b0 += eptq::kMatvecMaxBatch) {
+      eptq::LinearArgs sl[eptq::kMaxLayers];
+      for (int l = 0; l < n; ++l) {
+        sl[l] = a[l];
+        sl[l].B = B - b0 < eptq::kMatvecMaxBatch ? B - b0 : eptq::kMatvecMaxBatch;
+        sl[l].x = a[l].x + (size_t)b0 * a[l].ldx;
+        sl[l].y = a[l].y + (size_t)b0 * ldy;
+      }
+      rc = eptq::launch_decode_mfma_multi(sl, n, s, work, work ? work_bytes : 0);
+    }
+    if (rc == 0) return check_launch(fn);
+  }
+  // One launch when the decode kernel takes them all, else one per layer.
+  if (n > eptq::kMaxLayers || eptq::launch_decode_e8d4_multi(a, n, s, work, work ? work_bytes : 0) != 0) {
+    for (int l = 0; l < n; ++l) {
+      eptq::LinearArgs t;
+      const eptq_layer& L = layers[l];
+      layer_args(fn, eptq::KIND_E8D4, L.Q, codes, codes_dtype, L.g, L.h, x, x_dtype, L.O_vals, L.O_col,
+                 L.O_row_ptr, L.bias, L.S_group, L.n_groups, L.M, N, B, &t);
+      t.y = (uint16_t*)y + L.y_offset;
+      t.ldy = ldy;
+      const int rc = dispatch(fn, eptq::KIND_E8D4, t, s);
+      if (rc) return rc;
+    }
+  }
+  return check_launch(fn);
+}
+
 
 }  // namespace
 
@@ -370,21 +377,8 @@ int eptq_e8d4_forward_multi(int n_layers, const eptq_layer* layers, const void* 
 int eptq_e8d4_forward_multi_noalloc(int n_layers, const eptq_layer* layers, const void* codes,
                                     int codes_dtype, const void* x, int x_dtype, int N, int B, void* y,
                                     int ldy, void* stream) {
-  const char* fn = "eptq_e8d4_forward_multi_noalloc";
-  if (n_layers > 0 && layers) {
-    long long tiles = 0;
-    for (int l = 0; l < n_layers; ++l)
-      tiles += layers[l].M > 0 ? (8LL * layers[l].M + eptq::kSplitTileRows - 1) / eptq::kSplitTileRows : 0;
-    if (tiles > eptq::kSplitCounters)
-      return fail(EPTQ_EUNSUPPORTED,
-                  "%s: %lld tiles of %d output rows exceed the scratch's %d tile counters (at most %lld output "
-                  "rows per call)", fn, tiles, eptq::kSplitTileRows, eptq::kSplitCounters,
-                  (long long)eptq::kSplitCounters * eptq::kSplitTileRows);
-  }
-  char* work = nullptr;
-  if (const int rc = scratch_of_device(fn, (hipStream_t)stream, &work)) return rc;
-  return forward_multi(fn, n_layers, layers, codes, codes_dtype, x, x_dtype, N, B, y, ldy, work,
-                       (long long)kNoAllocScratchBytes, stream);
+  return forward_multi("eptq_e8d4_forward_multi_noalloc", n_layers, layers, codes, codes_dtype, x, x_dtype, N, B,
+                       y, ldy, nullptr, 0, stream, true);
 }
 
 long long eptq_e8d4_work_bytes(void) { return eptq::decode_mfma_work_bytes(); }

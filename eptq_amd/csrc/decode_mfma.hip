@@ -395,7 +395,10 @@ __global__ __launch_bounds__((S + 1) * 64, 3) void k_decode_mfma(MultiArgs ma, i
   // Split columns: every part leaves its partial sums (device-coherent
   // stores, complete before the tile's counter is raised); the last part to
   // arrive adds all Pt of them in part order, so the result does not depend
-  // on which part came last, writes y and resets the counter.
+  // on which part came last, writes y and resets the counter.  The count is
+  // an agent-scope acquire-release: each part's release publishes its sums
+  // (the workgroup barrier orders every wave's stores before it), and the
+  // last part's acquire makes all of them visible to its reads.
   bool fin = true;
   if (Pt > 1) {
     __shared__ int last_part;
@@ -406,7 +409,7 @@ __global__ __launch_bounds__((S + 1) * 64, 3) void k_decode_mfma(MultiArgs ma, i
     __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
     __syncthreads();
     if (tid == 0) {
-      const int old = __hip_atomic_fetch_add(wcnt + tile_g, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const int old = __hip_atomic_fetch_add(wcnt + tile_g, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
       last_part = old == Pt - 1;
       if (old == Pt - 1) __hip_atomic_store(wcnt + tile_g, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }

@@ -983,6 +983,17 @@ __global__ __launch_bounds__(kGT, 2) void k_gemm_e8(LinearArgs a, int OB) {
   gemm_tile<KIND_E8, HAS_S>(a, OB);
 }
 
+namespace {
+constexpr size_t kLdsBytes = 160 * 1024;
+
+// Static LDS of a kernel (0 if the runtime cannot say, which the launch's
+// own check then catches).
+size_t static_lds(const void* kern) {
+  hipFuncAttributes fa;
+  return hipFuncGetAttributes(&fa, kern) == hipSuccess ? fa.sharedSizeBytes : 0;
+}
+}  // namespace
+
 template <int KIND>
 int launch_gemm(const LinearArgs& a, hipStream_t s) {
   if (KIND == KIND_E8D4 && a.B <= kSliceMaxTokens && a.prep == 0) {
@@ -1054,13 +1065,18 @@ int launch_gemm(const LinearArgs& a, hipStream_t s) {
     const size_t dyn = g2::dyn_bytes(a.N);
     // Five-wave workgroups (one per CU) when they cover the layer in one
     // round of the device's CUs; else four-wave workgroups, two per CU.
-    const bool five = (a.M % 40) == 0 && (long)(a.M / 40) * TB <= dec::cu_count();
+    const void* kerns[4] = {(const void*)k_gemm_rows_e8d4<4, false>, (const void*)k_gemm_rows_e8d4<5, false>,
+                            (const void*)k_gemm_rows_e8d4<4, true>, (const void*)k_gemm_rows_e8d4<5, true>};
+    // A variant fits when its static LDS plus the activation rows stay
+    // within the CU's 160 KB.
+    static const size_t st[4] = {static_lds(kerns[0]), static_lds(kerns[1]), static_lds(kerns[2]),
+                                 static_lds(kerns[3])};
+    auto fits = [&](int v) { return dyn <= 96 * 1024 && st[v] + dyn <= kLdsBytes; };
+    bool five = (a.M % 40) == 0 && (long)(a.M / 40) * TB <= dec::cu_count() && fits(1 | (a.x_bf16 ? 2 : 0));
     const int OB = five ? a.M / 40 : a.M / 32;
     const long grid = (long)OB * TB;
-    if (grid <= 0x7fffffff && dyn <= 96 * 1024) {
+    if (grid <= 0x7fffffff && fits((five ? 1 : 0) | (a.x_bf16 ? 2 : 0))) {
       const int v = (five ? 1 : 0) | (a.x_bf16 ? 2 : 0);
-      const void* kerns[4] = {(const void*)k_gemm_rows_e8d4<4, false>, (const void*)k_gemm_rows_e8d4<5, false>,
-                              (const void*)k_gemm_rows_e8d4<4, true>, (const void*)k_gemm_rows_e8d4<5, true>};
       static size_t attr[4] = {0, 0, 0, 0};
       bool ok = true;
       if (dyn > attr[v]) {

@@ -339,8 +339,10 @@ __device__ __forceinline__ void rope_attn(const f16* __restrict__ qkv, const int
   }
   __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): the stores are complete
   __syncthreads();
+  // Agent-scope acquire-release count: releases this split's partial, and
+  // the last split's acquire makes every partial visible to its reads.
   if (t == 0) {
-    const int prev = __hip_atomic_fetch_add(cnt + bh, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int prev = __hip_atomic_fetch_add(cnt + bh, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
     s_last = prev == ns - 1;
     if (prev == ns - 1) __hip_atomic_store(cnt + bh, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
@@ -537,8 +539,10 @@ __global__ __launch_bounds__(kT) void k_lm_head_argmax(const f16* __restrict__ x
   }
   __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): the atomics are complete
   __syncthreads();
+  // Agent-scope acquire-release count: orders this workgroup's key maxima
+  // before it, and the last workgroup's acquire before its key reads.
   if (t == 0) {
-    const int prev = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int prev = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
     s_last = prev == (int)gridDim.x - 1;
     if (s_last) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }

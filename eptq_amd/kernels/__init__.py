@@ -10,14 +10,19 @@ its C ABI on the current HIP stream; there is no CPU or PyTorch fallback.
 Additions over the reference: fp32 tables are accepted (the kernels convert),
 bf16 activations give bf16 outputs, ``*_grouped`` variants take ``S_group``
 (the reference materializes an fp16 W instead, ``kernels/linear.py:97-120``),
-and ``eptq::e8d4_dequant`` / ``eptq::e8_dequant`` produce the bit-exact fp16 W of
-``dequantize_layer`` (``algorithms/eptq.py:406-471``) on the GPU.
+``eptq::e8d4_dequant`` / ``eptq::e8_dequant`` produce the bit-exact fp16 W of
+``dequantize_layer`` (``algorithms/eptq.py:406-471``) on the GPU, and
+``eptq::e8d4_forward_multi`` runs several E8-D4 layers that share x (q|k|v,
+gate|up) in one launch with a split-K workspace.  ``EPTQLinear.forward`` and
+``EPTQMultiLinear.forward`` call only these registered ops, so, as in the
+reference (``kernels/__init__.py:44-47``), ``torch.compile(fullgraph=True)``
+sees each quantized Linear as one op with no graph break.
 """
 
 from __future__ import annotations
 
 
-from typing import Optional
+from typing import List, Optional
 
 import torch
 
@@ -25,8 +30,8 @@ from . import _lib
 from ._lib import EPTQ_BF16, EPTQ_F16, EPTQ_F32, EptqError
 
 __all__ = ["e8_forward", "e8d4_forward", "e8_forward_grouped", "e8d4_forward_grouped",
-           "e8_dequant", "e8d4_dequant", "EptqError", "linear_forward", "linear_forward_multi",
-           "dequant", "decode_workspace", "stream_workspace"]
+           "e8d4_forward_multi", "e8_dequant", "e8d4_dequant", "EptqError", "linear_forward",
+           "linear_forward_multi", "dequant", "decode_workspace", "stream_workspace"]
 
 
 def _ptr(t: Optional[torch.Tensor]):
@@ -107,14 +112,24 @@ def decode_workspace(device) -> torch.Tensor:
 
 # One split-K workspace per (device, stream): launches on one stream run one
 # after another, so modules that share their stream's workspace never overlap
-# on it.  Created on first use (zero-filled on that stream).
+# on it.  Created on first eager use (zero-filled on that stream).
 _STREAM_WORK: dict = {}
 
 
-def stream_workspace(device) -> torch.Tensor:
+def stream_workspace(device) -> Optional[torch.Tensor]:
     """The decode workspace of the current stream on ``device`` (see
-    ``decode_workspace``), created on first use."""
+    ``decode_workspace``), created on first eager use.
+
+    While the current stream is capturing a graph this returns None (the
+    unsplit kernel, same results): a workspace made during a capture would
+    come from that graph's private pool with its zero fill recorded, not run,
+    and graphs captured on one stream may later replay concurrently on
+    different streams.  A caller that wants split-K inside a captured graph
+    attaches its own workspace (``EPTQLinear._work = decode_workspace(dev)``),
+    which that graph's replays then must not share with concurrent work."""
     device = torch.device(device)
+    if torch.cuda.is_current_stream_capturing():
+        return None
     stream = torch.cuda.current_stream(device)
     key = (device.index if device.index is not None else torch.cuda.current_device(), stream.cuda_stream)
     w = _STREAM_WORK.get(key)
@@ -263,3 +278,34 @@ def e8_dequant(Q: torch.Tensor, codes: torch.Tensor, g: torch.Tensor, h: torch.T
 @e8_dequant.register_fake
 def _e8_dequant_fake(Q, codes, g, h, O_vals, O_col, O_row_ptr, S_group=None):
     return Q.new_empty(Q.shape[0] * 8, Q.shape[1], dtype=torch.float16)
+
+
+@torch.library.custom_op("eptq::e8d4_forward_multi", mutates_args=("work",))
+def e8d4_forward_multi(Q: List[torch.Tensor], codes: torch.Tensor, g: List[torch.Tensor],
+                       h: List[torch.Tensor], x: torch.Tensor, O_vals: List[torch.Tensor],
+                       O_col: List[torch.Tensor], O_row_ptr: List[torch.Tensor],
+                       bias: List[Optional[torch.Tensor]], S_group: List[Optional[torch.Tensor]],
+                       work: Optional[torch.Tensor]) -> torch.Tensor:
+    """E8-D4 layers sharing ``x`` (B, N) -> (B, Σ 8·M_l), outputs side by side
+    (``linear_forward_multi``); the op ``EPTQLinear`` / ``EPTQMultiLinear``
+    call for E8-D4 layers.  No counterpart in the reference, whose module
+    calls ``eptq::e8d4_forward`` per projection (``kernels/linear.py:177-208``).
+
+    ``work`` (required, may be None; a mutated argument with a default
+    trips torch's in-place bookkeeping): a ``decode_workspace`` tensor
+    (declared mutated: the split-K parts write their partial sums there; the
+    counters return to zero), or None for the current stream's own (``stream_workspace``), which the op
+    looks up when it runs, like a BLAS library's internal workspace."""
+    layers = [dict(Q=Q[i], g=g[i], h=h[i], O_vals=O_vals[i], O_col=O_col[i], O_row_ptr=O_row_ptr[i],
+                   bias=bias[i], S_group=S_group[i]) for i in range(len(Q))]
+    if work is None and x.is_cuda:
+        work = stream_workspace(x.device)
+    return linear_forward_multi(layers, codes, x, work=work)
+
+
+@e8d4_forward_multi.register_fake
+def _e8d4_forward_multi_fake(Q, codes, g, h, x, O_vals, O_col, O_row_ptr, bias, S_group, work):
+    n = len(Q)
+    torch._check(n > 0 and all(len(t) == n for t in (g, h, O_vals, O_col, O_row_ptr, bias, S_group)),
+                 lambda: "every per-layer list must have one entry per layer")
+    return x.new_empty(x.shape[0], sum(q.shape[0] * 8 for q in Q))

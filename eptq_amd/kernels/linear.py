@@ -33,8 +33,7 @@ from typing import Optional, Tuple
 import torch
 import torch.nn as nn
 
-from . import dequant as _dequant
-from . import linear_forward, linear_forward_multi, stream_workspace
+from . import dequant as _dequant  # noqa: F401  (also registers the eptq:: ops)
 
 _KINDS = ("e8_lattice", "e8_d4")
 
@@ -103,7 +102,8 @@ class EPTQLinear(nn.Module):
         # Decode workspace of E8-D4 calls (``decode_workspace``): the
         # matrix-core kernel splits the columns of layers with few row tiles
         # over several workgroups through it.  None = the current stream's
-        # own (``stream_workspace``); calls sharing one must not overlap in
+        # own (``stream_workspace``; none, i.e. the unsplit kernel, while a
+        # graph is being captured); calls sharing one must not overlap in
         # time.
         self._work: Optional[torch.Tensor] = None
         if quantizer_type not in _KINDS:
@@ -166,21 +166,27 @@ class EPTQLinear(nn.Module):
                    quantizer_type=quantizer_type, S_group=S, table_f32=tab32)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
+        # Only registered ops below (reference kernels/linear.py:177-208), so
+        # torch.compile traces the call without a graph break.
         shape = x.shape
         out_dtype = x.dtype
         x2 = x.reshape(-1, self.in_features)
         if x2.dtype not in (torch.float16, torch.bfloat16):
             x2 = x2.half()
-        if not x2.is_contiguous():
-            x2 = x2.contiguous()
-        layer = dict(Q=self.Q, g=self.g, h=self.h, O_vals=self.O_vals, O_col=self.O_col,
-                     O_row_ptr=self.O_row_ptr, bias=self.bias, S_group=self.S_group)
+        x2 = x2.contiguous()
         if self.quantizer_type == "e8_d4":
-            work = self._work if self._work is not None else stream_workspace(x2.device)
-            y = linear_forward_multi([layer], self._codebook, x2, work=work)
+            y = torch.ops.eptq.e8d4_forward_multi([self.Q], self._codebook, [self.g], [self.h], x2,
+                                                  [self.O_vals], [self.O_col], [self.O_row_ptr],
+                                                  [self.bias], [self.S_group], self._work)
         else:
-            y = linear_forward(self.quantizer_type, self.Q, self._codebook, self.g, self.h, x2,
-                               self.O_vals, self.O_col, self.O_row_ptr, self.bias, self.S_group)
+            bias = self.bias if self.bias is not None else x2.new_empty(0, dtype=torch.float16)
+            if self.S_group is None:
+                y = torch.ops.eptq.e8_forward(self.Q, self._codebook, self.g, self.h, x2, self.O_vals,
+                                              self.O_col, self.O_row_ptr, bias)
+            else:
+                y = torch.ops.eptq.e8_forward_grouped(self.Q, self._codebook, self.g, self.h, x2,
+                                                      self.O_vals, self.O_col, self.O_row_ptr, bias,
+                                                      self.S_group)
         if y.dtype != out_dtype:
             y = y.to(out_dtype)
         return y.reshape(*shape[:-1], self.out_features)
@@ -225,10 +231,11 @@ class EPTQMultiLinear(nn.Module):
         if x2.dtype not in (torch.float16, torch.bfloat16):
             x2 = x2.half()
         x2 = x2.contiguous()
-        layers = [dict(Q=l.Q, g=l.g, h=l.h, O_vals=l.O_vals, O_col=l.O_col, O_row_ptr=l.O_row_ptr,
-                       bias=l.bias, S_group=l.S_group) for l in self.parts]
-        work = self._work if self._work is not None else stream_workspace(x2.device)
-        y = linear_forward_multi(layers, self.parts[0]._codebook, x2, work=work)
+        ps = list(self.parts)
+        y = torch.ops.eptq.e8d4_forward_multi([l.Q for l in ps], ps[0]._codebook, [l.g for l in ps],
+                                              [l.h for l in ps], x2, [l.O_vals for l in ps],
+                                              [l.O_col for l in ps], [l.O_row_ptr for l in ps],
+                                              [l.bias for l in ps], [l.S_group for l in ps], self._work)
         if y.dtype != out_dtype:
             y = y.to(out_dtype)
         return y.reshape(*shape[:-1], self.out_features)

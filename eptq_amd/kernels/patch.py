@@ -81,9 +81,10 @@ def load_quantized_model(quantized_dir: str, device: str = "cuda") -> Tuple[nn.M
     for name, param in global_params.items():
         _set_param(model, name, param)
 
-    meta = [n for n, p in model.named_parameters() if p.is_meta]
-    if meta:
-        print(f"WARNING: {len(meta)} meta parameters not loaded: {meta[:5]}", file=sys.stderr)
+    unloaded = [n for n, p in model.named_parameters() if p.is_meta]
+    if unloaded:
+        print(f"eptq_amd: {len(unloaded)} parameters still on the meta device after loading "
+              f"(first: {', '.join(unloaded[:5])})", file=sys.stderr)
     model = model.to(device=device)
     model.eval()
     print("eptq_amd: model ready", file=sys.stderr)

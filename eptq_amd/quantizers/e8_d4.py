@@ -64,6 +64,7 @@ class E8D4Quantizer(BaseQuantizer):
     ``raw_codes`` on-disk format), else ``None``.
     """
 
+    RAW_ATTR = "_raw_codes"
     DEFAULT_RADIUS = 1.875
 
     def __init__(self, device: str = "cpu", codebook: Optional[torch.Tensor] = None,

@@ -68,6 +68,7 @@ class E8LatticeQuantizer(BaseQuantizer):
     ``points`` is the fp32 (65535, 8) table divided by ``_radius``.
     """
 
+    RAW_ATTR = "_raw_points"
     DEFAULT_RADIUS = 1.6
 
     def __init__(self, device: str = "cpu", codebook: Optional[torch.Tensor] = None,

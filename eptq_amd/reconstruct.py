@@ -11,7 +11,7 @@ from __future__ import annotations
 
 import json
 from pathlib import Path
-from typing import Dict
+from typing import Dict, Optional
 
 import torch
 
@@ -25,49 +25,54 @@ def load_quantization_config(quantized_dir) -> Dict:
         return json.load(f)
 
 
-def load_quantizer(quantized_dir, device: str = "cuda") -> BaseQuantizer:
-    """``reconstruct.py:39-90``: the three ``quantizer.pt`` formats.
+_QUANTIZER_CLASSES = {"e8_lattice": E8LatticeQuantizer, "e8_d4": E8D4Quantizer}
 
-    * new: ``raw_codes`` + ``radius`` (+ ``warp_alpha``) -> table ``raw / radius``
-      computed on ``device`` (so its fp32 bits are the reference's on the same
-      device), raw codes kept for per-layer ``chosen_r``;
-    * mid: pre-divided ``codebook`` + ``saved_radius``;
-    * old: pre-divided ``codebook``, radius from ``quant_config.json``.
+
+def _legacy_radius(blob: Dict, quantized_dir: Path) -> Optional[float]:
+    """Radius of a pre-divided table: ``saved_radius`` in the mid format,
+    else ``codebook_radius`` from ``quant_config.json`` (old format), else
+    unknown (the quantizer's default stays)."""
+    if "saved_radius" in blob:
+        return float(blob["saved_radius"])
+    if not (quantized_dir / "quant_config.json").exists():
+        return None
+    r = load_quantization_config(quantized_dir).get("codebook_radius")
+    return None if r is None else float(r)
+
+
+def load_quantizer(quantized_dir, device: str = "cuda") -> BaseQuantizer:
+    """The codebook of a quantized directory (``reconstruct.py:39-90``).
+
+    Three ``quantizer.pt`` formats:
+
+    * ``raw_codes`` + ``radius`` (+ ``warp_alpha``): the table is
+      ``raw / radius`` divided on ``device`` — so its fp32 bits are those
+      the reference computes on the same device — then warped when
+      ``warp_alpha != 1``; the raw codes stay for per-layer ``chosen_r``.  A
+      type other than ``e8_lattice`` reads as E8-D4, as in the reference;
+    * ``codebook`` + ``saved_radius``: a pre-divided table and its radius;
+    * ``codebook`` alone: a pre-divided table, radius from
+      ``quant_config.json``.
     """
     quantized_dir = Path(quantized_dir)
-    data = torch.load(quantized_dir / "quantizer.pt", weights_only=True, map_location="cpu")
-    qtype = data.get("quantizer_type", "e8_lattice")
-    if "raw_codes" in data:
-        raw = data["raw_codes"].float().to(device)
-        radius = float(data["radius"])
-        if qtype == "e8_lattice":
-            eq = E8LatticeQuantizer(device=device, codebook=raw / radius)
-            eq._raw_points = raw
-        else:
-            eq = E8D4Quantizer(device=device, codebook=raw / radius)
-            eq._raw_codes = raw
-        eq._radius = radius
-        warp_alpha = float(data.get("warp_alpha", 1.0))
-        if warp_alpha != 1.0:
-            eq.warp_codebook(warp_alpha)
-        return eq
-    codebook = data["codebook"].float().to(device)
-    if qtype == "e8_lattice":
-        eq = E8LatticeQuantizer(device=device, codebook=codebook)
-    elif qtype == "e8_d4":
-        eq = E8D4Quantizer(device=device, codebook=codebook)
-    else:
-        raise ValueError(f"Unknown quantizer type: {qtype}")
-    if "saved_radius" in data:
-        eq._radius = float(data["saved_radius"])
-    else:
-        cfg_path = quantized_dir / "quant_config.json"
-        if cfg_path.exists():
-            with open(cfg_path) as f:
-                actual = json.load(f).get("codebook_radius")
-            if actual is not None:
-                eq._radius = float(actual)
-    return eq
+    blob = torch.load(quantized_dir / "quantizer.pt", weights_only=True, map_location="cpu")
+    kind = blob.get("quantizer_type", "e8_lattice")
+    if "raw_codes" in blob:
+        cls = E8LatticeQuantizer if kind == "e8_lattice" else E8D4Quantizer
+        q = cls.from_raw(blob["raw_codes"].float().to(device), float(blob["radius"]))
+        alpha = float(blob.get("warp_alpha", 1.0))
+        if alpha != 1.0:
+            q.warp_codebook(alpha)
+        return q
+    cls = _QUANTIZER_CLASSES.get(kind)
+    if cls is None:
+        raise ValueError(f"{quantized_dir / 'quantizer.pt'}: unsupported quantizer type {kind!r} "
+                         f"(expected one of {sorted(_QUANTIZER_CLASSES)})")
+    q = cls(device=device, codebook=blob["codebook"].float().to(device))
+    radius = _legacy_radius(blob, quantized_dir)
+    if radius is not None:
+        q._radius = radius
+    return q
 
 
 def save_quantizer(eq: BaseQuantizer, output_dir, quantizer_type: str) -> None:

@@ -117,8 +117,10 @@ long long eptq_e8d4_work_bytes(void);
  * Same arguments, checks and results as eptq_e8d4_forward_multi with a
  * workspace of that size.
  *
- * Limit: at most 16384 tiles of 64 output rows (1048576 rows) over all layers
- * of a call, else EPTQ_EUNSUPPORTED.  The first call on a device looks the
+ * Limit: the scratch holds 16384 tile counters and partial sums for 256
+ * CUs; a launch with more than 16384 tiles of 64 output rows (1048576 rows
+ * over its layers) runs unsplit, exactly as eptq_e8d4_forward_multi does
+ * with a workspace of this size.  The first call on a device looks the
  * array up and queues a kernel on `stream` that zeroes its counters (make
  * that call outside graph capture); every launch that uses a counter returns
  * it to zero.  All calls on one GPU share its array, which keeps the last

@@ -164,14 +164,28 @@ def test_fused_llama_linears_validate_arguments(lib):
     assert h(16, None, 16, 1e-5, 16, 100, 1000, 1, 16, 16, None, 16, None) == 2            # hidden size
 
 
-def test_noalloc_rejects_more_tiles_than_its_scratch_counts(lib):
-    """The allocation-free variant's scratch holds 16384 tile counters (64
-    output rows each); a call over more rows is refused before any device
-    call, with the limit in the message."""
+def test_noalloc_checks_like_the_workspace_form(lib):
+    """The allocation-free variant runs the same argument checks as
+    eptq_e8d4_forward_multi, before it looks its scratch up (no device call
+    for a refused or empty call), and sets no tile limit of its own: a call
+    over more 64-row tiles than the scratch counts (4 x 4097 here) passes the
+    checks and, on a GPU, runs unsplit."""
     L = _lib.EptqLayer
-    four = (L * 4)(*([L(16, 16, 16, None, None, 16, None, None, 0, 32769, 0)] * 4))   # 4 x 4097 tiles
-    rc = lib.eptq_e8d4_forward_multi_noalloc(4, four, 16, _lib.EPTQ_F16, 16, _lib.EPTQ_F16, 64, 1, 16,
-                                             8 * 32769, None)
-    assert rc == _lib.EPTQ_EUNSUPPORTED
-    msg = lib.eptq_last_error().decode()
-    assert "tile counters" in msg and "1048576 output rows" in msg
+    four = (L * 4)(*([L(16, 16, 16, None, None, 16, None, None, 0, 32769, 0)] * 4))
+    fm, na = lib.eptq_e8d4_forward_multi, lib.eptq_e8d4_forward_multi_noalloc
+    cases = [
+        (0, four, 16, 16, 64, 1, 16, 8 * 32769, _lib.EPTQ_EINVAL),          # no layers
+        (4, four, 16, 16, 64, -1, 16, 8 * 32769, _lib.EPTQ_EINVAL),         # B < 0
+        (4, four, 16, 8, 64, 1, 16, 8 * 32769, _lib.EPTQ_EUNSUPPORTED),     # x misaligned
+        (4, four, 16, 16, 60, 1, 16, 8 * 32769, _lib.EPTQ_EUNSUPPORTED),    # N % 8
+        (4, four, 16, 16, 64, 1, 16, 8 * 32768, _lib.EPTQ_EINVAL),          # layer outside y's row
+        (4, four, 16, 16, 64, 0, 16, 8 * 32769, _lib.EPTQ_OK),              # B = 0: nothing to do
+    ]
+    for n, ls, codes, x, N, B, y, ldy, want in cases:
+        rc_w = fm(n, ls, codes, _lib.EPTQ_F16, x, _lib.EPTQ_F16, N, B, y, ldy, None, 0, None)
+        msg_w = lib.eptq_last_error().decode()
+        rc_n = na(n, ls, codes, _lib.EPTQ_F16, x, _lib.EPTQ_F16, N, B, y, ldy, None)
+        msg_n = lib.eptq_last_error().decode()
+        assert rc_w == rc_n == want, (n, N, B, ldy, rc_w, rc_n)
+        if want:
+            assert msg_n.replace("_noalloc", "") == msg_w, (msg_w, msg_n)
