@@ -22,6 +22,7 @@ sees each quantized Linear as one op with no graph break.
 from __future__ import annotations
 
 
+import threading
 from typing import List, Optional
 
 import torch
@@ -112,7 +113,7 @@ def decode_workspace(device) -> torch.Tensor:
 
 # One split-K workspace per (device, stream): launches on one stream run one
 # after another, so modules that share their stream's workspace never overlap
-# on it.  Created on first eager use (zero-filled on that stream).
+# on it.  Created on first eager use, zero-filled before that stream uses it.
 _STREAM_WORK: dict = {}
 
 
@@ -134,10 +135,37 @@ def stream_workspace(device) -> Optional[torch.Tensor]:
     key = (device.index if device.index is not None else torch.cuda.current_device(), stream.cuda_stream)
     w = _STREAM_WORK.get(key)
     if w is None:
-        with torch.cuda.device(device), torch.cuda.stream(stream):
-            w = decode_workspace(device)
+        w = _workspace_outside_graph_pools(device, stream)
         _STREAM_WORK[key] = w
     return w
+
+
+def _workspace_outside_graph_pools(device, stream) -> torch.Tensor:
+    """``decode_workspace`` allocated and zero-filled by a helper thread on a
+    stream of its own, then ordered before ``stream``.  The calling thread
+    may be routing its allocations into a graph's private memory pool
+    (torch.compile's cudagraph warm-up runs do, per thread), where a buffer
+    kept alive across calls does not belong."""
+    box = {}
+
+    def run():
+        try:
+            with torch.cuda.device(device):
+                side = torch.cuda.Stream(device)
+                side.wait_stream(stream)
+                with torch.cuda.stream(side):
+                    box["w"] = decode_workspace(device)
+                    box["ev"] = side.record_event()
+        except BaseException as e:  # re-raised in the caller
+            box["err"] = e
+
+    t = threading.Thread(target=run, name="eptq-workspace")
+    t.start()
+    t.join()
+    if "err" in box:
+        raise box["err"]
+    stream.wait_event(box["ev"])
+    return box["w"]
 
 
 def linear_forward_multi(layers, codes, x, work: Optional[torch.Tensor] = None) -> torch.Tensor:
