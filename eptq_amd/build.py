@@ -13,7 +13,7 @@ from pathlib import Path
 
 ROOT = Path(__file__).resolve().parent
 REPO = ROOT.parent
-SOURCES = ["abi.hip", "dequant.hip", "matvec.hip", "decode.hip", "decode_mfma.hip", "gemm.hip", "llama_ops.hip", "chain.hip"]
+SOURCES = ["abi.hip", "dequant.hip", "matvec.hip", "decode.hip", "decode_mfma.hip", "gemm.hip", "llama_ops.hip"]
 OUT = ROOT / "_lib" / "libeptq_hip.so"
 
 HIPCC_FLAGS = [

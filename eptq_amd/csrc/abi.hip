@@ -343,14 +343,6 @@ int forward_multi(const char* fn, int n_layers, const eptq_layer* layers, const 
 
 }  // namespace
 
-int eptq::set_error(int code, const char* fmt, ...) {
-  va_list ap;
-  va_start(ap, fmt);
-  vsnprintf(g_err, sizeof(g_err), fmt, ap);
-  va_end(ap);
-  return code;
-}
-
 extern "C" {
 
 int eptq_abi_version(void) { return 3; }

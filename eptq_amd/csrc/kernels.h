@@ -10,9 +10,6 @@ namespace eptq {
 
 enum { KIND_E8D4 = 0, KIND_E8 = 1 };
 
-// Record an error message for eptq_last_error() (this host thread) and
-// return `code`.
-int set_error(int code, const char* fmt, ...);
 
 struct DequantArgs {
   const int16_t* Q;
