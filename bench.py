@@ -481,14 +481,18 @@ def decode_batches(torch, dev, stream_bytes=576 << 20):
                 copies.append((keep, arr))
             N = shapes[0][1]
             width = sum(o for o, _ in shapes)
-            for B in batches:
+            # Llama-3 runs in bf16 (HF default): its units also with bf16 x and y.
+            for B, bf in [(B, False) for B in batches] + ([(B, True) for B in batches] if qb else []):
                 x = make_x(B, N, seed=B, device=dev)
-                y = torch.empty((B, width), dtype=torch.float16, device=dev)
+                if bf:
+                    x = x.bfloat16()
+                y = torch.empty((B, width), dtype=x.dtype, device=dev)
+                xdt = _lib.EPTQ_BF16 if bf else _lib.EPTQ_F16
 
                 def f():
                     for keep, arr in copies:
                         rc = lib.eptq_e8d4_forward_multi(len(keep), arr, codes.data_ptr(), _lib.EPTQ_F16,
-                                                         x.data_ptr(), _lib.EPTQ_F16, N, B, y.data_ptr(), width,
+                                                         x.data_ptr(), xdt, N, B, y.data_ptr(), width,
                                                          work.data_ptr(), work.numel(), stream.cuda_stream)
                         if rc:
                             _lib.check(rc, "eptq_e8d4_forward_multi")
@@ -498,9 +502,10 @@ def decode_batches(torch, dev, stream_bytes=576 << 20):
                 nbytes = sum(algo_bytes(8 * qd.Q.shape[0], qd.Q.shape[1], B, int(qd.O.shape[0]),
                                         n_groups=0 if qd.S_group is None else int(qd.S_group.shape[0]))
                              for qd, _, _ in copies[0][0])
-                res[f"{uname} B={B}"] = {"shape": " + ".join(f"{o}x{i}" for o, i in shapes), "us": round(us, 2),
-                                         "gbs": round(nbytes / (us * 1e-6) / 1e9, 1),
-                                         "kernel": "k_decode_mfma" if B >= 5 else DECODE_KERNEL}
+                res[f"{uname} B={B}" + (" bf16" if bf else "")] = {
+                    "shape": " + ".join(f"{o}x{i}" for o, i in shapes), "us": round(us, 2),
+                    "gbs": round(nbytes / (us * 1e-6) / 1e9, 1),
+                    "kernel": "k_decode_mfma" if B >= 5 else DECODE_KERNEL}
                 del x, y
             del copies
             torch.cuda.empty_cache()

@@ -43,6 +43,22 @@ template <> struct Act<bf16> {
   }
 };
 
+// Two activation elements (one 32-bit word) as an fp16 pair.  bf16 values
+// convert exactly while they lie in fp16's normal range (bf16 carries 8
+// significand bits, fp16 11), so round-toward-zero conversion loses nothing
+// there; beyond it values saturate at the largest finite fp16.
+template <typename T> __device__ __forceinline__ uint32_t to_f16x2(uint32_t w);
+template <> __device__ __forceinline__ uint32_t to_f16x2<f16>(uint32_t w) { return w; }
+template <> __device__ __forceinline__ uint32_t to_f16x2<bf16>(uint32_t w) {
+  const auto p = __builtin_amdgcn_cvt_pkrtz(__builtin_bit_cast(float, w << 16),
+                                            __builtin_bit_cast(float, w & 0xffff0000u));
+  return __builtin_bit_cast(uint32_t, p);
+}
+// One element as fp16 (same conversion).
+template <typename T> __device__ __forceinline__ f16 to_f16(uint16_t b) {
+  return __builtin_bit_cast(f16, (uint16_t)(to_f16x2<T>((uint32_t)b) & 0xffffu));
+}
+
 // Bitfield insert: (mask & a) | (~mask & b) in one VALU op.
 // (t >> 16) & 0xFF8 in one op (SDWA word select of the second operand): the
 // table byte address of the upper index of a 32-bit word t = w >> 4.

@@ -266,10 +266,7 @@ int launch_decode_e8d4_multi(const LinearArgs* l, int n, hipStream_t s, void* wo
   if (a.prep != 0 && a.x_bf16) return -1;
   if (a.B < 1 || a.B > 8) return -1;
   if (a.codes_f32) return -1;  // fp32 tables take the generic kernel
-  if (a.x_bf16) {
-    if (a.B >= 2) return -1;   // the B >= 2 pairs are formed in fp16 arithmetic
-    return a.S ? launch_bt<1, true, bf16>(l, n, s) : launch_bt<1, false, bf16>(l, n, s);
-  }
+  if (a.x_bf16) return a.S ? launch_b<true, bf16>(l, n, s) : launch_b<false, bf16>(l, n, s);
   return a.S ? launch_b<true, f16>(l, n, s) : launch_b<false, f16>(l, n, s);
 }
 

@@ -20,7 +20,8 @@
 //    columns by a power of two 2^-e with max|x·h|·2^-e in [0.5, 1); packed
 //    fp16 FMAs accumulate a chunk (two rows per op), and one mixed-precision
 //    FMA per row moves the chunk sum into fp32 times 2^e.
-//  * B >= 2: the two indices of a 32-bit word (adjacent columns) are paired:
+//  * B >= 2 (bf16 x taken to fp16 first, exactly in fp16's normal range):
+//    the two indices of a 32-bit word (adjacent columns) are paired:
 //    byte permutes turn their two table vectors into (c_k(n), c_k(n+1)) fp16
 //    pairs and one v_dot2_f32_f16 per (k, b) accumulates both columns in
 //    fp32.  The activation pairs x·h are rounded to fp16 after scaling h by a
@@ -490,7 +491,7 @@ struct Layer {
           for (int b = 0; b < BT; ++b) {
             u32x4 w;
 #pragma unroll
-            for (int d = 0; d < 4; ++d) w[d] = pk_mul(xw[b][d], pk_mul(hw[d], dn));
+            for (int d = 0; d < 4; ++d) w[d] = pk_mul(to_f16x2<XT>(xw[b][d]), pk_mul(hw[d], dn));
             *(u32x4*)(xsd + b * NP + c * 8) = w;
           }
         }

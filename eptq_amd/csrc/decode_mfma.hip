@@ -89,8 +89,10 @@ __host__ __device__ inline size_t dyn_bytes(int N, bool has_s, int S) {
   return act > red ? act : red;
 }
 
-template <int S, bool HAS_S>
+template <int S, bool HAS_S, typename XT>
 // At most 168 VGPRs (3 waves per SIMD): one 9-wave workgroup per CU.
+// XT: activation and output type (bf16 x is taken to fp16 exactly in fp16's
+// normal range before the scale; y is rounded from the fp32 sums to XT).
 // Work split: tiles [0, T1) take one workgroup each; the tiles from T1 on
 // have their columns split over P workgroups (T1 = 0: every tile).  ma.start
 // counts tiles.
@@ -270,7 +272,7 @@ __global__ __launch_bounds__((S + 1) * 64, 3) void k_decode_mfma(MultiArgs ma, i
         const u32x4 sc = *(const u32x4*)(hsa + blk * kBlk + 16 * kg + 8 * g2);
         u32x4 bx;
 #pragma unroll
-        for (int d = 0; d < 4; ++d) bx[d] = pk_mul(x[g2][d], sc[d]);
+        for (int d = 0; d < 4; ++d) bx[d] = pk_mul(to_f16x2<XT>(x[g2][d]), sc[d]);
         u32x2 lo[4], hi[4];
         half.lookup(q[g2], tabB, lo, hi);
 #pragma unroll
@@ -312,7 +314,7 @@ __global__ __launch_bounds__((S + 1) * 64, 3) void k_decode_mfma(MultiArgs ma, i
         u32x4 wo[2], wm[2];
 #pragma unroll
         for (int q = 0; q < 8; ++q) {
-          const f16 x0 = as_f16(xb[2 * q]), x1 = as_f16(xb[2 * q + 1]);
+          const f16 x0 = to_f16<XT>(xb[2 * q]), x1 = to_f16<XT>(xb[2 * q + 1]);
           wo[q >> 2][q & 3] = (uint32_t)bits(x0 * h1) | ((uint32_t)bits(x1 * h1) << 16);
           if (HAS_S) wm[q >> 2][q & 3] = (uint32_t)bits(x0 * hm) | ((uint32_t)bits(x1 * hm) << 16);
         }
@@ -381,7 +383,7 @@ __global__ __launch_bounds__((S + 1) * 64, 3) void k_decode_mfma(MultiArgs ma, i
         const int ge = ebase + e2;
         const int col = gp(a.O_col)[ge];
         const f16x8 o = *gp((const f16x8*)(a.O + (size_t)ge * 8));
-        const f16 x16 = as_f16(gp(a.x)[(size_t)b * ldx + col]);
+        const f16 x16 = to_f16<XT>(gp(a.x)[(size_t)b * ldx + col]);
         const f16 h1 = as_f16(gp((const uint16_t*)a.h)[col]) * down;
         const float xo = (float)(f16)(x16 * h1);
         const float xm = HAS_S ? (float)(f16)(x16 * (f16)(h1 * as_f16(gp((const uint16_t*)a.S)[(size_t)grp * N + col]))) : xo;
@@ -445,7 +447,7 @@ __global__ __launch_bounds__((S + 1) * 64, 3) void k_decode_mfma(MultiArgs ma, i
       const int b = ((tid + NT * it) >> 5) & 15;
       const float y0 = s0[it] * out_scale * (float)gg[0] + (float)bb[0];
       const float y1 = s1[it] * out_scale * (float)gg[1] + (float)bb[1];
-      const uint32_t pk = (uint32_t)bits((f16)y0) | ((uint32_t)bits((f16)y1) << 16);
+      const uint32_t pk = (uint32_t)Act<XT>::from_f32(y0) | ((uint32_t)Act<XT>::from_f32(y1) << 16);
       *gp((uint32_t*)(a.y + (size_t)b * a.ldy + orow)) = pk;
     }
   }
@@ -462,7 +464,7 @@ inline int parts_for(int split, int tiles, void* work, long long work_bytes) {
   return P;
 }
 
-template <int S, bool HAS_S>
+template <int S, bool HAS_S, typename XT>
 int launch_t(const LinearArgs* l, int n, hipStream_t s, void* work, long long work_bytes) {
   int tiles = 0;
   for (int k = 0; k < n; ++k) tiles += (l[k].M + kTile - 1) / kTile;
@@ -481,7 +483,7 @@ int launch_t(const LinearArgs* l, int n, hipStream_t s, void* work, long long wo
     ma.start[k + 1] = ma.start[k] + (k < n ? (l[k].M + kTile - 1) / kTile : 0);   // tiles
   }
   const int grid = T1 + (tiles - T1) * P;
-  auto kern = k_decode_mfma<S, HAS_S>;
+  auto kern = k_decode_mfma<S, HAS_S, XT>;
   const size_t dyn = dyn_bytes(l[0].N, HAS_S, S);
   static size_t attr = 0;
   if (dyn > attr) {
@@ -502,7 +504,7 @@ int launch_t(const LinearArgs* l, int n, hipStream_t s, void* work, long long wo
 int launch_decode_mfma_multi(const LinearArgs* l, int n, hipStream_t s, void* work, long long work_bytes) {
   if (n < 1 || n > kMaxLayers) return -1;
   const LinearArgs& a = l[0];
-  if (a.B < 1 || a.B > 16 || a.x_bf16 || a.codes_f32 || a.prep != 0 || (a.N & 7) != 0) return -1;
+  if (a.B < 1 || a.B > 16 || a.codes_f32 || a.prep != 0 || (a.N & 7) != 0) return -1;
   // y is written in pairs of fp16 (4-byte stores).
   if ((a.ldy & 1) != 0 || ((uintptr_t)a.y & 3) != 0) return -1;
   for (int i = 0; i < n; ++i) {
@@ -521,8 +523,11 @@ int launch_decode_mfma_multi(const LinearArgs* l, int n, hipStream_t s, void* wo
   // (Two 6-wave workgroups per CU for layers with more tiles than CUs, so
   // that they run in one round, measured slower than two rounds of 9-wave
   // workgroups: gate|up 11008x4096 at B=8 24.6 us against 22.2 us.)
-  return a.S ? dmf::launch_t<dmf::kS, true>(l, n, s, work, work_bytes)
-             : dmf::launch_t<dmf::kS, false>(l, n, s, work, work_bytes);
+  if (a.x_bf16)
+    return a.S ? dmf::launch_t<dmf::kS, true, bf16>(l, n, s, work, work_bytes)
+               : dmf::launch_t<dmf::kS, false, bf16>(l, n, s, work, work_bytes);
+  return a.S ? dmf::launch_t<dmf::kS, true, f16>(l, n, s, work, work_bytes)
+             : dmf::launch_t<dmf::kS, false, f16>(l, n, s, work, work_bytes);
 }
 
 long long decode_mfma_work_bytes() {

@@ -85,7 +85,7 @@ int launch_decode_e8d4_multi(const LinearArgs* layers, int n, hipStream_t s, voi
 // layers[0].ldy; -1 when the pair is outside the kernel's range.
 int launch_decode_e8d4_pair(const LinearArgs* layers, hipStream_t s);
 
-// Matrix-core E8-D4 decode (B <= 16, fp16 x and table, no fused preparation);
+// Matrix-core E8-D4 decode (B <= 16, fp16 or bf16 x, fp16 table, no fused preparation);
 // -1 when the layers are outside its range.
 int launch_decode_mfma_multi(const LinearArgs* layers, int n, hipStream_t s, void* work = nullptr,
                              long long work_bytes = 0);

@@ -9,7 +9,8 @@ cases 2e-2 for the bf16 input and output roundings):
 * configuration 2 — Llama-3-8B q/o 4096x4096, k/v 1024x4096, gate/up
   14336x4096, down 4096x14336 with S_group (qb = 128), 0.2% critical blocks,
   batch 1, 4 and 16;
-* bf16 activations at batch 1 (the reference's default decode output type,
+* bf16 activations at batch 1 and at 2, 3, 4, 8 and 16 (the reference's
+  default decode output type,
   ``kernels/triton_e8d4.py:181``), with and without S_group, through the
   single-layer and the multi-layer entry points;
 * configuration 3 — Llama-2-13B 5120x5120, 13824x5120, 5120x13824 at 2048
@@ -101,6 +102,43 @@ def test_config2_batches(out, inp):
         e = rel_l2(_single(L, x), _ref(qd, W, x))
         print(f"  rel_l2 {e:.2e}", flush=True)
         assert e <= TOL, (out, inp, B)
+
+
+@pytest.mark.parametrize("qb", [None, 128])
+def test_bf16_batches_2_to_16(qb):
+    """bf16 x and y at B = 2, 3, 4, 8 and 16 (the reference decodes bf16 for
+    every B < 256, kernels/triton_e8d4.py:160-193): the vector kernel's bf16
+    instances up to 8 rows and the matrix-core kernel's from 5, single-layer
+    and multi-layer (q|k|v-like shapes, with the split-K workspace)."""
+    shapes = [(4096, 4096), (1024, 4096), (1024, 4096)]
+    qds, Ws = [], []
+    for k, (o, i) in enumerate(shapes):
+        qd = make_layer(o, i, seed=500 + k + (qb or 0), percmask=0.002, qb_size=qb, bias=k == 2)
+        n = layer_np(qd)
+        Ws.append(dequantize_layer(n["Q"], n["g"], n["h"], n["O"], table("e8_d4", 1.75), "e8_d4",
+                                   n["S_group"]).astype(np.float32))
+        qds.append(qd)
+    Ls = [_dev(qd) for qd in qds]
+    t = torch.from_numpy(table("e8_d4", 1.75)).half().cuda()
+    work = decode_workspace("cuda")
+    for B in (2, 3, 4, 8, 16):
+        x = make_x(B, 4096, seed=40 + B).bfloat16()
+        xf = x.float()
+        print(f"bf16 B={B} qb={qb}: single-layer and multi-layer", flush=True)
+        for qd, W, L in zip(qds[:2], Ws[:2], Ls[:2]):
+            y = linear_forward("e8_d4", L["Q"], t, L["g"], L["h"], x.cuda(), L["O_vals"], L["O_col"], L["O_row_ptr"],
+                               L["bias"], L["S_group"])
+            assert y.dtype == torch.bfloat16
+            e = rel_l2(y.float().cpu().numpy(), _ref(qd, W, xf))
+            print(f"  single rel_l2 {e:.2e}", flush=True)
+            assert e <= TOL_BF16, (B, qb)
+        y = linear_forward_multi(Ls, t, x.cuda(), work=work)
+        torch.cuda.synchronize()
+        assert y.dtype == torch.bfloat16
+        want = np.concatenate([_ref(qd, W, xf) for qd, W in zip(qds, Ws)], axis=1)
+        e = rel_l2(y.float().cpu().numpy(), want)
+        print(f"  multi rel_l2 {e:.2e}", flush=True)
+        assert e <= TOL_BF16, (B, qb)
 
 
 @pytest.mark.parametrize("qb", [None, 128])
