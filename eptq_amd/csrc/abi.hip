@@ -116,8 +116,10 @@ int layer_args(const char* fn, int kind, const void* Q, const void* codes, int c
   return EPTQ_OK;
 }
 
-// Launch one layer on the kernel for its codebook and batch size.
-int dispatch(const char* fn, int kind, const eptq::LinearArgs& a, hipStream_t s) {
+// Launch one layer on the kernel for its codebook and batch size (work: an
+// optional decode workspace, see eptq_e8d4_forward_multi).
+int dispatch(const char* fn, int kind, const eptq::LinearArgs& a, hipStream_t s, void* work = nullptr,
+             long long work_bytes = 0) {
   int rc = 0;
   if (a.B <= eptq::kMatvecMaxBatch) {
     if (kind == eptq::KIND_E8D4) {
@@ -127,7 +129,7 @@ int dispatch(const char* fn, int kind, const eptq::LinearArgs& a, hipStream_t s)
       rc = eptq::launch_matvec<eptq::KIND_E8>(a, s);
     }
   } else if (kind == eptq::KIND_E8D4) {
-    rc = eptq::launch_gemm<eptq::KIND_E8D4>(a, s);
+    rc = eptq::launch_gemm<eptq::KIND_E8D4>(a, s, work, work_bytes);
   } else {
     rc = eptq::launch_gemm<eptq::KIND_E8>(a, s);
   }
@@ -333,7 +335,7 @@ int forward_multi(const char* fn, int n_layers, const eptq_layer* layers, const 
                  L.O_row_ptr, L.bias, L.S_group, L.n_groups, L.M, N, B, &t);
       t.y = (uint16_t*)y + L.y_offset;
       t.ldy = ldy;
-      const int rc = dispatch(fn, eptq::KIND_E8D4, t, s);
+      const int rc = dispatch(fn, eptq::KIND_E8D4, t, s, work, work ? work_bytes : 0);
       if (rc) return rc;
     }
   }
@@ -381,7 +383,9 @@ int eptq_e8d4_forward_multi_noalloc(int n_layers, const eptq_layer* layers, cons
                        y, ldy, nullptr, 0, stream, true);
 }
 
-long long eptq_e8d4_work_bytes(void) { return eptq::decode_mfma_work_bytes(); }
+long long eptq_e8d4_work_bytes(void) {
+  return eptq::decode_mfma_work_bytes() + (long long)eptq::kPrefillSplitBytes;
+}
 
 int eptq_llama_norm_linear(int n_layers, const eptq_layer* layers, const void* codes,
                            const void* resid, const void* delta, const void* w, float eps,

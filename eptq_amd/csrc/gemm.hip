@@ -705,8 +705,14 @@ template <int BF> struct Lay {
 
 // NPW producer waves: 4, or 8 when the MFMA waves' registers allow four
 // waves per SIMD.
+//
+// Split K (part != null): the grid is P copies of the OB × TB tiles, copy p
+// taking K-steps [p·nk/P, (p+1)·nk/P); each writes its fp32 sums times 2^e
+// to part[p][token][feature] (8M features per token) and k_gemm_split_sum
+// adds the P copies in part order, then applies g and bias.
 template <int BF, int NPW>
-__global__ __launch_bounds__(64 * (8 + NPW), (8 + NPW) / 4) void k_gemm_lds_e8d4(LinearArgs a, int OB) {
+__global__ __launch_bounds__(64 * (8 + NPW), (8 + NPW) / 4) void k_gemm_lds_e8d4(LinearArgs a, int OB, int P,
+                                                                               float* __restrict__ part) {
   using L = g3::Lay<BF>;
   constexpr int kBK = g3::kBK, kBT = g3::kBT, kNT = 64 * (8 + NPW);
   static_assert(NPW == 4 || NPW == 8, "producer waves");
@@ -728,9 +734,14 @@ __global__ __launch_bounds__(64 * (8 + NPW), (8 + NPW) / 4) void k_gemm_lds_e8d4
   int blk = blockIdx.x;
   const int G = gridDim.x;
   if ((G & 7) == 0) blk = (blk & 7) * (G >> 3) + (blk >> 3);
+  const int tiles = G / P;
+  const int pp = blk / tiles;
+  blk -= pp * tiles;
   const int ob = blk % OB, tb = blk / OB;
   const int m0 = ob * QR, f0 = 8 * m0, t0 = tb * kBT;
   const int nk = N / kBK, nch = N / 8;
+  // This workgroup's K-steps [k0, k1) (all of them without a split).
+  const int k0 = pp * nk / P, k1 = (pp + 1) * nk / P, nkp = k1 - k0;
 
   // ---- table scaled by 2^-e (2^e >= max |h|), CSR rows, staged entries ----
   const f16x4 tl = ((const f16x4*)a.codes)[tid & 511];
@@ -861,23 +872,26 @@ __global__ __launch_bounds__(64 * (8 + NPW), (8 + NPW) / 4) void k_gemm_lds_e8d4
       }
     };
 
-    issue_i(0, 0);
-    if (nk > 1) issue_i(1, 1);
-    issue_x(0, 0);
+    // Stages alternate by step within this workgroup's range: step k0 + j
+    // uses stage j & 1.  The entry cursors start at each row's first entry;
+    // the first decode walks past the entries left of column 64·k0.
+    issue_i(k0, 0);
+    if (nkp > 1) issue_i(k0 + 1, 1);
+    issue_x(k0, 0);
     __syncthreads();   // table, entries, row pointers
 #pragma unroll
     for (int p = 0; p < NP; ++p) ncol[p] = ec[p] < ee[p] ? ecol[ec[p]] : 0x7fffffff;
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    decode(0, 0);
-    for (int kt = 0; kt < nk; ++kt) {
-      // Before the barrier: X(kt), indices(kt+1) landed, W(kt) written.
+    decode(k0, 0);
+    for (int j = 0; j < nkp; ++j) {
+      // Before the barrier: X(k0 + j), indices(k0 + j + 1) landed, W(k0 + j) written.
       asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
       __builtin_amdgcn_s_barrier();
       asm volatile("" ::: "memory");
-      if (kt + 2 < nk) issue_i(kt + 2, kt & 1);
-      if (kt + 1 < nk) {
-        issue_x(kt + 1, (kt + 1) & 1);
-        decode(kt + 1, (kt + 1) & 1);
+      if (j + 2 < nkp) issue_i(k0 + j + 2, j & 1);
+      if (j + 1 < nkp) {
+        issue_x(k0 + j + 1, (j + 1) & 1);
+        decode(k0 + j + 1, (j + 1) & 1);
       }
     }
     return;
@@ -892,12 +906,12 @@ __global__ __launch_bounds__(64 * (8 + NPW), (8 + NPW) / 4) void k_gemm_lds_e8d4
 #pragma unroll
     for (int q = 0; q < TB; ++q) acc[x][q] = (f32x4){0.f, 0.f, 0.f, 0.f};
   __syncthreads();   // the producers' first barrier
-  for (int kt = 0; kt < nk; ++kt) {
+  for (int j = 0; j < nkp; ++j) {
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
-    const char* xb = smem + L::X0 + (kt & 1) * L::XS;
-    const char* wb = smem + L::W0 + (kt & 1) * L::WS;
+    const char* xb = smem + L::X0 + (j & 1) * L::XS;
+    const char* wb = smem + L::W0 + (j & 1) * L::WS;
     f16x8 af[2][FA], bf[2][TB];
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
@@ -927,6 +941,7 @@ __global__ __launch_bounds__(64 * (8 + NPW), (8 + NPW) / 4) void k_gemm_lds_e8d4
       const int ehi = rps[q + 1] - e0;
       for (int e = elo; e < ehi; ++e) {
         const int col = a.O_col[e0 + e];
+        if (col < kBK * k0 || col >= kBK * k1) continue;   // another part's columns
         const f16x8 o = ((const f16x8*)a.O)[e0 + e];
         const f16 hc = __builtin_bit_cast(f16, a.h[col]);
         float dv[4];   // this lane's 4 features 16·(fl0/16) + 4·lg + v
@@ -954,6 +969,25 @@ __global__ __launch_bounds__(64 * (8 + NPW), (8 + NPW) / 4) void k_gemm_lds_e8d4
     }
   }
 
+  // ---- split K: this part's sums times 2^e, for k_gemm_split_sum ----
+  if (part) {
+    const size_t F = 8 * (size_t)a.M;
+#pragma unroll
+    for (int x = 0; x < FA; ++x) {
+      const int f = f0 + wf * FW + 16 * x + 4 * kg;
+#pragma unroll
+      for (int q = 0; q < TB; ++q) {
+        const int tt = t0 + wt * TW + 16 * q + i;
+        if (tt >= T) continue;
+        f32x4 o;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) o[v] = acc[x][q][v] * out_scale;
+        *(f32x4*)(part + ((size_t)pp * T + tt) * F + f) = o;
+      }
+    }
+    return;
+  }
+
   // ---- y = acc·2^e·g + bias: lane (n, lg) holds 4 consecutive features of token n ----
 #pragma unroll
   for (int x = 0; x < FA; ++x) {
@@ -971,6 +1005,36 @@ __global__ __launch_bounds__(64 * (8 + NPW), (8 + NPW) / 4) void k_gemm_lds_e8d4
       *(f16x4*)(a.y + (size_t)tt * a.ldy + f) = o;
     }
   }
+}
+
+// y[t][f] = fp16((Σ_p part[p][t][f]) · g[f] + bias[f]), the parts added in
+// order (deterministic); 8 features per thread.
+__global__ __launch_bounds__(256) void k_gemm_split_sum(LinearArgs a, int P, const float* __restrict__ part) {
+  const size_t F = 8 * (size_t)a.M;
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;   // (token, 8-feature chunk)
+  const size_t nc = F / 8;
+  if (i >= (size_t)a.B * nc) return;
+  const size_t t = i / nc, f = (i - t * nc) * 8;
+  f32x4 s0 = *(const f32x4*)(part + t * F + f), s1 = *(const f32x4*)(part + t * F + f + 4);
+  for (int p = 1; p < P; ++p) {
+    const float* q = part + ((size_t)p * a.B + t) * F + f;
+    s0 += *(const f32x4*)q;
+    s1 += *(const f32x4*)(q + 4);
+  }
+  const f16x8 g8 = *(const f16x8*)(a.g + f);
+  f16x8 b8 = {};
+  if (a.bias) b8 = *(const f16x8*)(a.bias + f);
+  u16x8 o;
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    o[v] = Act<f16>::from_f32(s0[v] * (float)g8[v] + (float)b8[v]);
+    o[4 + v] = Act<f16>::from_f32(s1[v] * (float)g8[4 + v] + (float)b8[4 + v]);
+  }
+  // Two 8-byte stores: y rows are 8-byte aligned (the GEMM's own stores).
+  const u32x4 w = __builtin_bit_cast(u32x4, o);
+  u32x2* yp = (u32x2*)(a.y + t * a.ldy + f);
+  yp[0] = (u32x2){w[0], w[1]};
+  yp[1] = (u32x2){w[2], w[3]};
 }
 
 template <bool HAS_S>
@@ -995,7 +1059,7 @@ size_t static_lds(const void* kern) {
 }  // namespace
 
 template <int KIND>
-int launch_gemm(const LinearArgs& a, hipStream_t s) {
+int launch_gemm(const LinearArgs& a, hipStream_t s, void* work, long long work_bytes) {
   if (KIND == KIND_E8D4 && a.B <= kSliceMaxTokens && a.prep == 0) {
     // Eligibility does not depend on the slice (B = 1..16 all qualify), so a
     // first slice that launches means every slice does.
@@ -1032,6 +1096,42 @@ int launch_gemm(const LinearArgs& a, hipStream_t s) {
       // and narrower tiles shorten each step.
       if (bf == 128 && (long)(a.M / 8) * TB <= cus) bf = 64;
     }
+    // With a workspace the tile width and the K split are chosen together:
+    // time ~ rounds of the CUs x K-steps per part x a tile's step time
+    // (measured ~1.09 / 1.33 / 1.66 / 1.66 us for 64 / 128 / 160 / 256
+    // features on 4096-5120-column layers), plus the parts' fp32 sums
+    // written and read once at ~4 TB/s and the summing launch (~3 us).
+    int P = 1;
+    const size_t woff = (size_t)decode_mfma_work_bytes();
+    const size_t wavail = work && work_bytes > (long long)woff ? (size_t)work_bytes - woff : 0;
+    if (bf && wavail) {
+      const int nk = a.N / g3::kBK;
+      const double per = (double)a.B * 8 * a.M * 4;
+      const int widths[4] = {64, 128, 160, 256};
+      const double step[4] = {1.09, 1.33, 1.66, 1.66};
+      double best = -1;
+      int bw = bf, bp = 1;
+      for (int wi = 0; wi < 4; ++wi) {
+        const int w = widths[wi];
+        if (a.M % (w / 8) != 0) continue;
+        const long gw = (a.M / (w / 8)) * TB;
+        for (int pp = 1; pp <= kPrefillMaxParts; ++pp) {
+          if (pp > 1 && (gw * pp > cus || nk / pp < 8 || (size_t)(pp * per) > wavail)) break;
+          const double t = (double)((gw * pp + cus - 1) / cus) * ((nk + pp - 1) / pp) * step[wi] +
+                           (pp > 1 ? 2.0 * pp * per / 4.0e6 + 3.0 : 0.0);
+          if (best < 0 || t < best) {
+            best = t;
+            bw = w;
+            bp = pp;
+          }
+        }
+      }
+      // An unsplit choice keeps the measured width rule above.
+      if (bp > 1) {
+        bf = bw;
+        P = bp;
+      }
+    }
     const long grid = bf ? (a.M / (bf / 8)) * TB : 0;
     if (bf && grid <= 0x7fffffff) {
       // 160-feature tiles: 8 producer waves (the MFMA waves fit four waves per
@@ -1044,10 +1144,16 @@ int launch_gemm(const LinearArgs& a, hipStream_t s) {
       if (!attr[v]) attr[v] = hipFuncSetAttribute(kerns[v], hipFuncAttributeMaxDynamicSharedMemorySize, bytes[v]) == hipSuccess;
       if (attr[v]) {
         const int OB = a.M / (bf / 8);
-        if (v == 0) k_gemm_lds_e8d4<256, 4><<<(unsigned)grid, 768, bytes[0], s>>>(a, OB);
-        else if (v == 1) k_gemm_lds_e8d4<160, 8><<<(unsigned)grid, 1024, bytes[1], s>>>(a, OB);
-        else if (v == 2) k_gemm_lds_e8d4<128, 8><<<(unsigned)grid, 1024, bytes[2], s>>>(a, OB);
-        else k_gemm_lds_e8d4<64, 8><<<(unsigned)grid, 1024, bytes[3], s>>>(a, OB);
+        float* part = P > 1 ? (float*)((char*)work + woff) : nullptr;
+        const unsigned g = (unsigned)(grid * P);
+        if (v == 0) k_gemm_lds_e8d4<256, 4><<<g, 768, bytes[0], s>>>(a, OB, P, part);
+        else if (v == 1) k_gemm_lds_e8d4<160, 8><<<g, 1024, bytes[1], s>>>(a, OB, P, part);
+        else if (v == 2) k_gemm_lds_e8d4<128, 8><<<g, 1024, bytes[2], s>>>(a, OB, P, part);
+        else k_gemm_lds_e8d4<64, 8><<<g, 1024, bytes[3], s>>>(a, OB, P, part);
+        if (part) {
+          const size_t chunks = (size_t)a.B * a.M;   // 8-feature chunks
+          k_gemm_split_sum<<<(unsigned)((chunks + 255) / 256), 256, 0, s>>>(a, P, part);
+        }
         return 0;
       }
     }
@@ -1120,7 +1226,7 @@ int launch_gemm(const LinearArgs& a, hipStream_t s) {
   return 0;
 }
 
-template int launch_gemm<KIND_E8D4>(const LinearArgs&, hipStream_t);
-template int launch_gemm<KIND_E8>(const LinearArgs&, hipStream_t);
+template int launch_gemm<KIND_E8D4>(const LinearArgs&, hipStream_t, void*, long long);
+template int launch_gemm<KIND_E8>(const LinearArgs&, hipStream_t, void*, long long);
 
 }  // namespace eptq

@@ -69,7 +69,16 @@ struct MultiArgs {
 template <int KIND> int launch_dequant(const DequantArgs& a, hipStream_t s);
 template <int KIND> int launch_matvec(const LinearArgs& a, hipStream_t s);
 // MFMA prefill GEMM (B > 16); batch tiles of the matvec where it does not apply.
-template <int KIND> int launch_gemm(const LinearArgs& a, hipStream_t s);
+// work (nullable, work_bytes long): a decode workspace; past its first
+// decode_mfma_work_bytes() bytes, launches whose tiles leave half the CUs
+// idle or more split K over up to kPrefillMaxParts parts (fp32 sums there,
+// added in part order by a second launch).  Launches sharing it must not
+// overlap in time.
+template <int KIND> int launch_gemm(const LinearArgs& a, hipStream_t s, void* work = nullptr,
+                                    long long work_bytes = 0);
+constexpr int kPrefillMaxParts = 4;
+// The prefill area of a decode workspace (eptq_e8d4_work_bytes() includes it).
+constexpr size_t kPrefillSplitBytes = (size_t)64 << 20;
 // Persistent E8-D4 decode (B <= 8); -1 when the layer/batch is outside its range.
 int launch_decode_e8d4(const LinearArgs& a, hipStream_t s);
 // Several layers sharing x (same N, B, table, dtypes) in one launch; -1 when

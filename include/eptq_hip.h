@@ -95,16 +95,20 @@ typedef struct {
  * work: NULL, or a 16-byte aligned device buffer of work_bytes bytes,
  * zero-filled before its first use (eptq_e8d4_work_bytes() bytes cover every
  * launch).  With it, batches (or 16-row slices) of 5..16 rows on layers with
- * few 64-row tiles have
- * each tile's columns split over up to 4 workgroups, whose fp32 partial sums
- * meet in the buffer; the kernel leaves its counters at zero.  Calls that
- * share a buffer must not run at the same time.
+ * few 64-row tiles have each tile's columns split over up to 4 workgroups,
+ * whose fp32 partial sums meet in the buffer (the kernel leaves its counters
+ * at zero), and prefill launches above 128 rows whose tiles leave half the
+ * CUs idle or more split K over up to 4 parts whose fp32 sums a second launch
+ * adds in part order (a 64 MiB area past the decode part; a smaller buffer
+ * only takes the decode split).  Calls that share a buffer must not run at
+ * the same time.
  */
 int eptq_e8d4_forward_multi(int n_layers, const eptq_layer* layers, const void* codes,
                             int codes_dtype, const void* x, int x_dtype, int N, int B, void* y,
                             int ldy, void* work, long long work_bytes, void* stream);
 
-/* Bytes of the eptq_e8d4_forward_multi workspace for the current device. */
+/* Bytes of the eptq_e8d4_forward_multi workspace for the current device
+ * (the decode split-K area, then the 64 MiB prefill split-K area). */
 long long eptq_e8d4_work_bytes(void);
 
 /*
