@@ -7,6 +7,7 @@ dozen dispatches each, no graph capture.
 
     python -m eptq_amd.profile_cases decode --shape 4096x4096 --batch 1 --copies 8
     python -m eptq_amd.profile_cases prefill --shape 5120x5120 --tokens 2048
+    python -m eptq_amd.profile_cases prefill --shape 4096x11008 --tokens 512 --work
     python -m eptq_amd.profile_cases e8 --shape 3072x768 --copies 8
     python -m eptq_amd.profile_cases step --layers 4
     python -m eptq_amd.profile_cases module --tokens 2048
@@ -39,6 +40,8 @@ def main(argv=None) -> None:
     ap.add_argument("--layers", type=int, default=4, help="decoder layers (case step)")
     ap.add_argument("--qb", type=int, default=0)
     ap.add_argument("--bf16", action="store_true", help="bf16 activations (cases decode, prefill)")
+    ap.add_argument("--work", action="store_true",
+                    help="through the multi-layer entry point with a decode workspace (split K; cases decode, prefill)")
     args = ap.parse_args(argv)
 
     import torch
@@ -57,11 +60,15 @@ def main(argv=None) -> None:
         x = make_x(T, inp, seed=1, device=dev)
         if args.bf16:
             x = x.bfloat16()
+        work = decode_workspace(dev) if args.work else None
         torch.cuda.synchronize()
         for _ in range(args.reps):
             for L in layers:
-                linear_forward("e8_d4", L["Q"], codes, L["g"], L["h"], x, L["O_vals"], L["O_col"],
-                               L["O_row_ptr"], None, L["S_group"])
+                if work is not None:
+                    linear_forward_multi([L], codes, x, work=work)
+                else:
+                    linear_forward("e8_d4", L["Q"], codes, L["g"], L["h"], x, L["O_vals"], L["O_col"],
+                                   L["O_row_ptr"], None, L["S_group"])
     elif args.case == "e8":
         codes = E8LatticeQuantizer(radius=1.6).flat_table().half().to(dev)
         layers = [_layer(torch, out, inp, 7100 + c, 0.002, dev, bias=True) for c in range(args.copies)]
