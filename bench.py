@@ -31,7 +31,7 @@ JSON fields beyond the driver contract:
   down) of Llama-2-7B at batch 1 and 8 (benchmark configuration 1) and of
   Llama-3-8B with S_group qb=128 at batch 1, 4 and 16 (configuration 2), one
   launch each with the decode workspace: microseconds and algorithmic GB/s.
-  Batches of 5..16 run the matrix-core decode kernel.
+  Batches of 3..16 run the matrix-core decode kernel.
 * ``prefill`` — the Llama-2-13B shapes at 2048 tokens (benchmark
   configuration 3): ``fused`` (the dequantize-into-LDS MFMA GEMM, which the
   C ABI and the module forward run) and, as a yardstick only,
@@ -147,7 +147,7 @@ def make_units(torch, codes, layers, xs, B):
     from eptq_amd.kernels import _lib
     lib = _lib.load()
     units, i = [], 0
-    # Split-K workspace of the matrix-core decode (batches of 5..16); the
+    # Split-K workspace of the matrix-core decode (batches of 3..16); the
     # launches of a step run one after another on one stream.
     from eptq_amd.kernels import decode_workspace
     work = decode_workspace(codes.device)
@@ -437,8 +437,8 @@ def decode_batches(torch, dev, stream_bytes=576 << 20):
     is built as enough distinct copies (different seeds) to exceed
     ``stream_bytes`` of indices (over 512 MB, twice the 256 MB MALL), and the copies are
     launched back to back with HIP events around the whole group, as a decode
-    step streams distinct layers.  B = 1..4 run the vector decode kernel,
-    5..16 the matrix-core one."""
+    step streams distinct layers.  B = 1..2 run the vector decode kernel,
+    3..16 the matrix-core one."""
     from eptq_amd.kernels import _lib, decode_workspace
     from eptq_amd.quantizers import E8D4Quantizer
     from eptq_amd.synthetic import make_layer, make_x
@@ -505,7 +505,7 @@ def decode_batches(torch, dev, stream_bytes=576 << 20):
                 res[f"{uname} B={B}" + (" bf16" if bf else "")] = {
                     "shape": " + ".join(f"{o}x{i}" for o, i in shapes), "us": round(us, 2),
                     "gbs": round(nbytes / (us * 1e-6) / 1e9, 1),
-                    "kernel": "k_decode_mfma" if B >= 5 else DECODE_KERNEL}
+                    "kernel": "k_decode_mfma" if B >= 3 else DECODE_KERNEL}
                 del x, y
             del copies
             torch.cuda.empty_cache()

@@ -89,10 +89,12 @@ __host__ __device__ inline size_t dyn_bytes(int N, bool has_s, int S) {
   return act > red ? act : red;
 }
 
-template <int S, bool HAS_S, typename XT>
+template <int S, bool HAS_S, typename XT, bool XH>
 // At most 168 VGPRs (3 waves per SIMD): one 9-wave workgroup per CU.
 // XT: activation and output type (bf16 x is taken to fp16 exactly in fp16's
 // normal range before the scale; y is rounded from the fp32 sums to XT).
+// XH (B <= 8): each lane loads half of its batch row pair's activations (see
+// the column waves' loads below).
 // Work split: tiles [0, T1) take one workgroup each; the tiles from T1 on
 // have their columns split over P workgroups (T1 = 0: every tile).  ma.start
 // counts tiles.
@@ -144,12 +146,17 @@ __global__ __launch_bounds__((S + 1) * 64, 3) void k_decode_mfma(MultiArgs ma, i
   // round trip then runs under the prologue instead of after it.
   f16x4 tload = {};
   if (tid < 512) tload = ((const f16x4*)a.codes)[tid];
+  // (Only waves with a chunk below nchp issue a load: every load instruction
+  // costs address-unit time, in range or not.)
   u32x4 hw[4], sw[4];
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
     const int c = tid + NT * k;
-    hw[k] = ld16(rh, c * 16);                  // zero past N
-    if (HAS_S) sw[k] = ld16(rs, c * 16);
+    hw[k] = sw[k] = u32x4{0u, 0u, 0u, 0u};
+    if (NT * k + 64 * wave < nchp) {             // wave-uniform
+      hw[k] = ld16(rh, c * 16);                  // zero past N
+      if (HAS_S) sw[k] = ld16(rs, c * 16);
+    }
   }
   // g and bias of this thread's two outputs (thread t < 512: rows 2(t%32), +1
   // of the tile), read long before the output stage needs them.
@@ -169,18 +176,26 @@ __global__ __launch_bounds__((S + 1) * 64, 3) void k_decode_mfma(MultiArgs ma, i
   const int i = lane & 15, kg = lane >> 4;
   const int qrow = m0 + (i >> 1);
   const __amdgpu_buffer_rsrc_t rq = rsrc(a.Q, M * N * 2);
-  int qo = qrow < M ? (qrow * N + blo * kBlk + 16 * kg) * 2 : 0x40000000;
-  int xo = ((lane & 15) * ldx + blo * kBlk + 16 * kg) * 2;
-  u32x4 qv[kDepth][2], xv[kDepth][2];
+  // Address-unit economy (every 16-byte load instruction costs the CU's
+  // address unit the same time, whatever it reads): the two lanes of a block
+  // row (i, i ^ 1) each load half of the row's 16 indices and take the other
+  // half from their partner (DPP); with XH, lane (b, kg) loads half of batch
+  // row b & 7's 16 activations (columns 8·(b >> 3) ..) and lane b < 8 takes
+  // the other half from lane b ^ 8 (lanes b >= 8 then hold values of no
+  // batch row: their MFMA columns are never read).
+  int qo = qrow < M ? (qrow * N + blo * kBlk + 16 * kg + 8 * (i & 1)) * 2 : 0x40000000;
+  int xo = XH ? ((lane & 7) * ldx + blo * kBlk + 16 * kg + 8 * ((lane >> 3) & 1)) * 2
+              : ((lane & 15) * ldx + blo * kBlk + 16 * kg) * 2;
+  constexpr int XL = XH ? 1 : 2;   // activation loads per block
+  u32x4 qv[kDepth], xv[kDepth][XL];
   int rpv = 0;
   if (wave < S) {
 #pragma unroll
     for (int d = 0; d < kDepth; ++d) {
       if (blo + d < bhi) {
-        qv[d][0] = ld16<kNonTemporal>(rq, qo + d * kBlk * 2);
-        qv[d][1] = ld16<kNonTemporal>(rq, qo + d * kBlk * 2 + 16);
-        xv[d][0] = ld16(rx, xo + d * kBlk * 2);
-        xv[d][1] = ld16(rx, xo + d * kBlk * 2 + 16);
+        qv[d] = ld16<kNonTemporal>(rq, qo + d * kBlk * 2);
+#pragma unroll
+        for (int u = 0; u < XL; ++u) xv[d][u] = ld16(rx, xo + d * kBlk * 2 + 16 * u);
       }
     }
   } else {
@@ -266,7 +281,23 @@ __global__ __launch_bounds__((S + 1) * 64, 3) void k_decode_mfma(MultiArgs ma, i
 #pragma unroll
     for (int c = 0; c < 4; ++c) acc[c] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
 
-    auto block = [&](const u32x4 (&q)[2], const u32x4 (&x)[2], int blk) {
+    auto block = [&](const u32x4 qh, const u32x4 (&xh)[XL], int blk) {
+      // The 16 indices of the lane's block row (columns 16·kg ..): q[0] from
+      // the even lane of the pair, q[1] from the odd one (DPP quad_perm
+      // [0,0,2,2] and [1,1,3,3]); the activations likewise (row_ror:8).
+      u32x4 q[2], x[2];
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        q[0][d] = (uint32_t)__builtin_amdgcn_mov_dpp((int)qh[d], 0xA0, 0xF, 0xF, false);
+        q[1][d] = (uint32_t)__builtin_amdgcn_mov_dpp((int)qh[d], 0xF5, 0xF, 0xF, false);
+      }
+      x[0] = xh[0];
+      if constexpr (XH) {
+#pragma unroll
+        for (int d = 0; d < 4; ++d) x[1][d] = (uint32_t)__builtin_amdgcn_mov_dpp((int)xh[0][d], 0x128, 0xF, 0xF, false);
+      } else {
+        x[1] = xh[XL - 1];
+      }
 #pragma unroll
       for (int g2 = 0; g2 < 2; ++g2) {
         const u32x4 sc = *(const u32x4*)(hsa + blk * kBlk + 16 * kg + 8 * g2);
@@ -290,10 +321,9 @@ __global__ __launch_bounds__((S + 1) * 64, 3) void k_decode_mfma(MultiArgs ma, i
         block(qv[d], xv[d], blk);
         if (blk + kDepth < bhi) {
           const int off = (blk - blo + kDepth) * kBlk * 2;
-          qv[d][0] = ld16<kNonTemporal>(rq, qo + off);
-          qv[d][1] = ld16<kNonTemporal>(rq, qo + off + 16);
-          xv[d][0] = ld16(rx, xo + off);
-          xv[d][1] = ld16(rx, xo + off + 16);
+          qv[d] = ld16<kNonTemporal>(rq, qo + off);
+#pragma unroll
+          for (int u = 0; u < XL; ++u) xv[d][u] = ld16(rx, xo + off + 16 * u);
         }
       }
     }
@@ -464,7 +494,7 @@ inline int parts_for(int split, int tiles, void* work, long long work_bytes) {
   return P;
 }
 
-template <int S, bool HAS_S, typename XT>
+template <int S, bool HAS_S, typename XT, bool XH>
 int launch_t(const LinearArgs* l, int n, hipStream_t s, void* work, long long work_bytes) {
   int tiles = 0;
   for (int k = 0; k < n; ++k) tiles += (l[k].M + kTile - 1) / kTile;
@@ -483,7 +513,7 @@ int launch_t(const LinearArgs* l, int n, hipStream_t s, void* work, long long wo
     ma.start[k + 1] = ma.start[k] + (k < n ? (l[k].M + kTile - 1) / kTile : 0);   // tiles
   }
   const int grid = T1 + (tiles - T1) * P;
-  auto kern = k_decode_mfma<S, HAS_S, XT>;
+  auto kern = k_decode_mfma<S, HAS_S, XT, XH>;
   const size_t dyn = dyn_bytes(l[0].N, HAS_S, S);
   static size_t attr = 0;
   if (dyn > attr) {
@@ -523,11 +553,18 @@ int launch_decode_mfma_multi(const LinearArgs* l, int n, hipStream_t s, void* wo
   // (Two 6-wave workgroups per CU for layers with more tiles than CUs, so
   // that they run in one round, measured slower than two rounds of 9-wave
   // workgroups: gate|up 11008x4096 at B=8 24.6 us against 22.2 us.)
-  if (a.x_bf16)
-    return a.S ? dmf::launch_t<dmf::kS, true, bf16>(l, n, s, work, work_bytes)
-               : dmf::launch_t<dmf::kS, false, bf16>(l, n, s, work, work_bytes);
-  return a.S ? dmf::launch_t<dmf::kS, true, f16>(l, n, s, work, work_bytes)
-             : dmf::launch_t<dmf::kS, false, f16>(l, n, s, work, work_bytes);
+  using namespace dmf;
+  const bool xh = a.B <= 8;
+  if (a.x_bf16) {
+    if (a.S) return xh ? launch_t<kS, true, bf16, true>(l, n, s, work, work_bytes)
+                       : launch_t<kS, true, bf16, false>(l, n, s, work, work_bytes);
+    return xh ? launch_t<kS, false, bf16, true>(l, n, s, work, work_bytes)
+              : launch_t<kS, false, bf16, false>(l, n, s, work, work_bytes);
+  }
+  if (a.S) return xh ? launch_t<kS, true, f16, true>(l, n, s, work, work_bytes)
+                     : launch_t<kS, true, f16, false>(l, n, s, work, work_bytes);
+  return xh ? launch_t<kS, false, f16, true>(l, n, s, work, work_bytes)
+            : launch_t<kS, false, f16, false>(l, n, s, work, work_bytes);
 }
 
 long long decode_mfma_work_bytes() {

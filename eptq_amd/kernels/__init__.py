@@ -173,7 +173,7 @@ def linear_forward_multi(layers, codes, x, work: Optional[torch.Tensor] = None) 
     side by side, in one decode launch when the kernel takes them all.
     ``layers``: dicts with Q, g, h, O_vals, O_col, O_row_ptr and optional
     bias, S_group (the EPTQLinear buffers).  ``work``: optional workspace from
-    ``decode_workspace`` (lets batches of 5..16 split the columns of layers
+    ``decode_workspace`` (lets batches of 3..16 split the columns of layers
     with few row tiles over several workgroups); calls sharing one must not
     overlap in time."""
     _require(len(layers) > 0, "no layers")

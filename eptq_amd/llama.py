@@ -249,7 +249,7 @@ class QuantLlama(nn.Module):
         if self.split_attention:
             nbytes = _lib.load().eptq_llama_attn_work_bytes(batch, cfg.heads)
             self.attn_work = torch.zeros(nbytes, dtype=torch.uint8, device=device)
-        # Split-K workspace of the decode Linears (batches of 5..16, and the
+        # Split-K workspace of the decode Linears (batches of 3..16, and the
         # 16-token slices of short prefills through the modules): the model's
         # launches run one after another on one stream.
         self.lin_work = decode_workspace(device)

@@ -94,7 +94,7 @@ typedef struct {
  *
  * work: NULL, or a 16-byte aligned device buffer of work_bytes bytes,
  * zero-filled before its first use (eptq_e8d4_work_bytes() bytes cover every
- * launch).  With it, batches (or 16-row slices) of 5..16 rows on layers with
+ * launch).  With it, batches (or 16-row slices) of 3..16 rows on layers with
  * few 64-row tiles have each tile's columns split over up to 4 workgroups,
  * whose fp32 partial sums meet in the buffer (the kernel leaves its counters
  * at zero), and prefill launches above 128 rows whose tiles leave half the
