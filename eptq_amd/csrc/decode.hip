@@ -11,7 +11,7 @@ namespace eptq {
 
 using namespace dec;
 
-template <int BT, int J, int P, int S, bool HAS_S, typename XT>
+template <int BT, int J, int P, int S, bool HAS_S, typename XT, bool ONE>
 __global__ __launch_bounds__(kT) void k_decode_e8d4(MultiArgs ma) {
   __shared__ f16x4 tab[512];
   __shared__ float red[2][kW][BT * 8];
@@ -29,7 +29,7 @@ __global__ __launch_bounds__(kT) void k_decode_e8d4(MultiArgs ma) {
   const int wg = (int)blockIdx.x - ma.start[li];
   const int G = ma.start[li + 1] - ma.start[li];
 
-  using L = Layer<BT, J, P, S, HAS_S, XT>;
+  using L = Layer<BT, J, P, S, HAS_S, XT, false, ONE>;
   const L layer(a, wg, G);
   const Smem<BT> sm{tab, red, wmax, (uint16_t*)dyn, (float*)(dyn + BT * (a.N + 8) * 2)};
   typename L::State st;
@@ -121,33 +121,10 @@ int cu_count() {
 
 namespace {
 
-template <int BT, int J, int S, bool HAS_S, typename XT>
-int launch_k(const LinearArgs* layers, int n, hipStream_t s) {
-  // About 8 index chunks (128 bytes) per lane in flight: P row groups of
-  // min(J, 4) chunks.
+template <int BT, int J, int S, bool HAS_S, typename XT, bool ONE>
+int launch_one(const LinearArgs* layers, int n, hipStream_t s, int per_cu, size_t dyn) {
   constexpr int P = 8 / (J > 4 ? 4 : J);
   constexpr int R = kW / S;
-  // The fused RMSNorm keeps a whole row in the first CAP chunks per thread.
-  if (layers[0].prep == 1 && Layer<BT, J, P, S, HAS_S, XT>::CAP * kT * 8 < layers[0].N) return -1;
-  auto kern = k_decode_e8d4<BT, J, P, S, HAS_S, XT>;
-  // As many workgroups per CU as registers and LDS allow (one wave of each
-  // workgroup per SIMD): occupancy hides the LDS lookup latency.
-  static int reg_cu = 0;
-  static size_t static_lds = 0;
-  if (reg_cu == 0) {
-    hipFuncAttributes fa;
-    int v = 128;
-    if (hipFuncGetAttributes(&fa, (const void*)kern) == hipSuccess) {
-      if (fa.numRegs > 0) v = fa.numRegs;
-      static_lds = fa.sharedSizeBytes;
-    }
-    const int waves = 512 / ((v + 7) / 8 * 8);
-    reg_cu = waves < 1 ? 1 : (waves > 8 ? 8 : waves);
-  }
-  const size_t dyn = act_lds_bytes(layers[0].N, BT);
-  int per_cu = (int)(kLdsPerCu / (static_lds + dyn + 256));
-  if (per_cu > reg_cu) per_cu = reg_cu;
-  if (per_cu < 1) per_cu = 1;
   MultiArgs ma;
   ma.n = n;
   ma.start[0] = 0;
@@ -162,8 +139,51 @@ int launch_k(const LinearArgs* layers, int n, hipStream_t s) {
       ma.start[l + 1] = ma.start[l];
     }
   }
-  kern<<<ma.start[n], kT, dyn, s>>>(ma);
+  k_decode_e8d4<BT, J, P, S, HAS_S, XT, ONE><<<ma.start[n], kT, dyn, s>>>(ma);
   return 0;
+}
+
+template <int BT, int J, int S, bool HAS_S, typename XT>
+int launch_k(const LinearArgs* layers, int n, hipStream_t s) {
+  // About 8 index chunks (128 bytes) per lane in flight: P row groups of
+  // min(J, 4) chunks.
+  constexpr int P = 8 / (J > 4 ? 4 : J);
+  constexpr int R = kW / S;
+  // The fused RMSNorm keeps a whole row in the first CAP chunks per thread.
+  if (layers[0].prep == 1 && Layer<BT, J, P, S, HAS_S, XT>::CAP * kT * 8 < layers[0].N) return -1;
+  // As many workgroups per CU as registers and LDS allow (one wave of each
+  // workgroup per SIMD): occupancy hides the LDS lookup latency.
+  const size_t dyn = act_lds_bytes(layers[0].N, BT);
+  auto per_cu_of = [&](const void* kern, int& reg_cu, size_t& static_lds) {
+    if (reg_cu == 0) {
+      hipFuncAttributes fa;
+      int v = 128;
+      if (hipFuncGetAttributes(&fa, kern) == hipSuccess) {
+        if (fa.numRegs > 0) v = fa.numRegs;
+        static_lds = fa.sharedSizeBytes;
+      }
+      const int waves = 512 / ((v + 7) / 8 * 8);
+      reg_cu = waves < 1 ? 1 : (waves > 8 ? 8 : waves);
+    }
+    int per_cu = (int)(kLdsPerCu / (static_lds + dyn + 256));
+    if (per_cu > reg_cu) per_cu = reg_cu;
+    return per_cu < 1 ? 1 : per_cu;
+  };
+  // One row group per workgroup in every layer (the Llama decode shapes at
+  // B <= 2): the form without look-ahead loads, sized by its own registers.
+  if constexpr (BT <= 2) {
+    static int reg_one = 0;
+    static size_t lds_one = 0;
+    const int per_cu = per_cu_of((const void*)k_decode_e8d4<BT, J, P, S, HAS_S, XT, true>, reg_one, lds_one);
+    bool one = true;
+    for (int l = 0; l < n; ++l)
+      if ((layers[l].M + R - 1) / R > cu_count() * per_cu) one = false;
+    if (one) return launch_one<BT, J, S, HAS_S, XT, true>(layers, n, s, per_cu, dyn);
+  }
+  static int reg_gen = 0;
+  static size_t lds_gen = 0;
+  const int per_cu = per_cu_of((const void*)k_decode_e8d4<BT, J, P, S, HAS_S, XT, false>, reg_gen, lds_gen);
+  return launch_one<BT, J, S, HAS_S, XT, false>(layers, n, s, per_cu, dyn);
 }
 
 template <int BT, int J, bool HAS_S>

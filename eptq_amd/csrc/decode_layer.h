@@ -218,18 +218,21 @@ struct Walk {
   }
 
   // Entry ranges of the first two row groups (issued early: the entry loads
-  // need them).
+  // need them); ONE: the workgroup has one row group.
+  template <bool ONE>
   __device__ __forceinline__ void rows_first(RowState& st) const {
     row_range(wg, st.crb, st.cre);
-    row_range(wg + G, st.nrb, st.nre);
+    if (ONE) st.nrb = st.nre = 0;
+    else row_range(wg + G, st.nrb, st.nre);
   }
 
   // Index chunks in flight: K of each of the kRing/K row groups of the ring,
   // then the first row group's critical-block entries and epilogue operands.
-  template <int VV>
+  // ONE: the workgroup has one row group; only its first K chunks.
+  template <int VV, bool ONE>
   __device__ __forceinline__ void issue_ring(RowState& st) const {
 #pragma unroll
-    for (int k = 0; k < kRing; ++k) {
+    for (int k = 0; k < (ONE ? K : kRing); ++k) {
       const int p = K == 4 ? k >> 2 : K == 2 ? k >> 1 : k;
       const int j = k - p * K;
       load_chunk(st.ring[k], wg + p * G, j);
@@ -243,7 +246,12 @@ struct Walk {
 // layer w % 2 (gate, up) at row slot w / 2; the output is the SwiGLU product
 // silu(gate) ⊙ up, each factor rounded to the activation type first, as the
 // unfused Linear outputs are.
-template <int BT, int J, int P, int S, bool HAS_S, typename XT, bool PAIR = false>
+// ONE: every workgroup has exactly one row group (G = RG), so nothing is
+// prefetched for a next one.  Every load instruction costs the CU's address
+// unit the same time whether it reads memory or falls past its buffer, so
+// the general form's look-ahead loads (ring slots, entry ranges, entries and
+// epilogue operands of row groups that do not exist) are not free.
+template <int BT, int J, int P, int S, bool HAS_S, typename XT, bool PAIR = false, bool ONE = false>
 struct Layer {
   static constexpr int V = BT * 8;
   static constexpr int R = PAIR ? kW / S / 2 : kW / S;   // rows per row group (per layer)
@@ -271,8 +279,8 @@ struct Layer {
         w(a_, wg_, G_, S, J, V, PAIR) {}
 
   __device__ __forceinline__ int chunk(int j) const { return w.chunk(j); }
-  __device__ __forceinline__ void rows_first(State& st) const { w.rows_first(st); }
-  __device__ __forceinline__ void issue_ring(State& st) const { w.issue_ring<V>(st); }
+  __device__ __forceinline__ void rows_first(State& st) const { w.template rows_first<ONE>(st); }
+  __device__ __forceinline__ void issue_ring(State& st) const { w.template issue_ring<V, ONE>(st); }
 
   // The activation table x·h (scaled) into LDS; returns the output scale.
   // The loads are issued first (h and x rows through buffer resources whose
@@ -529,7 +537,7 @@ struct Layer {
     int par = 0;
     for (int rg0 = wg; rg0 < RG; rg0 += P * G) {
 #pragma unroll
-    for (int p = 0; p < P; ++p) {
+    for (int p = 0; p < (ONE ? 1 : P); ++p) {
       const int rg = rg0 + p * G;
       if (rg >= RG) break;                       // uniform across the workgroup
       const int m = rg * R + slot;
@@ -540,10 +548,10 @@ struct Layer {
       // next one's.
       const int orow = w.out_row(rg);
       const f16 og = st.og, ob = st.ob;
-      w.load_epilogue<V>(rg + G, st.og, st.ob);
+      if (!ONE) w.load_epilogue<V>(rg + G, st.og, st.ob);
       // Row pointers two row groups ahead (their entries are loaded next).
-      int frb, fre;
-      w.row_range(rg + 2 * G, frb, fre);
+      int frb = 0, fre = 0;
+      if (!ONE) w.row_range(rg + 2 * G, frb, fre);
       // S at the critical blocks' columns (grouped layers), issued part-way
       // through the chunk loop once the entry columns have arrived.
       f16 gs = (f16)1.0f;
@@ -589,7 +597,7 @@ struct Layer {
         // Refill this chunk's ring slot: the chunk K ahead in the same row,
         // else the matching chunk of the row group P·G ahead.
         if (j + K < J) w.load_chunk(st.ring[p * K + j % K], rg, j + K);
-        else w.load_chunk(st.ring[p * K + j % K], rg + P * G, j + K - J);
+        else if (!ONE) w.load_chunk(st.ring[p * K + j % K], rg + P * G, j + K - J);
         if (!live) continue;
         if constexpr (BT == 1) {
           const float sc = csc[cj];
@@ -669,9 +677,11 @@ struct Layer {
       }
 
       // Next row group's entries.
-      w.load_entries(st, st.nrb, st.nre);
-      st.crb = st.nrb; st.cre = st.nre;
-      st.nrb = frb; st.nre = fre;
+      if (!ONE) {
+        w.load_entries(st, st.nrb, st.nre);
+        st.crb = st.nrb; st.cre = st.nre;
+        st.nrb = frb; st.nre = fre;
+      }
 
       const int base = wave_reduce_halving<V>(acc);
       if constexpr (PAIR) {
