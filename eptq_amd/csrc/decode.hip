@@ -13,7 +13,7 @@ using namespace dec;
 
 template <int BT, int J, int P, int S, bool HAS_S, typename XT, bool ONE>
 __global__ __launch_bounds__(kT) void k_decode_e8d4(MultiArgs ma) {
-  __shared__ f16x4 tab[512];
+  __shared__ __attribute__((aligned(16))) f16x4 tab[512];
   __shared__ float red[2][kW][BT * 8];
   __shared__ float wmax[kW];
   // Activation side, shared by the workgroup: xs[b][n] = fp16 x·h (scaled),
@@ -38,14 +38,12 @@ __global__ __launch_bounds__(kT) void k_decode_e8d4(MultiArgs ma) {
   // Table and activations before the index stream, so their loads are not
   // queued behind the HBM index traffic (vmcnt counts loads in issue order).
   const int tid = threadIdx.x;
-  f16x4 tload[2];
-#pragma unroll
-  for (int p = 0; p < 2; ++p) tload[p] = ((const f16x4*)a.codes)[tid + kT * p];   // fp16 table
+  static_assert(2 * kT == 512, "one 16-byte table load per thread");
+  const u32x4 tload = *gp((const u32x4*)a.codes + tid);   // fp16 table rows 2·tid, 2·tid + 1
   const float out_scale = layer.build_act(sm);
   layer.issue_ring(st);
   __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-  for (int p = 0; p < 2; ++p) tab[(tid + kT * p) ^ 0x100] = tload[p];
+  *(u32x4*)&tab[(2 * tid) ^ 0x100] = tload;   // rows 2·tid, 2·tid + 1 stay adjacent
   __syncthreads();
   layer.rows(st, sm, out_scale);
 }
@@ -60,7 +58,7 @@ __host__ __device__ inline size_t pair_table_bytes(int N, int BT) { return (act_
 // built from one read of x (and one RMSNorm, prep 1).
 template <int BT, int J, int P, bool HAS_S>
 __global__ __launch_bounds__(kT) void k_decode_e8d4_pair(MultiArgs ma) {
-  __shared__ f16x4 tab[512];
+  __shared__ __attribute__((aligned(16))) f16x4 tab[512];
   __shared__ float red[2][kW][BT * 8];
   __shared__ float wmax[2][kW];
   __shared__ uint16_t pairx[2][2][64];
@@ -76,16 +74,14 @@ __global__ __launch_bounds__(kT) void k_decode_e8d4_pair(MultiArgs ma) {
   typename L::State st;
   layer.rows_first(st);
   const int tid = threadIdx.x;
-  f16x4 tload[2];
-#pragma unroll
-  for (int p = 0; p < 2; ++p) tload[p] = ((const f16x4*)a.codes)[tid + kT * p];   // fp16 table
+  static_assert(2 * kT == 512, "one 16-byte table load per thread");
+  const u32x4 tload = *gp((const u32x4*)a.codes + tid);   // fp16 table rows 2·tid, 2·tid + 1
   float scale1;
   const float scale0 =
       L(ma.l[0], (int)blockIdx.x, (int)gridDim.x).template build_act<true>(sm0, ma.l[1].h, &sm1, &scale1);
   layer.issue_ring(st);
   __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-  for (int p = 0; p < 2; ++p) tab[(tid + kT * p) ^ 0x100] = tload[p];
+  *(u32x4*)&tab[(2 * tid) ^ 0x100] = tload;   // rows 2·tid, 2·tid + 1 stay adjacent
   __syncthreads();
   layer.rows(st, up ? sm1 : sm0, up ? scale1 : scale0, pairx);
 }

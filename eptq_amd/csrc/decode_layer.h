@@ -161,11 +161,14 @@ struct Walk {
   __device__ __forceinline__ void row_range(int rg, int& rb, int& re) const {
     const int M = a.M;
     const int row = rg * R + slot;             // wave-uniform
-    const int rr = row < M ? row : M;
+    const int rr = row < M ? row : M - 1;
     const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(
         (void*)a.O_row_ptr, (short)0, (M + 1) * 4, kBufferWord3);
-    rb = (int)__builtin_amdgcn_raw_buffer_load_b32(rp, rr * 4, 0, 0);
-    re = (int)__builtin_amdgcn_raw_buffer_load_b32(rp, (row < M ? rr + 1 : rr) * 4, 0, 0);
+    // Both pointers in one load instruction; rows past M: the empty range at
+    // the end.
+    const auto v = __builtin_amdgcn_raw_buffer_load_b64(rp, rr * 4, 0, 0);
+    rb = (int)(row < M ? v[0] : v[1]);
+    re = (int)v[1];
   }
 
   // Index chunks are read through a buffer resource spanning one row (an
@@ -228,7 +231,10 @@ struct Walk {
 
   // Index chunks in flight: K of each of the kRing/K row groups of the ring,
   // then the first row group's critical-block entries and epilogue operands.
-  // ONE: the workgroup has one row group; only its first K chunks.
+  // ONE: the workgroup has one row group; only its first K chunks.  (The
+  // entry and bias loads stay unconditional: a load skipped on one path
+  // merges with a constant on the other, and the compiler waits for every
+  // load in flight at that merge.)
   template <int VV, bool ONE>
   __device__ __forceinline__ void issue_ring(RowState& st) const {
 #pragma unroll
