@@ -144,15 +144,17 @@ __global__ __launch_bounds__((S + 1) * 64, 3) void k_decode_mfma(MultiArgs ma, i
   // prologue's waits for h cover the ring too (a wave with fewer blocks
   // issues fewer loads, so the compiler cannot count them), but the ring's
   // round trip then runs under the prologue instead of after it.
-  f16x4 tload = {};
-  if (tid < 512) tload = ((const f16x4*)a.codes)[tid];
-  // (Only waves with a chunk below nchp issue a load: every load instruction
-  // costs address-unit time, in range or not.)
+  // Loads skipped on some path are left undefined there (never merged with
+  // a constant: the compiler would wait for every load in flight at such a
+  // merge, before the ring is issued) and used only under the same
+  // condition.  Only waves with a chunk below nchp load h: every load
+  // instruction costs address-unit time, in range or not.
+  f16x4 tload;
+  if (tid < 512) tload = *gp((const f16x4*)a.codes + tid);
   u32x4 hw[4], sw[4];
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
     const int c = tid + NT * k;
-    hw[k] = sw[k] = u32x4{0u, 0u, 0u, 0u};
     if (NT * k + 64 * wave < nchp) {             // wave-uniform
       hw[k] = ld16(rh, c * 16);                  // zero past N
       if (HAS_S) sw[k] = ld16(rs, c * 16);
@@ -188,7 +190,12 @@ __global__ __launch_bounds__((S + 1) * 64, 3) void k_decode_mfma(MultiArgs ma, i
               : ((lane & 15) * ldx + blo * kBlk + 16 * kg) * 2;
   constexpr int XL = XH ? 1 : 2;   // activation loads per block
   u32x4 qv[kDepth], xv[kDepth][XL];
-  int rpv = 0;
+  // The tile's CSR row pointers (part 0 applies the critical blocks; the
+  // other parts see an empty range), for the staging wave; loaded by every
+  // wave so that no wave merges it with a constant before its ring.
+  const __amdgpu_buffer_rsrc_t rp = rsrc(a.O_row_ptr, (M + 1) * 4);
+  const int rrow = m0 + (part == 0 && lane <= kTile ? lane : part == 0 ? kTile : 0);
+  const int rpv = (int)__builtin_amdgcn_raw_buffer_load_b32(rp, (rrow < M ? rrow : M) * 4, 0, 0);
   if (wave < S) {
 #pragma unroll
     for (int d = 0; d < kDepth; ++d) {
@@ -198,12 +205,6 @@ __global__ __launch_bounds__((S + 1) * 64, 3) void k_decode_mfma(MultiArgs ma, i
         for (int u = 0; u < XL; ++u) xv[d][u] = ld16(rx, xo + d * kBlk * 2 + 16 * u);
       }
     }
-  } else {
-    // Staging wave: the tile's CSR row pointers (part 0 applies the
-    // critical blocks; the other parts see an empty range).
-    const __amdgpu_buffer_rsrc_t rp = rsrc(a.O_row_ptr, (M + 1) * 4);
-    const int r = m0 + (part == 0 && lane <= kTile ? lane : part == 0 ? kTile : 0);
-    rpv = (int)__builtin_amdgcn_raw_buffer_load_b32(rp, (r < M ? r : M) * 4, 0, 0);
   }
 
   // h (and the S row) into LDS as loaded; max|h|.
@@ -218,7 +219,8 @@ __global__ __launch_bounds__((S + 1) * 64, 3) void k_decode_mfma(MultiArgs ma, i
     }
   };
 #pragma unroll
-  for (int k = 0; k < 4; ++k) put(tid + NT * k, hw[k], HAS_S ? sw[k] : hw[k]);
+  for (int k = 0; k < 4; ++k)
+    if (NT * k + 64 * wave < nchp) put(tid + NT * k, hw[k], HAS_S ? sw[k] : hw[k]);
   for (int c = tid + 4 * NT; c < nchp; c += NT) put(c, ld16(rh, c * 16), HAS_S ? ld16(rs, c * 16) : u32x4{});
   mx = fmaxf(mx, partner<1>(mx));
   mx = fmaxf(mx, partner<2>(mx));
