@@ -56,7 +56,7 @@ __host__ __device__ inline size_t pair_table_bytes(int N, int BT) { return (act_
 // workgroup serving the same rows of both (wave w: layer w % 2, row slot
 // w / 2); y = silu(gate) ⊙ up at ma.l[0].y.  Both activation tables are
 // built from one read of x (and one RMSNorm, prep 1).
-template <int BT, int J, int P, bool HAS_S>
+template <int BT, int J, int P, bool HAS_S, bool ONE>
 __global__ __launch_bounds__(kT) void k_decode_e8d4_pair(MultiArgs ma) {
   __shared__ __attribute__((aligned(16))) f16x4 tab[512];
   __shared__ float red[2][kW][BT * 8];
@@ -66,7 +66,7 @@ __global__ __launch_bounds__(kT) void k_decode_e8d4_pair(MultiArgs ma) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const bool up = wave & 1;
   const LinearArgs a = up ? ma.l[1] : ma.l[0];
-  using L = Layer<BT, J, P, 1, HAS_S, f16, true>;
+  using L = Layer<BT, J, P, 1, HAS_S, f16, true, ONE>;
   const L layer(a, (int)blockIdx.x, (int)gridDim.x);
   const size_t act = pair_table_bytes(a.N, BT);   // the second table 16-byte aligned
   const Smem<BT> sm0{tab, red, wmax[0], (uint16_t*)dyn, (float*)(dyn + BT * (a.N + 8) * 2)};
@@ -188,33 +188,42 @@ int launch_pair_k(const LinearArgs* l, hipStream_t s) {
   using L = Layer<BT, J, P, 1, HAS_S, f16, true>;
   // The fused RMSNorm keeps a whole row in the first CAP chunks per thread.
   if (l[0].prep == 1 && L::CAP * kT * 8 < l[0].N) return -1;
-  auto kern = k_decode_e8d4_pair<BT, J, P, HAS_S>;
-  static int reg_cu = 0;
-  static size_t static_lds = 0;
-  if (reg_cu == 0) {
-    hipFuncAttributes fa;
-    int v = 128;
-    if (hipFuncGetAttributes(&fa, (const void*)kern) == hipSuccess) {
-      if (fa.numRegs > 0) v = fa.numRegs;
-      static_lds = fa.sharedSizeBytes;
-    }
-    const int waves = 512 / ((v + 7) / 8 * 8);
-    reg_cu = waves < 1 ? 1 : (waves > 8 ? 8 : waves);
-  }
   const size_t dyn = 2 * pair_table_bytes(l[0].N, BT);
-  int per_cu = (int)(kLdsPerCu / (static_lds + dyn + 256));
-  if (per_cu > reg_cu) per_cu = reg_cu;
-  if (per_cu < 1) per_cu = 1;
+  auto per_cu_of = [&](const void* kern, int& reg_cu, size_t& static_lds) {
+    if (reg_cu == 0) {
+      hipFuncAttributes fa;
+      int v = 128;
+      if (hipFuncGetAttributes(&fa, kern) == hipSuccess) {
+        if (fa.numRegs > 0) v = fa.numRegs;
+        static_lds = fa.sharedSizeBytes;
+      }
+      const int waves = 512 / ((v + 7) / 8 * 8);
+      reg_cu = waves < 1 ? 1 : (waves > 8 ? 8 : waves);
+    }
+    int per_cu = (int)(kLdsPerCu / (static_lds + dyn + 256));
+    if (per_cu > reg_cu) per_cu = reg_cu;
+    return per_cu < 1 ? 1 : per_cu;
+  };
   const int RG = (l[0].M + L::R - 1) / L::R;
-  const int G = cu_count() * per_cu < RG ? cu_count() * per_cu : RG;
   MultiArgs ma;
   ma.n = 2;
   ma.l[0] = l[0];
   ma.l[1] = l[1];
   ma.l[2] = ma.l[3] = l[0];
   ma.start[0] = 0;
+  // One row group per workgroup: the form without look-ahead loads.
+  static int reg_one = 0, reg_gen = 0;
+  static size_t lds_one = 0, lds_gen = 0;
+  const int pc1 = per_cu_of((const void*)k_decode_e8d4_pair<BT, J, P, HAS_S, true>, reg_one, lds_one);
+  if (RG <= cu_count() * pc1) {
+    ma.start[1] = ma.start[2] = ma.start[3] = ma.start[4] = RG;
+    k_decode_e8d4_pair<BT, J, P, HAS_S, true><<<RG, kT, dyn, s>>>(ma);
+    return 0;
+  }
+  const int pc = per_cu_of((const void*)k_decode_e8d4_pair<BT, J, P, HAS_S, false>, reg_gen, lds_gen);
+  const int G = cu_count() * pc < RG ? cu_count() * pc : RG;
   ma.start[1] = ma.start[2] = ma.start[3] = ma.start[4] = G;
-  kern<<<G, kT, dyn, s>>>(ma);
+  k_decode_e8d4_pair<BT, J, P, HAS_S, false><<<G, kT, dyn, s>>>(ma);
   return 0;
 }
 
