@@ -121,6 +121,19 @@ template <int BT, int J, int S, bool HAS_S, typename XT, bool ONE>
 int launch_one(const LinearArgs* layers, int n, hipStream_t s, int per_cu, size_t dyn) {
   constexpr int P = 8 / (J > 4 ? 4 : J);
   constexpr int R = kW / S;
+  const int cap = cu_count() * per_cu;
+  // ONE: the launch's row groups fit in one round (sum RG <= cap).  Workgroups
+  // are raised to a whole number of CU rounds (within cap), given to the
+  // layers in proportion to their rows and never more than a layer's rows:
+  // with the strided row map every CU then holds about the same number of
+  // rows (688 row groups of 4 rows on 256 CUs left CUs with 3 and with 2).
+  long rg_sum = 0, m_sum = 0;
+  for (int l = 0; l < n; ++l) {
+    rg_sum += (layers[l].M + R - 1) / R;
+    m_sum += layers[l].M;
+  }
+  long total = (rg_sum + cu_count() - 1) / cu_count() * cu_count();
+  if (total > cap) total = cap;
   MultiArgs ma;
   ma.n = n;
   ma.start[0] = 0;
@@ -128,7 +141,12 @@ int launch_one(const LinearArgs* layers, int n, hipStream_t s, int per_cu, size_
     if (l < n) {
       ma.l[l] = layers[l];
       const int RG = (layers[l].M + R - 1) / R;
-      const int g = cu_count() * per_cu < RG ? cu_count() * per_cu : RG;
+      int g = cap < RG ? cap : RG;
+      if (ONE) {
+        long extra = (total - rg_sum) * layers[l].M / (m_sum > 0 ? m_sum : 1);
+        g = RG + (int)(extra > 0 ? extra : 0);
+        if (g > layers[l].M) g = layers[l].M;
+      }
       ma.start[l + 1] = ma.start[l] + g;
     } else {
       ma.l[l] = layers[0];

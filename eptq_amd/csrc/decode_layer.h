@@ -141,15 +141,23 @@ struct RowState {
 struct Walk {
   const LinearArgs& a;
   int wg, G, S, J, K, R, slot, seg, lane, tid, V;
+  bool strided;
 
   // pair: the workgroup serves two layers of equal shape (SwiGLU gate and
   // up), wave w layer w % 2 at row slot w / 2 (S = 1): R = 2 rows per layer.
-  __device__ __forceinline__ Walk(const LinearArgs& a_, int wg_, int G_, int S_, int J_, int V_, bool pair = false)
+  // strided (the single-row-group form): the workgroup's one row group is
+  // rows wg, wg + G, wg + 2G, ... (one per row slot), so G may exceed the
+  // number of row groups: rows then spread evenly over the workgroups.
+  __device__ __forceinline__ Walk(const LinearArgs& a_, int wg_, int G_, int S_, int J_, int V_, bool pair = false,
+                                  bool strided_ = false)
       : a(a_), wg(wg_), G(G_), S(S_), J(J_), K(J_ > 4 ? 4 : J_), R(pair ? kW / S_ / 2 : kW / S_),
         slot(pair ? (__builtin_amdgcn_readfirstlane(threadIdx.x >> 6) / S_) >> 1
                   : __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) / S_),
         seg(__builtin_amdgcn_readfirstlane(threadIdx.x >> 6) % S_), lane(threadIdx.x & 63),
-        tid(threadIdx.x), V(V_) {}
+        tid(threadIdx.x), V(V_), strided(strided_) {}
+
+  // The row of row slot sl in row group rg.
+  __device__ __forceinline__ int row_of(int rg, int sl) const { return strided ? sl * G + rg : rg * R + sl; }
 
   __device__ __forceinline__ int chunk(int j) const { return seg * 64 + lane + 64 * S * j; }
 
@@ -160,7 +168,7 @@ struct Walk {
   // wait for it.
   __device__ __forceinline__ void row_range(int rg, int& rb, int& re) const {
     const int M = a.M;
-    const int row = rg * R + slot;             // wave-uniform
+    const int row = row_of(rg, slot);          // wave-uniform
     const int rr = row < M ? row : M - 1;
     const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(
         (void*)a.O_row_ptr, (short)0, (M + 1) * 4, kBufferWord3);
@@ -177,7 +185,7 @@ struct Walk {
   // the load it needs (vmcnt counts loads in issue order).
   __device__ __forceinline__ void load_chunk(u32x4& dst, int rg, int j) const {
     const int M = a.M, N = a.N;
-    const int row = rg * R + slot;            // wave-uniform
+    const int row = row_of(rg, slot);         // wave-uniform
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
         (void*)(a.Q + (size_t)(row < M ? row : 0) * N), (short)0, row < M ? N * 2 : 0, kBufferWord3);
     dst = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, chunk(j) * 16, 0, kNonTemporal));
@@ -201,7 +209,7 @@ struct Walk {
   // The output row this thread writes for row group rg, and its (batch row,
   // row-in-block) position.
   __device__ __forceinline__ int out_row(int rg) const {
-    return S == 1 ? rg * R + slot : rg * R + (tid < R * V ? tid / V : 0);
+    return S == 1 ? row_of(rg, slot) : row_of(rg, tid < R * V ? tid / V : 0);
   }
   template <int VV>
   __device__ __forceinline__ int wbase() const {
@@ -282,7 +290,7 @@ struct Layer {
       : a(a_), wg(wg_), G(G_), tid(threadIdx.x), lane(threadIdx.x & 63),
         wave(__builtin_amdgcn_readfirstlane(threadIdx.x >> 6)), slot(PAIR ? (wave / S) >> 1 : wave / S),
         seg(wave % S), N(a_.N), M(a_.M), B(a_.B), nch(a_.N >> 3), NP(a_.N + 8), RG((a_.M + R - 1) / R),
-        w(a_, wg_, G_, S, J, V, PAIR) {}
+        w(a_, wg_, G_, S, J, V, PAIR, ONE) {}
 
   __device__ __forceinline__ int chunk(int j) const { return w.chunk(j); }
   __device__ __forceinline__ void rows_first(State& st) const { w.template rows_first<ONE>(st); }
@@ -541,12 +549,13 @@ struct Layer {
     const int wb = wbase >> 3, wk = wbase & 7;
 
     int par = 0;
-    for (int rg0 = wg; rg0 < RG; rg0 += P * G) {
+    // ONE: exactly one pass, rg = wg (its rows wg + G·slot).
+    for (int rg0 = wg; ONE ? rg0 == wg : rg0 < RG; rg0 += P * G) {
 #pragma unroll
     for (int p = 0; p < (ONE ? 1 : P); ++p) {
       const int rg = rg0 + p * G;
-      if (rg >= RG) break;                       // uniform across the workgroup
-      const int m = rg * R + slot;
+      if (!ONE && rg >= RG) break;               // uniform across the workgroup
+      const int m = w.row_of(rg, slot);
       const bool row_ok = m < M;
       const int grp = HAS_S ? (8 * (row_ok ? m : 0)) / a.qb : 0;
 
