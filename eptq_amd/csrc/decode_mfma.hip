@@ -196,16 +196,6 @@ __global__ __launch_bounds__((S + 1) * 64, 3) void k_decode_mfma(MultiArgs ma, i
   const __amdgpu_buffer_rsrc_t rp = rsrc(a.O_row_ptr, (M + 1) * 4);
   const int rrow = m0 + (part == 0 && lane <= kTile ? lane : part == 0 ? kTile : 0);
   const int rpv = (int)__builtin_amdgcn_raw_buffer_load_b32(rp, (rrow < M ? rrow : M) * 4, 0, 0);
-  if (wave < S) {
-#pragma unroll
-    for (int d = 0; d < kDepth; ++d) {
-      if (blo + d < bhi) {
-        qv[d] = ld16<kNonTemporal>(rq, qo + d * kBlk * 2);
-#pragma unroll
-        for (int u = 0; u < XL; ++u) xv[d][u] = ld16(rx, xo + d * kBlk * 2 + 16 * u);
-      }
-    }
-  }
 
   // h (and the S row) into LDS as loaded; max|h|.
   float mx = 0.0f;
@@ -230,15 +220,34 @@ __global__ __launch_bounds__((S + 1) * 64, 3) void k_decode_mfma(MultiArgs ma, i
   mx = fmaxf(mx, partner<32>(mx));
   if (lane == 0) wmax[wave] = mx;
   if (tid < 512) tab[tid ^ 0x100] = tload;
+  // The ring goes out once h and the table are in (a ring issued earlier
+  // is waited for whole before h can be stored: its loads are conditional,
+  // so the compiler cannot count them); its round trip then runs under the
+  // barriers and the scaling.
+  __builtin_amdgcn_sched_barrier(0);
+  if (wave < S) {
+#pragma unroll
+    for (int d = 0; d < kDepth; ++d) {
+      if (blo + d < bhi) {
+        qv[d] = ld16<kNonTemporal>(rq, qo + d * kBlk * 2);
+#pragma unroll
+        for (int u = 0; u < XL; ++u) xv[d][u] = ld16(rx, xo + d * kBlk * 2 + 16 * u);
+      }
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
 
-  // Staging wave: the entries' columns and O vectors.
-  const int rsv = __builtin_amdgcn_readlane(rpv, 0);
-  const int nent = __builtin_amdgcn_readlane(rpv, kTile) - rsv;
-  const int nst = nent < kEntCap ? nent : kEntCap;
+  // Staging wave: the entries' columns and O vectors (the row pointers are
+  // read by the staging wave alone: a column wave reading them here would
+  // wait for its whole ring).
   constexpr int kPass = kEntCap / 64;
   int scol[kPass];
   u32x4 so[kPass];
+  int nst = 0;
   if (wave == S) {
+    const int rsv = __builtin_amdgcn_readlane(rpv, 0);
+    const int nent = __builtin_amdgcn_readlane(rpv, kTile) - rsv;
+    nst = nent < kEntCap ? nent : kEntCap;
     if (lane <= kTile) erow[lane] = rpv - rsv;
     if (lane == 0) ebase = rsv;
     const __amdgpu_buffer_rsrc_t rc = rsrc(a.O_col + rsv, nst * 4);
