@@ -36,6 +36,8 @@
 // column for each batch row) into LDS while the column waves run, and the
 // output stage adds O·(x h) minus what the marker contributed.
 
+#include <type_traits>
+
 #include "mfma_decode.h"
 
 namespace eptq {
@@ -53,7 +55,8 @@ using mdec::rsrc;
 
 constexpr int kTile = 8;        // block rows per tile (64 output rows)
 constexpr int kBlk = 64;        // columns per block: 4 K groups x 16
-constexpr int kDepth = 6;       // blocks of indices and activations in flight per lane
+constexpr int kDepth = 6;       // blocks of indices and activations in flight per lane (long waves)
+constexpr int kFar = 0x40000000;  // a buffer offset past every operand (a load there reads zeros)
 constexpr int kEntCap = 256;    // critical blocks of a tile prefetched before the column loop
 constexpr int kRedLd = 68;      // floats per batch row of a wave's partial sums
 constexpr int kS = 8;           // column waves per workgroup (one workgroup per CU)
@@ -140,11 +143,8 @@ __global__ __launch_bounds__((S + 1) * 64, 3) void k_decode_mfma(MultiArgs ma, i
   const __amdgpu_buffer_rsrc_t rx = rsrc(a.x, ((B - 1) * ldx + N) * 2);
   const __amdgpu_buffer_rsrc_t rs = rsrc(HAS_S ? a.S + (size_t)grp * N : nullptr, HAS_S ? N * 2 : 0);
 
-  // Table, h and the S row first, then the column waves' whole ring: the
-  // prologue's waits for h cover the ring too (a wave with fewer blocks
-  // issues fewer loads, so the compiler cannot count them), but the ring's
-  // round trip then runs under the prologue instead of after it.
-  // Loads skipped on some path are left undefined there (never merged with
+  // Table, h and the S row first (the column waves' ring follows them into
+  // LDS).  Loads skipped on some path are left undefined there (never merged with
   // a constant: the compiler would wait for every load in flight at such a
   // merge, before the ring is issued) and used only under the same
   // condition.  Only waves with a chunk below nchp load h: every load
@@ -189,10 +189,10 @@ __global__ __launch_bounds__((S + 1) * 64, 3) void k_decode_mfma(MultiArgs ma, i
   int xo = XH ? ((lane & 7) * ldx + blo * kBlk + 16 * kg + 8 * ((lane >> 3) & 1)) * 2
               : ((lane & 15) * ldx + blo * kBlk + 16 * kg) * 2;
   constexpr int XL = XH ? 1 : 2;   // activation loads per block
-  u32x4 qv[kDepth], xv[kDepth][XL];
+  constexpr int kShort = 8;        // most blocks per wave loaded at once
   // The tile's CSR row pointers (part 0 applies the critical blocks; the
-  // other parts see an empty range), for the staging wave; loaded by every
-  // wave so that no wave merges it with a constant before its ring.
+  // other parts see an empty range), for the staging wave (the compiler
+  // moves the load into that wave's path).
   const __amdgpu_buffer_rsrc_t rp = rsrc(a.O_row_ptr, (M + 1) * 4);
   const int rrow = m0 + (part == 0 && lane <= kTile ? lane : part == 0 ? kTile : 0);
   const int rpv = (int)__builtin_amdgcn_raw_buffer_load_b32(rp, (rrow < M ? rrow : M) * 4, 0, 0);
@@ -220,77 +220,45 @@ __global__ __launch_bounds__((S + 1) * 64, 3) void k_decode_mfma(MultiArgs ma, i
   mx = fmaxf(mx, partner<32>(mx));
   if (lane == 0) wmax[wave] = mx;
   if (tid < 512) tab[tid ^ 0x100] = tload;
-  // The ring goes out once h and the table are in (a ring issued earlier
-  // is waited for whole before h can be stored: its loads are conditional,
-  // so the compiler cannot count them); its round trip then runs under the
-  // barriers and the scaling.
-  __builtin_amdgcn_sched_barrier(0);
-  if (wave < S) {
-#pragma unroll
-    for (int d = 0; d < kDepth; ++d) {
-      if (blo + d < bhi) {
-        qv[d] = ld16<kNonTemporal>(rq, qo + d * kBlk * 2);
-#pragma unroll
-        for (int u = 0; u < XL; ++u) xv[d][u] = ld16(rx, xo + d * kBlk * 2 + 16 * u);
-      }
-    }
-  }
-  __builtin_amdgcn_sched_barrier(0);
-
-  // Staging wave: the entries' columns and O vectors (the row pointers are
-  // read by the staging wave alone: a column wave reading them here would
-  // wait for its whole ring).
-  constexpr int kPass = kEntCap / 64;
-  int scol[kPass];
-  u32x4 so[kPass];
-  int nst = 0;
-  if (wave == S) {
-    const int rsv = __builtin_amdgcn_readlane(rpv, 0);
-    const int nent = __builtin_amdgcn_readlane(rpv, kTile) - rsv;
-    nst = nent < kEntCap ? nent : kEntCap;
-    if (lane <= kTile) erow[lane] = rpv - rsv;
-    if (lane == 0) ebase = rsv;
-    const __amdgpu_buffer_rsrc_t rc = rsrc(a.O_col + rsv, nst * 4);
-    const __amdgpu_buffer_rsrc_t ro = rsrc(a.O + (size_t)rsv * 8, nst * 16);
-#pragma unroll
-    for (int p = 0; p < kPass; ++p) {
-      scol[p] = (int)__builtin_amdgcn_raw_buffer_load_b32(rc, (lane + 64 * p) * 4, 0, 0);
-      so[p] = ld16(ro, (lane + 64 * p) * 16);
-    }
-  }
-  __syncthreads();
-  // Workgroup scale 2^-e with max|h|·2^-e <= 1; hs = fp16(h·2^-e), hss = fp16(hs·S).
-  mx = wmax[0];
-#pragma unroll
-  for (int w = 1; w <= S; ++w) mx = fmaxf(mx, wmax[w]);
-  int ex = 0;
-  if (mx > 1.0f) ex = (int)((__builtin_bit_cast(uint32_t, mx) >> 23) & 0xff) - 126;   // 2^ex >= mx
-  const float out_scale = __builtin_ldexpf(1.0f, ex);
-  const f16 down = (f16)__builtin_ldexpf(1.0f, -ex);
-  const uint32_t down2 = __builtin_bit_cast(uint32_t, (h2){down, down});
-  for (int c = tid; c < nchp; c += NT) {
-    u32x4 h = *(const u32x4*)(hs + c * 8);
-#pragma unroll
-    for (int d = 0; d < 4; ++d) h[d] = pk_mul(h[d], down2);
-    *(u32x4*)(hs + c * 8) = h;
-    if (HAS_S) {
-      u32x4 sv = *(const u32x4*)(hss + c * 8);
-#pragma unroll
-      for (int d = 0; d < 4; ++d) sv[d] = pk_mul(h[d], sv[d]);
-      *(u32x4*)(hss + c * 8) = sv;
-    }
-  }
-  __syncthreads();
   const char* __restrict__ tabB = (const char*)tab;
-  const f16x4 t5 = tab[511 ^ 0x100];
   const uint16_t* __restrict__ hsa = HAS_S ? hss : hs;   // the scale row of the main loop
 
-  f32x4 acc[4];
-  if (wave < S) {
-    // ---- column wave --------------------------------------------------------
-    const mdec::Half half(i);
+  // The two barriers around the scaling, run by every wave on its own path
+  // (a load issued before them and used after must not cross a merge of
+  // paths that issued different numbers of loads: the compiler would then
+  // wait for every load in flight).  Workgroup scale 2^-e with
+  // max|h|·2^-e <= 1; hs = fp16(h·2^-e), hss = fp16(hs·S).
+  float out_scale = 1.0f;
+  f16 down = (f16)1.0f;
+  auto scale = [&]() {
+    __syncthreads();
+    float m = wmax[0];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) acc[c] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+    for (int w = 1; w <= S; ++w) m = fmaxf(m, wmax[w]);
+    int ex = 0;
+    if (m > 1.0f) ex = (int)((__builtin_bit_cast(uint32_t, m) >> 23) & 0xff) - 126;   // 2^ex >= m
+    out_scale = __builtin_ldexpf(1.0f, ex);
+    down = (f16)__builtin_ldexpf(1.0f, -ex);
+    const uint32_t down2 = __builtin_bit_cast(uint32_t, (h2){down, down});
+    for (int c = tid; c < nchp; c += NT) {
+      u32x4 h = *(const u32x4*)(hs + c * 8);
+#pragma unroll
+      for (int d = 0; d < 4; ++d) h[d] = pk_mul(h[d], down2);
+      *(u32x4*)(hs + c * 8) = h;
+      if (HAS_S) {
+        u32x4 sv = *(const u32x4*)(hss + c * 8);
+#pragma unroll
+        for (int d = 0; d < 4; ++d) sv[d] = pk_mul(h[d], sv[d]);
+        *(u32x4*)(hss + c * 8) = sv;
+      }
+    }
+    __syncthreads();
+  };
+
+  f32x4 acc[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) acc[c] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+  const mdec::Half half(i);
 
     auto block = [&](const u32x4 qh, const u32x4 (&xh)[XL], int blk) {
       // The 16 indices of the lane's block row (columns 16·kg ..): q[0] from
@@ -324,22 +292,97 @@ __global__ __launch_bounds__((S + 1) * 64, 3) void k_decode_mfma(MultiArgs ma, i
       }
     };
 
-    for (int k = blo; k < bhi; k += kDepth) {
+  if (wave < S) {
+    // ---- column wave --------------------------------------------------------
+    // The ring goes out once h and the table are in LDS; its round trip runs
+    // under the barriers and the scaling.  (Issued before h has arrived, the
+    // ring's load instructions hold up the other waves' h loads in the CU's
+    // address unit, and so the barriers: 7% slower at B = 8.)  Up to kShort
+    // blocks: the wave's blocks rounded up to an even count are all loaded
+    // at once, unconditionally (at most one placeholder block, read past the
+    // buffer), so that the compiler counts them and block d waits only for
+    // its own loads.  More blocks: a ring of kDepth, refilled as blocks are
+    // done (its loads are conditional: those waits are for every load in
+    // flight).
+    const int n = bhi - blo;   // wave-uniform
+    auto exact = [&](auto nv) {
+      constexpr int V = decltype(nv)::value;
+      u32x4 qe[V], xe[V][XL];
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
+      for (int d = 0; d < V; ++d) {
+        const int oq = d < n ? qo + d * kBlk * 2 : kFar;
+        const int ox = d < n ? xo + d * kBlk * 2 : kFar;
+        qe[d] = ld16<kNonTemporal>(rq, oq);
+#pragma unroll
+        for (int u = 0; u < XL; ++u) xe[d][u] = ld16(rx, ox + 16 * u);
+        __builtin_amdgcn_sched_barrier(0);   // in block order
+      }
+      scale();
+      __builtin_amdgcn_sched_barrier(0);   // no block's work above the barriers
+#pragma unroll
+      for (int d = 0; d < V; ++d)
+        if ((V > 2 && d < V - 1) || d < n) block(qe[d], xe[d], blo + d);
+    };
+    if (n <= 2) {
+      exact(std::integral_constant<int, 2>{});
+    } else if (n <= 4) {
+      exact(std::integral_constant<int, 4>{});
+    } else if (n <= 6) {
+      exact(std::integral_constant<int, 6>{});
+    } else if (kShort >= 8 && n <= 8) {
+      exact(std::integral_constant<int, (kShort >= 8 ? 8 : 6)>{});
+    } else {
+      u32x4 qv[kDepth], xv[kDepth][XL];
+    __builtin_amdgcn_sched_barrier(0);
+    if (wave < S) {
+  #pragma unroll
       for (int d = 0; d < kDepth; ++d) {
-        const int blk = k + d;
-        if (blk >= bhi) break;                     // uniform
-        block(qv[d], xv[d], blk);
-        if (blk + kDepth < bhi) {
-          const int off = (blk - blo + kDepth) * kBlk * 2;
-          qv[d] = ld16<kNonTemporal>(rq, qo + off);
-#pragma unroll
-          for (int u = 0; u < XL; ++u) xv[d][u] = ld16(rx, xo + off + 16 * u);
+        if (blo + d < bhi) {
+          qv[d] = ld16<kNonTemporal>(rq, qo + d * kBlk * 2);
+  #pragma unroll
+          for (int u = 0; u < XL; ++u) xv[d][u] = ld16(rx, xo + d * kBlk * 2 + 16 * u);
+        }
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+      scale();
+      for (int k = blo; k < bhi; k += kDepth) {
+  #pragma unroll
+        for (int d = 0; d < kDepth; ++d) {
+          const int blk = k + d;
+          if (blk >= bhi) break;                     // uniform
+          block(qv[d], xv[d], blk);
+          if (blk + kDepth < bhi) {
+            const int off = (blk - blo + kDepth) * kBlk * 2;
+            qv[d] = ld16<kNonTemporal>(rq, qo + off);
+  #pragma unroll
+            for (int u = 0; u < XL; ++u) xv[d][u] = ld16(rx, xo + off + 16 * u);
+          }
         }
       }
     }
   } else {
-    // ---- staging wave: the tile's first kEntCap critical blocks into LDS ------
+    // ---- staging wave: the tile's entries (columns, O) --------------------------
+    // (The row pointers are read by this wave alone: a column wave reading
+    // them would wait for its whole ring.)
+    constexpr int kPass = kEntCap / 64;
+    int scol[kPass];
+    u32x4 so[kPass];
+    const int rsv = __builtin_amdgcn_readlane(rpv, 0);
+    const int nent = __builtin_amdgcn_readlane(rpv, kTile) - rsv;
+    const int nst = nent < kEntCap ? nent : kEntCap;
+    if (lane <= kTile) erow[lane] = rpv - rsv;
+    if (lane == 0) ebase = rsv;
+    const __amdgpu_buffer_rsrc_t rc = rsrc(a.O_col + rsv, nst * 4);
+    const __amdgpu_buffer_rsrc_t ro = rsrc(a.O + (size_t)rsv * 8, nst * 16);
+#pragma unroll
+    for (int p = 0; p < kPass; ++p) {
+      scol[p] = (int)__builtin_amdgcn_raw_buffer_load_b32(rc, (lane + 64 * p) * 4, 0, 0);
+      so[p] = ld16(ro, (lane + 64 * p) * 16);
+    }
+    scale();
+    // The tile's first kEntCap critical blocks into LDS.
 #pragma unroll
     for (int p = 0; p < kPass; ++p) {
       if (64 * p >= nst) break;                    // uniform
@@ -381,6 +424,7 @@ __global__ __launch_bounds__((S + 1) * 64, 3) void k_decode_mfma(MultiArgs ma, i
 
   // ---- output: item t (< 512) -> batch row t/32, rows 2(t%32), +1; thread
   // tid takes items tid, tid + NT (NT is a multiple of 32: one row pair).
+  const f16x4 t5 = tab[511 ^ 0x100];
   constexpr int kItems = (512 + NT - 1) / NT;
   const int r = (tid & 31) * 2;
   const int br = r >> 3, k = r & 7;
