@@ -20,14 +20,15 @@ __global__ __launch_bounds__(kT) void k_decode_e8d4(MultiArgs ma) {
   // rows padded by one zero chunk; for B = 1 also csc[c] = the scale of chunk c.
   extern __shared__ __align__(16) char dyn[];
 
-  // This workgroup's layer and its index among the layer's workgroups.
-  int li = 0;
-#pragma unroll
-  for (int l = 1; l < kMaxLayers; ++l)
-    if (l < ma.n && (int)blockIdx.x >= ma.start[l]) li = l;
-  const LinearArgs a = li == 0 ? ma.l[0] : li == 1 ? ma.l[1] : li == 2 ? ma.l[2] : ma.l[3];
-  const int wg = (int)blockIdx.x - ma.start[li];
+  // This workgroup's layer (grid row) and its index among the layer's
+  // workgroups.  The layer is the grid row rather than a search of the
+  // launch's layer boundaries, so the layer's arguments are read in the
+  // workgroup's first scalar loads, not in a second round trip after them.
+  const int li = (int)blockIdx.y;
+  const int wg = (int)blockIdx.x;
   const int G = ma.start[li + 1] - ma.start[li];
+  if (wg >= G) return;   // rows of the grid past this layer's workgroups
+  const LinearArgs a = ma.l[li];
 
   using L = Layer<BT, J, P, S, HAS_S, XT, false, ONE>;
   const L layer(a, wg, G);
@@ -153,7 +154,9 @@ int launch_one(const LinearArgs* layers, int n, hipStream_t s, int per_cu, size_
       ma.start[l + 1] = ma.start[l];
     }
   }
-  k_decode_e8d4<BT, J, P, S, HAS_S, XT, ONE><<<ma.start[n], kT, dyn, s>>>(ma);
+  int gx = 1;
+  for (int l = 0; l < n; ++l) gx = ma.start[l + 1] - ma.start[l] > gx ? ma.start[l + 1] - ma.start[l] : gx;
+  k_decode_e8d4<BT, J, P, S, HAS_S, XT, ONE><<<dim3(gx, n), kT, dyn, s>>>(ma);
   return 0;
 }
 

@@ -368,7 +368,7 @@ struct Layer {
             ss[b] += (float)r[e] * (float)r[e];
           }
           xpre[k][b] = __builtin_bit_cast(u32x4, r);
-          if (blockIdx.x == 0 && a.xsum && c < nch && b < B)
+          if (blockIdx.x == 0 && blockIdx.y == 0 && a.xsum && c < nch && b < B)
             *gp((u32x4*)(a.xsum + (size_t)b * N + c * 8)) = xpre[k][b];
         }
       }
