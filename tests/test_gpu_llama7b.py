@@ -12,6 +12,9 @@ blocks), 128-token random prompt, greedy decode at batch 1 and 8.
   relative L2.
 * Eight greedy steps replayed from the captured HIP graph give the tokens
   of eight eager steps.
+* Past the attention kernel's 256-row chunks: prompts of 254 and 510 tokens,
+  three greedy steps, then the logits at position 257 (two chunks) and 513
+  (three chunks) against the same dense reference.
 """
 
 from __future__ import annotations
@@ -133,3 +136,24 @@ def test_llama7b_decode(llama7b, B):
         assert torch.equal(dec.tok, eager[i]), f"step {i}"
     assert int(dec.pos.item()) == PROMPT + 8
     dec.graph = None
+
+
+@pytest.mark.parametrize("P", [254, 510])
+def test_llama7b_decode_past_chunks(llama7b, P):
+    from eptq_amd.llama import GraphDecoder
+    print(f"config 4 at B=1: prefill {P} tokens, 3 steps, logits at {P + 3}", flush=True)
+    dec = GraphDecoder(llama7b, 1, P + 8, device="cuda")
+    gen = torch.Generator("cuda").manual_seed(300 + P)
+    prompt = torch.randint(0, llama7b.cfg.vocab, (1, P), device="cuda", generator=gen)
+    toks = [dec.prefill(prompt).clone()]
+    for _ in range(3):
+        dec.step()
+        toks.append(dec.tok.clone())
+    assert int(dec.pos.item()) == P + 3
+    with torch.no_grad():
+        logits = llama7b.decode_next(dec.tok, dec.pos).float()
+    torch.cuda.synchronize()
+    want = _dense_last_logits(llama7b, torch.cat([prompt] + toks, dim=1))
+    err = rel_l2(logits.cpu().numpy(), want.cpu().numpy())
+    print(f"config 4 at B=1, position {P + 3}: logits rel_l2 {err:.3e}", flush=True)
+    assert err <= 1e-2
