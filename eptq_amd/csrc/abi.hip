@@ -113,6 +113,8 @@ int layer_args(const char* fn, int kind, const void* Q, const void* codes, int c
   a->nw = nullptr;
   a->xsum = nullptr;
   a->eps = 0.0f;
+  a->pad_ = 0;
+  a->res = nullptr;
   return EPTQ_OK;
 }
 
@@ -192,6 +194,13 @@ bool overlaps(const void* a, const void* b, size_t bytes) {
   if (!a || !b) return false;
   const uintptr_t x = (uintptr_t)a, y = (uintptr_t)b;
   return x < y + bytes && y < x + bytes;
+}
+
+// [a, a + a_bytes) and [b, b + b_bytes) share a byte.
+bool ranges_overlap(const void* a, size_t a_bytes, const void* b, size_t b_bytes) {
+  if (!a || !b || !a_bytes || !b_bytes) return false;
+  const uintptr_t x = (uintptr_t)a, y = (uintptr_t)b;
+  return x < y + b_bytes && y < x + a_bytes;
 }
 
 // Layers reading an activation that the decode kernel forms itself (prep 1:
@@ -399,6 +408,45 @@ int eptq_llama_norm_swiglu(const eptq_layer* gate_up, const void* codes, const v
   if (!gate_up) return fail(EPTQ_EINVAL, "eptq_llama_norm_swiglu: null layers");
   return fused_linear("eptq_llama_norm_swiglu", 2, gate_up, codes, resid, N, 1, delta, w, eps, resid_out, N, B, out,
                       8 * gate_up[0].M, stream, true);
+}
+
+int eptq_llama_linear(int n_layers, const eptq_layer* layers, const void* codes, const void* x, int N, int B,
+                      const void* norm_w, float eps, const void* resid, void* y, int ldy, void* work,
+                      long long work_bytes, void* stream) {
+  const char* fn = "eptq_llama_linear";
+  const int n = n_layers;
+  if (n < 1 || n > eptq::kMaxLayers || !layers) return fail(EPTQ_EINVAL, "%s: n_layers=%d (1..%d)", fn, n, eptq::kMaxLayers);
+  if (B < 0 || B > 16) return fail(B < 0 ? EPTQ_EINVAL : EPTQ_EUNSUPPORTED, "%s: B=%d (0..16)", fn, B);
+  if (B > 0 && (!x || !y)) return fail(EPTQ_EINVAL, "%s: null x/y", fn);
+  if (work && (!aligned16(work) || work_bytes < 0))
+    return fail(EPTQ_EINVAL, "%s: work must be 16-byte aligned with work_bytes >= 0", fn);
+  if ((x && !aligned16(x)) || (norm_w && !aligned16(norm_w)))
+    return fail(EPTQ_EUNSUPPORTED, "%s: x and norm_w must be 16-byte aligned", fn);
+  if (resid && ((uintptr_t)resid & 3) != 0) return fail(EPTQ_EUNSUPPORTED, "%s: resid must be 4-byte aligned", fn);
+  const size_t x_bytes = (size_t)B * N * 2, y_bytes = (size_t)B * (size_t)(ldy > 0 ? ldy : 0) * 2;
+  if (ranges_overlap(x, x_bytes, y, y_bytes) || ranges_overlap(x, x_bytes, resid, y_bytes))
+    return fail(EPTQ_EINVAL, "%s: x overlaps y or resid", fn);
+  eptq::LinearArgs a[eptq::kMaxLayers];
+  for (int l = 0; l < n; ++l) {
+    const eptq_layer& L = layers[l];
+    int rc = layer_args(fn, eptq::KIND_E8D4, L.Q, codes, EPTQ_F16, L.g, L.h, x, EPTQ_F16, L.O_vals, L.O_col,
+                        L.O_row_ptr, L.bias, L.S_group, L.n_groups, L.M, N, B, &a[l]);
+    if (rc) return rc;
+    if (L.y_offset < 0 || L.y_offset + 8LL * L.M > (long long)ldy || (L.y_offset & 3))
+      return fail(EPTQ_EINVAL, "%s: layer %d columns [%lld, %lld) outside a y row of %d (offset %% 4 == 0)",
+                  fn, l, L.y_offset, L.y_offset + 8LL * L.M, ldy);
+    a[l].y = (uint16_t*)y + L.y_offset;
+    a[l].ldy = ldy;
+    a[l].prep = norm_w ? 1 : 0;
+    a[l].nw = (const eptq::f16*)norm_w;
+    a[l].eps = eps;
+    a[l].res = resid ? (const uint16_t*)resid + L.y_offset : nullptr;
+  }
+  if (B == 0) return EPTQ_OK;
+  if (eptq::launch_decode_mfma_multi(a, n, (hipStream_t)stream, work, work ? work_bytes : 0) != 0)
+    return fail(EPTQ_EUNSUPPORTED, "%s: the matrix-core decode kernel does not take N=%d B=%d%s", fn, N, B,
+                norm_w ? " with the norm" : "");
+  return check_launch(fn);
 }
 
 int eptq_e8d4_dequant(const void* Q, const void* codes_f32, const void* g, const void* h,

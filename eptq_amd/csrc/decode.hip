@@ -312,6 +312,8 @@ int launch_decode_e8d4_multi(const LinearArgs* l, int n, hipStream_t s, void* wo
         l[i].xsum != a.xsum || l[i].eps != a.eps)
       return -1;
   if (a.prep != 0 && a.x_bf16) return -1;
+  for (int i = 0; i < n; ++i)
+    if (l[i].res) return -1;   // residual epilogue: matrix-core kernel only
   if (a.B < 1 || a.B > 8) return -1;
   if (a.codes_f32) return -1;  // fp32 tables take the generic kernel
   if (a.x_bf16) return a.S ? launch_b<true, bf16>(l, n, s) : launch_b<false, bf16>(l, n, s);
@@ -326,7 +328,7 @@ int launch_decode_e8d4_pair(const LinearArgs* l, hipStream_t s) {
   const LinearArgs& b = l[1];
   if (b.M != a.M || b.N != a.N || b.B != a.B || b.x != a.x || b.codes != a.codes || b.codes_f32 || a.codes_f32 ||
       a.x_bf16 || b.x_bf16 || (b.S != nullptr) != (a.S != nullptr) || b.prep != a.prep || b.ldx != a.ldx ||
-      b.x2 != a.x2 || b.nw != a.nw || b.xsum != a.xsum || b.eps != a.eps)
+      b.x2 != a.x2 || b.nw != a.nw || b.xsum != a.xsum || b.eps != a.eps || a.res || b.res)
     return -1;
   const int B = a.B;
   if (B == 1) return a.S ? launch_pair_bt<1, true>(l, s) : launch_pair_bt<1, false>(l, s);

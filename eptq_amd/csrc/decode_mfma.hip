@@ -92,12 +92,18 @@ __host__ __device__ inline size_t dyn_bytes(int N, bool has_s, int S) {
   return act > red ? act : red;
 }
 
-template <int S, bool HAS_S, typename XT, bool XH>
+template <int S, bool HAS_S, typename XT, bool XH, bool NORM>
 // At most 168 VGPRs (3 waves per SIMD): one 9-wave workgroup per CU.
 // XT: activation and output type (bf16 x is taken to fp16 exactly in fp16's
 // normal range before the scale; y is rounded from the fp32 sums to XT).
 // XH (B <= 8): each lane loads half of its batch row pair's activations (see
 // the column waves' loads below).
+// NORM (prep 1, fp16 x, B <= 8, N a multiple of 64): the input is
+// RMSNorm(x) = nw ⊙ x / rms(x).  The column scale becomes fp16(h·nw) (before
+// the power of two), the column waves add up x² over the activations they
+// load, and each batch row's sums are multiplied by 1/rms at the output (a
+// split tile's parts leave their x² sums with their partial sums).
+// a.res (fp16 x): y = fp16(res + fp16(out)).
 // Work split: tiles [0, T1) take one workgroup each; the tiles from T1 on
 // have their columns split over P workgroups (T1 = 0: every tile).  ma.start
 // counts tiles.
@@ -114,6 +120,8 @@ __global__ __launch_bounds__((S + 1) * 64, 3) void k_decode_mfma(MultiArgs ma, i
   __shared__ int erow[kTile + 1];   // entry index (from the tile's first) where each block row starts
   __shared__ int ebase;             // the tile's first entry
   __shared__ float wmax[S + 1];
+  __shared__ float wss[NORM ? S : 1][8];   // NORM: per column wave, Σx² per batch row
+  __shared__ float sinv[8];                // NORM: 1/rms per batch row
   extern __shared__ __attribute__((aligned(16))) char dyn[];
 
   // This workgroup's tile (index among all tiles of the launch) and part:
@@ -142,6 +150,7 @@ __global__ __launch_bounds__((S + 1) * 64, 3) void k_decode_mfma(MultiArgs ma, i
   const __amdgpu_buffer_rsrc_t rh = rsrc(a.h, N * 2);
   const __amdgpu_buffer_rsrc_t rx = rsrc(a.x, ((B - 1) * ldx + N) * 2);
   const __amdgpu_buffer_rsrc_t rs = rsrc(HAS_S ? a.S + (size_t)grp * N : nullptr, HAS_S ? N * 2 : 0);
+  const __amdgpu_buffer_rsrc_t rnw = rsrc(NORM ? a.nw : nullptr, NORM ? N * 2 : 0);
 
   // Table, h and the S row first (the column waves' ring follows them into
   // LDS).  Loads skipped on some path are left undefined there (never merged with
@@ -151,13 +160,14 @@ __global__ __launch_bounds__((S + 1) * 64, 3) void k_decode_mfma(MultiArgs ma, i
   // instruction costs address-unit time, in range or not.
   f16x4 tload;
   if (tid < 512) tload = *gp((const f16x4*)a.codes + tid);
-  u32x4 hw[4], sw[4];
+  u32x4 hw[4], sw[4], ww[4];
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
     const int c = tid + NT * k;
     if (NT * k + 64 * wave < nchp) {             // wave-uniform
       hw[k] = ld16(rh, c * 16);                  // zero past N
       if (HAS_S) sw[k] = ld16(rs, c * 16);
+      if (NORM) ww[k] = ld16(rnw, c * 16);
     }
   }
   // g and bias of this thread's two outputs (thread t < 512: rows 2(t%32), +1
@@ -167,6 +177,11 @@ __global__ __launch_bounds__((S + 1) * 64, 3) void k_decode_mfma(MultiArgs ma, i
   const uint32_t gpair = *gp((const uint32_t*)(a.g + oi));
   const __amdgpu_buffer_rsrc_t rbias = rsrc(a.bias, a.bias ? 16 * M : 0);
   const uint32_t bpair = __builtin_amdgcn_raw_buffer_load_b32(rbias, oi * 2, 0, 0);
+  // The residual of this thread's output pair (batch row tid / 32; zeros when
+  // absent or past the batch).
+  static_assert(NT >= 512, "one output pair per thread");
+  const __amdgpu_buffer_rsrc_t rres = rsrc(a.res, a.res ? B * a.ldy * 2 : 0);
+  const uint32_t rpair = __builtin_amdgcn_raw_buffer_load_b32(rres, (((tid >> 5) & 15) * a.ldy + orow) * 2, 0, 0);
 
   // Column waves: blocks [blo, bhi) of the tile's rows, the first kDepth of
   // them in flight.  Lane (i, kg) reads the 16 indices of block row m0 + i/2
@@ -197,10 +212,14 @@ __global__ __launch_bounds__((S + 1) * 64, 3) void k_decode_mfma(MultiArgs ma, i
   const int rrow = m0 + (part == 0 && lane <= kTile ? lane : part == 0 ? kTile : 0);
   const int rpv = (int)__builtin_amdgcn_raw_buffer_load_b32(rp, (rrow < M ? rrow : M) * 4, 0, 0);
 
-  // h (and the S row) into LDS as loaded; max|h|.
+  // h (times nw with NORM; and the S row) into LDS as loaded; max|h|.
   float mx = 0.0f;
-  auto put = [&](int c, const u32x4 h, const u32x4 sv) {
+  auto put = [&](int c, u32x4 h, const u32x4 sv, const u32x4 wv) {
     if (c < nchp) {
+      if (NORM) {
+#pragma unroll
+        for (int d = 0; d < 4; ++d) h[d] = pk_mul(h[d], wv[d]);
+      }
       *(u32x4*)(hs + c * 8) = h;
       if (HAS_S) *(u32x4*)(hss + c * 8) = sv;
       const f16x8 hv = __builtin_bit_cast(f16x8, h);
@@ -210,8 +229,9 @@ __global__ __launch_bounds__((S + 1) * 64, 3) void k_decode_mfma(MultiArgs ma, i
   };
 #pragma unroll
   for (int k = 0; k < 4; ++k)
-    if (NT * k + 64 * wave < nchp) put(tid + NT * k, hw[k], HAS_S ? sw[k] : hw[k]);
-  for (int c = tid + 4 * NT; c < nchp; c += NT) put(c, ld16(rh, c * 16), HAS_S ? ld16(rs, c * 16) : u32x4{});
+    if (NT * k + 64 * wave < nchp) put(tid + NT * k, hw[k], HAS_S ? sw[k] : hw[k], NORM ? ww[k] : hw[k]);
+  for (int c = tid + 4 * NT; c < nchp; c += NT)
+    put(c, ld16(rh, c * 16), HAS_S ? ld16(rs, c * 16) : u32x4{}, NORM ? ld16(rnw, c * 16) : u32x4{});
   mx = fmaxf(mx, partner<1>(mx));
   mx = fmaxf(mx, partner<2>(mx));
   mx = fmaxf(mx, partner<4>(mx));
@@ -258,6 +278,7 @@ __global__ __launch_bounds__((S + 1) * 64, 3) void k_decode_mfma(MultiArgs ma, i
   f32x4 acc[4];
 #pragma unroll
   for (int c = 0; c < 4; ++c) acc[c] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+  float ssq = 0.0f;   // NORM: Σx² of this lane's activations (batch row lane & 7)
   const mdec::Half half(i);
 
     auto block = [&](const u32x4 qh, const u32x4 (&xh)[XL], int blk) {
@@ -271,6 +292,10 @@ __global__ __launch_bounds__((S + 1) * 64, 3) void k_decode_mfma(MultiArgs ma, i
         q[1][d] = (uint32_t)__builtin_amdgcn_mov_dpp((int)qh[d], 0xF5, 0xF, 0xF, false);
       }
       x[0] = xh[0];
+      if constexpr (NORM) {
+#pragma unroll
+        for (int d = 0; d < 4; ++d) ssq = dec::dot2(xh[0][d], xh[0][d], ssq);
+      }
       if constexpr (XH) {
 #pragma unroll
         for (int d = 0; d < 4; ++d) x[1][d] = (uint32_t)__builtin_amdgcn_mov_dpp((int)xh[0][d], 0x128, 0xF, 0xF, false);
@@ -419,8 +444,20 @@ __global__ __launch_bounds__((S + 1) * 64, 3) void k_decode_mfma(MultiArgs ma, i
 #pragma unroll
     for (int v = 0; v < 4; ++v)
       *(f32x4*)&red[wave][b][16 * lg + 4 * v] = (f32x4){acc[0][v], acc[1][v], acc[2][v], acc[3][v]};
+    if constexpr (NORM) {
+      ssq += partner<8>(ssq);
+      ssq += partner<16>(ssq);
+      ssq += partner<32>(ssq);
+      if (lane < 8) wss[wave][lane] = ssq;
+    }
   }
   __syncthreads();
+  // NORM: this part's Σx² of batch row tid (tid < 8), the waves in order.
+  float ssl = 0.0f;
+  if (NORM && tid < 8) {
+#pragma unroll
+    for (int w = 0; w < S; ++w) ssl += wss[NORM ? w : 0][tid];
+  }
 
   // ---- output: item t (< 512) -> batch row t/32, rows 2(t%32), +1; thread
   // tid takes items tid, tid + NT (NT is a multiple of 32: one row pair).
@@ -469,7 +506,8 @@ __global__ __launch_bounds__((S + 1) * 64, 3) void k_decode_mfma(MultiArgs ma, i
         const int col = gp(a.O_col)[ge];
         const f16x8 o = *gp((const f16x8*)(a.O + (size_t)ge * 8));
         const f16 x16 = to_f16<XT>(gp(a.x)[(size_t)b * ldx + col]);
-        const f16 h1 = as_f16(gp((const uint16_t*)a.h)[col]) * down;
+        const f16 hc = as_f16(gp((const uint16_t*)a.h)[col]);
+        const f16 h1 = (NORM ? (f16)(hc * as_f16(gp((const uint16_t*)a.nw)[col])) : hc) * down;
         const float xo = (float)(f16)(x16 * h1);
         const float xm = HAS_S ? (float)(f16)(x16 * (f16)(h1 * as_f16(gp((const uint16_t*)a.S)[(size_t)grp * N + col]))) : xo;
         t0 += (float)o[k] * xo - (float)t5p[0] * xm;
@@ -495,9 +533,13 @@ __global__ __launch_bounds__((S + 1) * 64, 3) void k_decode_mfma(MultiArgs ma, i
   if (Pt > 1) {
     __shared__ int last_part;
     float* base = wpart + (size_t)(tile_g - T1) * Pt * (kPartBytes / 4) + r;
+    float* ssb = wpart + (size_t)(tile_g - T1) * Pt * (kPartBytes / 4) + 16 * 64;   // Σx² slots
 #pragma unroll
     for (int it = 0; it < kItems; ++it)
       if (ok[it]) st_pair(base + part * (kPartBytes / 4) + (((tid + NT * it) >> 5) & 15) * 64, s0[it], s1[it]);
+    if (NORM && tid < 8)
+      __hip_atomic_store((uint32_t*)(ssb + part * (kPartBytes / 4) + tid), __builtin_bit_cast(uint32_t, ssl),
+                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
     __syncthreads();
     if (tid == 0) {
@@ -522,17 +564,36 @@ __global__ __launch_bounds__((S + 1) * 64, 3) void k_decode_mfma(MultiArgs ma, i
         s0[it] = t0;
         s1[it] = t1;
       }
+      if (NORM && tid < 8) {   // the parts' Σx², in part order
+        float t = 0.0f;
+        for (int q = 0; q < Pt; ++q)
+          t += q == part ? ssl
+                         : __builtin_bit_cast(float, __hip_atomic_load((const uint32_t*)(ssb + q * (kPartBytes / 4) + tid),
+                                                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+        ssl = t;
+      }
     }
+  }
+  if (NORM && fin) {   // fin is uniform over the workgroup
+    if (tid < 8) sinv[tid] = rsqrtf(ssl / (float)N + a.eps);
+    __syncthreads();
   }
   if (fin) {
     const h2 gg = __builtin_bit_cast(h2, gpair), bb = __builtin_bit_cast(h2, bpair);
+    const h2 rr = __builtin_bit_cast(h2, rpair);
 #pragma unroll
     for (int it = 0; it < kItems; ++it) {
       if (!ok[it]) continue;
       const int b = ((tid + NT * it) >> 5) & 15;
-      const float y0 = s0[it] * out_scale * (float)gg[0] + (float)bb[0];
-      const float y1 = s1[it] * out_scale * (float)gg[1] + (float)bb[1];
-      const uint32_t pk = (uint32_t)Act<XT>::from_f32(y0) | ((uint32_t)Act<XT>::from_f32(y1) << 16);
+      const float sc = NORM ? out_scale * sinv[b & 7] : out_scale;
+      const float y0 = s0[it] * sc * (float)gg[0] + (float)bb[0];
+      const float y1 = s1[it] * sc * (float)gg[1] + (float)bb[1];
+      uint32_t pk = (uint32_t)Act<XT>::from_f32(y0) | ((uint32_t)Act<XT>::from_f32(y1) << 16);
+      if (a.res) {   // fp16 only (the launcher's check): y = fp16(res + fp16(out))
+        const h2 o = __builtin_bit_cast(h2, pk);
+        pk = (uint32_t)Act<XT>::from_f32((float)rr[0] + (float)o[0]) |
+             ((uint32_t)Act<XT>::from_f32((float)rr[1] + (float)o[1]) << 16);
+      }
       *gp((uint32_t*)(a.y + (size_t)b * a.ldy + orow)) = pk;
     }
   }
@@ -549,7 +610,7 @@ inline int parts_for(int split, int tiles, void* work, long long work_bytes) {
   return P;
 }
 
-template <int S, bool HAS_S, typename XT, bool XH>
+template <int S, bool HAS_S, typename XT, bool XH, bool NORM = false>
 int launch_t(const LinearArgs* l, int n, hipStream_t s, void* work, long long work_bytes) {
   int tiles = 0;
   for (int k = 0; k < n; ++k) tiles += (l[k].M + kTile - 1) / kTile;
@@ -568,7 +629,7 @@ int launch_t(const LinearArgs* l, int n, hipStream_t s, void* work, long long wo
     ma.start[k + 1] = ma.start[k] + (k < n ? (l[k].M + kTile - 1) / kTile : 0);   // tiles
   }
   const int grid = T1 + (tiles - T1) * P;
-  auto kern = k_decode_mfma<S, HAS_S, XT, XH>;
+  auto kern = k_decode_mfma<S, HAS_S, XT, XH, NORM>;
   const size_t dyn = dyn_bytes(l[0].N, HAS_S, S);
   static size_t attr = 0;
   if (dyn > attr) {
@@ -589,15 +650,22 @@ int launch_t(const LinearArgs* l, int n, hipStream_t s, void* work, long long wo
 int launch_decode_mfma_multi(const LinearArgs* l, int n, hipStream_t s, void* work, long long work_bytes) {
   if (n < 1 || n > kMaxLayers) return -1;
   const LinearArgs& a = l[0];
-  if (a.B < 1 || a.B > 16 || a.codes_f32 || a.prep != 0 || (a.N & 7) != 0) return -1;
+  if (a.B < 1 || a.B > 16 || a.codes_f32 || (a.N & 7) != 0) return -1;
+  // prep 1 (the norm at the output; no residual add before it, no xsum) and
+  // the residual: fp16 x, B <= 8, whole 64-column blocks (so Σx² sees no
+  // column past N).
+  const bool norm = a.prep == 1;
+  if (a.prep != 0 && (!norm || a.x2 || a.xsum || !a.nw || a.B > 8 || (a.N & 63) != 0 || a.x_bf16)) return -1;
+  if (norm && (((uintptr_t)a.nw & 15) != 0)) return -1;
   // y is written in pairs of fp16 (4-byte stores).
   if ((a.ldy & 1) != 0 || ((uintptr_t)a.y & 3) != 0) return -1;
   for (int i = 0; i < n; ++i) {
     const LinearArgs& b = l[i];
     if (b.N != a.N || b.B != a.B || b.x != a.x || b.ldx != a.ldx || b.codes != a.codes ||
         b.codes_f32 != a.codes_f32 || b.x_bf16 != a.x_bf16 || (b.S != nullptr) != (a.S != nullptr) ||
-        b.prep != 0 || ((uintptr_t)b.y & 3) != 0)
+        b.prep != a.prep || b.nw != a.nw || b.eps != a.eps || b.x2 || b.xsum || ((uintptr_t)b.y & 3) != 0)
       return -1;
+    if (b.res && (a.x_bf16 || ((uintptr_t)b.res & 3) != 0)) return -1;
     // S_group: one scale row per 64-row tile.
     if (b.S && (b.qb <= 0 || b.qb % 64 != 0)) return -1;
     if ((long)b.M * b.N * 2 >= (1L << 30)) return -1;   // 32-bit buffer offsets
@@ -610,6 +678,8 @@ int launch_decode_mfma_multi(const LinearArgs* l, int n, hipStream_t s, void* wo
   // workgroups: gate|up 11008x4096 at B=8 24.6 us against 22.2 us.)
   using namespace dmf;
   const bool xh = a.B <= 8;
+  if (norm) return a.S ? launch_t<kS, true, f16, true, true>(l, n, s, work, work_bytes)
+                       : launch_t<kS, false, f16, true, true>(l, n, s, work, work_bytes);
   if (a.x_bf16) {
     if (a.S) return xh ? launch_t<kS, true, bf16, true>(l, n, s, work, work_bytes)
                        : launch_t<kS, true, bf16, false>(l, n, s, work, work_bytes);

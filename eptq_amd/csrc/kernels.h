@@ -46,14 +46,19 @@ struct LinearArgs {
   // kernel only): the Linear's input is
   //   prep 0: x
   //   prep 1: RMSNorm(x + x2) = nw ⊙ r / rms(r), r = fp16(x + x2) (x2 may be
-  //           null); the first workgroup writes r to xsum (if non-null)
+  //           null); the first workgroup writes r to xsum (if non-null).
+  //           The matrix-core kernel takes prep 1 with x2 and xsum null: it
+  //           multiplies the weights by nw ⊙ x and the sums by 1/rms(x).
   int prep;
   int ldx;              // elements between consecutive rows of x
   const uint16_t* x2;
   const f16* nw;
   uint16_t* xsum;
   float eps;
-  int pad_[3];
+  int pad_;
+  // Residual (matrix-core kernel only; null elsewhere): y = fp16(res + fp16(out)),
+  // res laid out like y (it may be y itself).
+  const uint16_t* res;
 };
 static_assert(sizeof(LinearArgs) % 16 == 0, "LinearArgs is a whole number of 16-byte words");
 
@@ -94,16 +99,18 @@ int launch_decode_e8d4_multi(const LinearArgs* layers, int n, hipStream_t s, voi
 // layers[0].ldy; -1 when the pair is outside the kernel's range.
 int launch_decode_e8d4_pair(const LinearArgs* layers, hipStream_t s);
 
-// Matrix-core E8-D4 decode (B <= 16, fp16 or bf16 x, fp16 table, no fused preparation);
+// Matrix-core E8-D4 decode (B <= 16, fp16 or bf16 x, fp16 table; prep 1 and a
+// residual for fp16 x, B <= 8, N a multiple of 64);
 // -1 when the layers are outside its range.
 int launch_decode_mfma_multi(const LinearArgs* layers, int n, hipStream_t s, void* work = nullptr,
                              long long work_bytes = 0);
 // Split-K workspace of the matrix-core decode kernel: kSplitCounters int
 // arrival counters (one per 64-row tile of a launch), then fp32 partial sums,
-// kSplitPartBytes per (split tile, part).
+// kSplitPartBytes per (split tile, part): [16 batch rows][64 outputs], then
+// the part's sum of squares of x per batch row (prep 1).
 constexpr int kSplitCounters = 16384;
 constexpr size_t kSplitCounterBytes = (size_t)kSplitCounters * 4;
-constexpr size_t kSplitPartBytes = 16 * 64 * 4;
+constexpr size_t kSplitPartBytes = (16 * 64 + 16) * 4;
 constexpr int kSplitTileRows = 64;
 // Workspace bytes that let the matrix-core decode split every launch it takes.
 long long decode_mfma_work_bytes();

@@ -228,7 +228,8 @@ class QuantLlama(nn.Module):
         self.kc: Optional[list] = None
         self.split_attention = False
         # Decode step: the residual add + RMSNorm inside the q|k|v and gate|up
-        # launches (6 launches per layer) or as launches of their own (8).
+        # launches (B <= 2: the vector kernel; 3..8: the matrix-core kernel,
+        # with the adds in the o and down launches) or as launches of their own.
         self.fused_ops = True
 
     def alloc_cache(self, batch: int, max_len: int, device):
@@ -290,6 +291,22 @@ class QuantLlama(nn.Module):
         _lib.check(rc, "eptq_e8d4_forward_multi")
         return y
 
+    def _llin(self, mod, x, norm_w=None, resid=None):
+        """mod(t) on the matrix-core decode kernel (``eptq_llama_linear``),
+        t = x or RMSNorm(x) with weight norm_w; with resid the result is added
+        to resid in place and resid returned."""
+        arr, width = _cached_array(mod)
+        B, N = x.shape
+        y = resid if resid is not None else torch.empty((B, width), dtype=x.dtype, device=x.device)
+        work = getattr(self, "lin_work", None)
+        rc = _lib.load().eptq_llama_linear(
+            len(arr), arr, _parts(mod)[0]._codebook.data_ptr(), x.data_ptr(), N, B,
+            None if norm_w is None else norm_w.data_ptr(), self.cfg.eps,
+            None if resid is None else resid.data_ptr(), y.data_ptr(), width,
+            None if work is None else work.data_ptr(), 0 if work is None else work.numel(), _stream(x))
+        _lib.check(rc, "eptq_llama_linear")
+        return y
+
     def _norm_into(self, mod, x, delta, w):
         """mod(RMSNorm(x + delta)) and the residual x + delta (a new tensor when
         fused; x itself, updated in place, on the separate-launch path)."""
@@ -328,18 +345,30 @@ class QuantLlama(nn.Module):
         h = rmsnorm_(x, delta, self.norm.weight, self.cfg.eps)
         return self.lm_head(h)
 
+    def _matrix_core_step(self, B):
+        """Whether a decode step of B rows runs its Linears on the matrix-core
+        kernel with the norms and residual adds folded in (6 launches per
+        layer): 3 <= B <= 8, fp16, hidden a multiple of 64."""
+        return (self.fused_ops and 3 <= B <= 8 and self.cfg.hidden % 64 == 0
+                and self.embed_tokens.weight.dtype == torch.float16)
+
     def _decode_layers(self, tok, pos):
         """The decoder layers of one decode step: the residual stream x and the
-        last layer's output delta (their sum is the final norm's input)."""
+        last layer's output delta (their sum is the final norm's input; delta
+        is None when the last add is already in x)."""
         cfg = self.cfg
         H, Hk, D = cfg.heads, cfg.kv_heads, cfg.head_dim
         x = self.embed_tokens(tok[:, 0])                    # (B, hidden), the residual stream
         B = x.shape[0]
         lib = _lib.load()
         delta = None
+        mc = self._matrix_core_step(B)
         for i, layer in enumerate(self.layers):
             ln1, ln2 = layer.input_layernorm.weight, layer.post_attention_layernorm.weight
-            qkv, x = self._norm_into(layer.qkv_proj, x, delta, ln1)
+            if mc:
+                qkv = self._llin(layer.qkv_proj, x, norm_w=ln1)
+            else:
+                qkv, x = self._norm_into(layer.qkv_proj, x, delta, ln1)
             att = torch.empty((B, H * D), dtype=x.dtype, device=x.device)
             rc = lib.eptq_llama_rope_attn(qkv.data_ptr(), pos.data_ptr(), self.cos_tab.data_ptr(),
                                           self.sin_tab.data_ptr(), self.kc[i].data_ptr(), self.vc[i].data_ptr(),
@@ -347,6 +376,11 @@ class QuantLlama(nn.Module):
                                           None if self.attn_work is None else self.attn_work.data_ptr(),
                                           _stream(x))
             _lib.check(rc, "eptq_llama_rope_attn")
+            if mc:
+                self._llin(layer.o_proj, att, resid=x)                 # x += o(att)
+                act = silu_mul(self._llin(layer.gate_up_proj, x, norm_w=ln2))
+                self._llin(layer.down_proj, act, resid=x)              # x += down(act)
+                continue
             o = self._lin(layer.o_proj, att)
             act, x = self._norm_swiglu(layer.gate_up_proj, x, o, ln2)
             delta = self._lin(layer.down_proj, act)

@@ -131,7 +131,7 @@ long long eptq_e8d4_work_bytes(void);
  * call's contents: calls that overlap in time on one GPU race (wrong
  * results), whatever their streams.
  */
-#define EPTQ_NOALLOC_SCRATCH_BYTES 1114112
+#define EPTQ_NOALLOC_SCRATCH_BYTES 1130496
 int eptq_e8d4_forward_multi_noalloc(int n_layers, const eptq_layer* layers, const void* codes,
                                     int codes_dtype, const void* x, int x_dtype, int N, int B, void* y,
                                     int ldy, void* stream);

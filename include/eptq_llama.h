@@ -71,6 +71,27 @@ int eptq_llama_norm_linear(int n_layers, const eptq_layer* layers, const void* c
 int eptq_llama_norm_swiglu(const eptq_layer* gate_up, const void* codes, const void* resid, const void* delta,
                            const void* w, float eps, void* resid_out, int N, int B, void* out, void* stream);
 
+/* A decoder Linear group on the matrix-core decode kernel, with the RMSNorm
+ * before it and the residual add after it folded in (the fused forms of
+ * eptq_llama_norm_linear and eptq_llama_norm_swiglu take B <= 2 only):
+ *   y = Linear(t) (+ resid),  t = x, or t = RMSNorm(x) = norm_w ⊙ x ·
+ *   rsqrt(mean(x²) + eps) when norm_w is not NULL.
+ * The norm is applied as Linear(norm_w ⊙ x) · rsqrt(mean(x²) + eps) per batch
+ * row, so t is not rounded to fp16 (the result agrees with eptq_llama_rmsnorm
+ * then the Linear to fp16 rounding, not bit for bit).  With resid (laid out
+ * like y; it may be y itself) y = fp16(resid + fp16(Linear)), bit-identical to
+ * the Linear followed by the residual add of eptq_llama_rmsnorm.  layers,
+ * codes (fp16 table), y, ldy, work and work_bytes as in
+ * eptq_e8d4_forward_multi; x (B, N) fp16 must not overlap y or resid; norm_w
+ * (N) fp16, 16-byte aligned.  EPTQ_EUNSUPPORTED when the matrix-core kernel
+ * does not take the call (B > 16, or B > 8 or N % 64 != 0 with norm_w; then
+ * run eptq_llama_rmsnorm, the Linear and the add apart).  No counterpart in
+ * the reference, whose decode step runs the norms, Linears and residual adds
+ * as separate operators (bench_decode.py:44-71). */
+int eptq_llama_linear(int n_layers, const eptq_layer* layers, const void* codes, const void* x, int N, int B,
+                      const void* norm_w, float eps, const void* resid, void* y, int ldy, void* work,
+                      long long work_bytes, void* stream);
+
 /* Bytes of the eptq_llama_lm_head_argmax workspace for B batch rows
  * (zero-filled before its first use; every call leaves it zeroed). */
 long long eptq_llama_lm_head_work_bytes(int B);

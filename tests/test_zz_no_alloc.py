@@ -31,7 +31,7 @@ from _util import csr_dev, layer_np, table
 pytestmark = pytest.mark.gpu
 
 TOL = 1e-2
-SCRATCH_BYTES = 1114112   # EPTQ_NOALLOC_SCRATCH_BYTES
+SCRATCH_BYTES = 1130496   # EPTQ_NOALLOC_SCRATCH_BYTES
 
 
 def _layers(shapes, seed):
