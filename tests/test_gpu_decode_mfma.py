@@ -214,3 +214,34 @@ def test_mfma_decode_row_slices(B):
     assert rel_l2(y1.float().cpu().numpy(), y0.float().cpu().numpy()) < 1e-3
     assert torch.equal(linear_forward_multi(layers, lins[0]._codebook, x, work=work), y1)
     assert int(work[:65536].view(torch.int32).abs().sum()) == 0
+
+
+@pytest.mark.parametrize("n_layers,out,inp,B,work", [
+    (3, 1024, 2048, 3, False),
+    (3, 1024, 2048, 8, True),     # 48 tiles, each split over 4 parts
+    (2, 4096, 1024, 5, True),
+    (2, 1000, 1024, 8, False),    # last tile of 5 block rows
+])
+def test_mfma_decode_equal_layers(n_layers, out, inp, B, work):
+    """Layers of equal shape in one launch (q|k|v, gate|up): within 1e-2 of
+    the oracle, and without a workspace bit-identical to each layer launched
+    on its own (same tiles, same sums, same order)."""
+    from eptq_amd.kernels import decode_workspace
+    print(f"mfma decode equal layers {n_layers}x{out}x{inp} B={B} work={work}", flush=True)
+    q = E8D4Quantizer(radius=1.75)
+    qds = [make_layer(out, inp, seed=300 + 7 * k + B, percmask=0.002) for k in range(n_layers)]
+    lins = [EPTQLinear.from_quantized_data(qd, q, "e8_d4").cuda() for qd in qds]
+    x = make_x(B, inp, seed=B + 40)
+    layers = [dict(Q=l.Q, g=l.g, h=l.h, O_vals=l.O_vals, O_col=l.O_col, O_row_ptr=l.O_row_ptr,
+                   bias=l.bias, S_group=l.S_group) for l in lins]
+    w = decode_workspace("cuda") if work else None
+    y = linear_forward_multi(layers, lins[0]._codebook, x.cuda(), work=w)
+    torch.cuda.synchronize()
+    yn = y.float().cpu().numpy()
+    want = np.concatenate([_ref(qd, x) for qd in qds], axis=1)
+    e = rel_l2(yn, want)
+    print(f"  rel_l2 {e:.2e}", flush=True)
+    assert np.isfinite(yn).all() and e <= TOL
+    if not work:
+        alone = torch.cat([linear_forward_multi([L], lins[0]._codebook, x.cuda()) for L in layers], dim=1)
+        assert torch.equal(y, alone)

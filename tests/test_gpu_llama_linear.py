@@ -86,6 +86,8 @@ def _norm_w(N, seed):
     ([(1024, 1024), (256, 1024), (256, 1024)], 1024, 8, None, True),    # split over parts
     ([(11008, 1024), (11008, 1024)], 1024, 8, None, True),              # gate|up-like: 344 tiles
     ([(2048, 4096)], 4096, 5, 128, True),                                # S_group, one row per 128 rows
+    ([(1024, 1024), (1024, 1024), (1024, 1024)], 1024, 8, None, True),  # three equal layers, split over parts
+    ([(1024, 2048), (1024, 2048)], 2048, 4, None, False),               # two equal layers, whole tiles
 ])
 def test_llama_linear_norm(shapes, N, B, qb, use_work):
     print(f"eptq_llama_linear norm {shapes} B={B} qb={qb} work={use_work}", flush=True)
