@@ -595,7 +595,7 @@ def prefill_gemm(torch, dev, T=2048, reps=10):
     from eptq_amd.quantizers import E8D4Quantizer
     from eptq_amd.synthetic import make_layer, make_x
 
-    from eptq_amd.kernels import dequant
+    from eptq_amd.kernels import dequant, f16_gemm
 
     codes32 = E8D4Quantizer(radius=1.75).flat_table().float().to(dev)
     codes = codes32.half()
@@ -621,8 +621,15 @@ def prefill_gemm(torch, dev, T=2048, reps=10):
             W = dequant("e8_d4", layer["Q"], codes32, layer["g"], layer["h"], layer["O_vals"],
                         layer["O_col"], layer["O_row_ptr"])
             torch.nn.functional.linear(x, W)
+
+        def f3():
+            # The two-pass prefill of this library: the same W, then its own
+            # LDS-DMA GEMM (eptq_f16_gemm).
+            W = dequant("e8_d4", layer["Q"], codes32, layer["g"], layer["h"], layer["O_vals"],
+                        layer["O_col"], layer["O_row_ptr"])
+            f16_gemm(W, x)
         row = {"shape": f"{o}x{i}", "tokens": T}
-        for key, fn in (("fused", f), ("dequant_library_gemm", f2)):
+        for key, fn in (("fused", f), ("dequant_library_gemm", f2), ("two_pass", f3)):
             fn()
             d, _ = event_timed(torch, [fn] * reps, stream)
             us = statistics.median(d) * 1e3

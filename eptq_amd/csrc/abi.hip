@@ -449,6 +449,20 @@ int eptq_llama_linear(int n_layers, const eptq_layer* layers, const void* codes,
   return check_launch(fn);
 }
 
+int eptq_f16_gemm(const void* W, const void* x, const void* bias, int F, int N, int T, void* y, int ldy,
+                  void* stream) {
+  const char* fn = "eptq_f16_gemm";
+  if (F <= 0 || N <= 0 || T < 0 || ldy < F) return fail(EPTQ_EINVAL, "%s: F=%d N=%d T=%d ldy=%d", fn, F, N, T, ldy);
+  if (T == 0) return EPTQ_OK;
+  if (!W || !x || !y) return fail(EPTQ_EINVAL, "%s: null W/x/y", fn);
+  if (ranges_overlap(y, (size_t)T * ldy * 2, x, (size_t)T * N * 2) || ranges_overlap(y, (size_t)T * ldy * 2, W, (size_t)F * N * 2))
+    return fail(EPTQ_EINVAL, "%s: y overlaps x or W", fn);
+  if (eptq::launch_gemm_f16w((const uint16_t*)W, (const uint16_t*)x, (const eptq::f16*)bias, F, N, T, N, (uint16_t*)y,
+                             ldy, (hipStream_t)stream) != 0)
+    return fail(EPTQ_EUNSUPPORTED, "%s: F=%d N=%d ldy=%d (multiples of 64, 64, 4) or alignment", fn, F, N, ldy);
+  return check_launch(fn);
+}
+
 int eptq_e8d4_dequant(const void* Q, const void* codes_f32, const void* g, const void* h,
                       const void* O_vals, const void* O_col, const void* O_row_ptr,
                       const void* S_group, int n_groups, int M, int N, void* W, void* stream) {

@@ -1007,6 +1007,321 @@ __global__ __launch_bounds__(64 * (8 + NPW), (8 + NPW) / 4) void k_gemm_lds_e8d4
   }
 }
 
+// Prefill GEMM over weights already dequantized: y = x·Wᵀ + bias for fp16 W
+// (F × N, row-major, F = out_features) and x (T × N).  The tiles and MFMA
+// waves of k_gemm_lds_e8d4 (BF features × 256 tokens, 64-column K-steps, two
+// stages, one barrier per step); the producer waves bring both the x tile and
+// the W tile in by LDS DMA, W in the swizzled layout the decode writes (the
+// swizzle is in the source addresses: LDS DMA writes each lane's 16 bytes at
+// 16·lane of the instruction's kilobyte).  With W from k_dequant this is the
+// two-pass prefill: every weight decoded once, rather than once per 256-token
+// tile as in the fused kernel.
+template <int BF, int NPW, int NS, int GT = 4>
+__global__ __launch_bounds__(64 * (8 + NPW), (8 + NPW) / 4) void k_gemm_f16w(
+    const uint16_t* __restrict__ W, const uint16_t* __restrict__ x, const f16* __restrict__ bias, int N, int T,
+    int ldx, uint16_t* __restrict__ y, int ldy, int OB) {
+  constexpr int kBK = g3::kBK, kBT = g3::kBT;
+  constexpr int XS = kBT * 128, WS = BF * 128, W0 = NS * XS;
+  static_assert(NS == 2 || NS == 3, "stages");
+  constexpr int FW = BF / 2, FA = FW / 16, TW = kBT / 4, TB = TW / 16;
+  static_assert(NPW == 4 || NPW == 8, "producer waves");
+  static_assert(FW % 16 == 0 && BF % 8 == 0, "whole MFMA tiles, whole W kilobytes");
+  extern __shared__ __attribute__((aligned(1024))) char smem[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  // Workgroups are dealt to the 8 XCDs round-robin: give each XCD a run of
+  // consecutive tiles (same token tile, neighbouring feature tiles).
+  int blk = blockIdx.x;
+  const int G = gridDim.x;
+  if ((G & 7) == 0) blk = (blk & 7) * (G >> 3) + (blk >> 3);
+  // Tiles in bands of GT token tiles, token tile fastest: the 32 consecutive
+  // tiles one XCD runs at a time cover GT token tiles x 32/GT feature tiles,
+  // so each x and W slice comes from the last-level cache once per XCD and
+  // from the XCD's L2 for the rest.
+  const int TBn = G / OB;
+  const int band = blk / (GT * OB), r = blk - band * GT * OB;
+  const int gt = min(GT, TBn - band * GT);
+  const int ob = r / gt, tb = band * GT + r % gt;
+  const int f0 = ob * BF, t0 = tb * kBT;
+  const int nk = N / kBK;
+
+  if (wave >= 8) {
+    // ================= producer waves 8 .. 8 + NPW - 1 =================
+    const int dw = wave - 8;
+    constexpr int kXI = 32 / NPW;
+    auto issue_x = [&](int s, int st) {
+      char* base = smem + st * XS;
+#pragma unroll
+      for (int p = 0; p < kXI; ++p) {
+        const int j = NPW * p + dw;
+        const int r = 8 * j + (lane >> 3);
+        const int c = (lane & 7) ^ ((r >> 1) & 7);
+        const int tt = t0 + r < T ? t0 + r : T - 1;
+        __builtin_amdgcn_global_load_lds((const void*)(x + (size_t)tt * ldx + s * kBK + 8 * c),
+                                         (__attribute__((address_space(3))) void*)(base + j * 1024), 16, 0, 0);
+      }
+    };
+    // Kilobyte j of a W stage holds rows 8j .. 8j+7 (row pairs rp = 4j + lane/16);
+    // lane l's 16 bytes land at slot l % 16 of its pair's 256 bytes, which
+    // g3::wpos gives to chunk c = v/2 of row 2·rp + t, v = slot ^ 2(rp % 8),
+    // t = (v & 1) ^ ((rp / 2) & 1).  Every wave issues WI instructions (a
+    // wave with fewer kilobytes repeats its last one: the same bytes to the
+    // same place), so a wait can count them.
+    constexpr int WI = (BF / 8 + NPW - 1) / NPW;
+    auto issue_w = [&](int s, int st) {
+      char* base = smem + W0 + st * WS;
+#pragma unroll
+      for (int u = 0; u < WI; ++u) {
+        const int j0 = dw + NPW * u, j = j0 < BF / 8 ? j0 : j0 - NPW;
+        const int rp = 4 * j + (lane >> 4);
+        const int v = (lane & 15) ^ (2 * (rp & 7));
+        const int c = v >> 1, r = 2 * rp + ((v & 1) ^ ((rp >> 1) & 1));
+        __builtin_amdgcn_global_load_lds((const void*)(W + (size_t)(f0 + r) * N + s * kBK + 8 * c),
+                                         (__attribute__((address_space(3))) void*)(base + j * 1024), 16, 0, 0);
+      }
+    };
+    // NS stages: the loads of step j + NS - 1 go out after barrier j, so
+    // each step's loads have NS - 1 steps to land.
+#pragma unroll
+    for (int j = 0; j < NS - 1; ++j) {
+      if (j < nk) {
+        issue_x(j, j);
+        issue_w(j, j);
+      }
+    }
+    for (int j = 0; j < nk; ++j) {
+      // Before the barrier: X(j) and W(j) landed (the NS - 2 later steps'
+      // loads may still be in flight; every step issues the same count).
+      if (NS == 3 && j + 1 < nk) {
+        asm volatile("s_waitcnt vmcnt(%0)" :: "n"(kXI + WI) : "memory");
+      } else {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      }
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      if (j + NS - 1 < nk) {
+        issue_x(j + NS - 1, (j + NS - 1) % NS);
+        issue_w(j + NS - 1, (j + NS - 1) % NS);
+      }
+    }
+    return;
+  }
+
+  // ================= MFMA waves 0-7 =================
+  const int wf = wave & 1, wt = wave >> 1;
+  const int i = lane & 15, kg = lane >> 4;
+  f32x4 acc[FA][TB];
+#pragma unroll
+  for (int xx = 0; xx < FA; ++xx)
+#pragma unroll
+    for (int q = 0; q < TB; ++q) acc[xx][q] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  for (int j = 0; j < nk; ++j) {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    const char* xb = smem + (j % NS) * XS;
+    const char* wb = smem + W0 + (j % NS) * WS;
+    f16x8 af[2][FA], bf[2][TB];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+      for (int xx = 0; xx < FA; ++xx) af[ks][xx] = *(const f16x8*)(wb + g3::wpos(wf * FW + 16 * xx + i, 4 * ks + kg));
+#pragma unroll
+      for (int q = 0; q < TB; ++q) bf[ks][q] = *(const f16x8*)(xb + g3::xpos(wt * TW + 16 * q + i, 4 * ks + kg));
+    }
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int xx = 0; xx < FA; ++xx)
+#pragma unroll
+        for (int q = 0; q < TB; ++q)
+          acc[xx][q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[ks][xx], bf[ks][q], acc[xx][q], 0, 0, 0);
+  }
+  // ---- y = acc + bias: lane (n, lg) holds 4 consecutive features of token n ----
+#pragma unroll
+  for (int xx = 0; xx < FA; ++xx) {
+    const int f = f0 + wf * FW + 16 * xx + 4 * kg;
+    f16x4 b4 = {};
+    if (bias) b4 = *(const f16x4*)(bias + f);
+#pragma unroll
+    for (int q = 0; q < TB; ++q) {
+      const int tt = t0 + wt * TW + 16 * q + i;
+      if (tt >= T) continue;
+      f16x4 o;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) o[v] = (f16)(acc[xx][q][v] + (float)b4[v]);
+      *(f16x4*)(y + (size_t)tt * ldy + f) = o;
+    }
+  }
+}
+
+// k_gemm_f16w with BF x BT tiles and four matrix-core waves, one per SIMD,
+// each holding a (BF/2) x (BT/2) block of the tile, and their LDS reads a half-step ahead of
+// their MFMAs: the reads for the second half of step j (k 32..63) go out
+// before the MFMAs of the first half, the barrier of step j + 1 sits between
+// the two halves, and the reads of step j + 1's first half go out before the
+// MFMAs of step j's second half.  So the MFMAs never wait for LDS, and the
+// barrier no longer lines every wave's reads up into one burst.  Four
+// producer waves (one per SIMD) bring x and W in by LDS DMA, three stages
+// deep.  Eight waves in all: 256 registers per wave for up to 160 fp32
+// accumulators and two sets of fragments.
+template <int BF, int BT, int GT = 4>
+__global__ __launch_bounds__(512, 2) void k_gemm_f16w4(
+    const uint16_t* __restrict__ W, const uint16_t* __restrict__ x, const f16* __restrict__ bias, int N, int T,
+    int ldx, uint16_t* __restrict__ y, int ldy, int OB) {
+  constexpr int kBK = g3::kBK, kBT = BT, NS = 3, NPW = 4;
+  constexpr int XS = kBT * 128, WS = BF * 128, W0 = NS * XS;
+  constexpr int FW = BF / 2, FA = FW / 16, TW = kBT / 2, TB = TW / 16;
+  static_assert(FW % 16 == 0 && TW % 16 == 0 && FA * TB <= 40, "whole MFMA tiles, accumulators fit");
+  static_assert(NS * (XS + WS) <= g3::kLds, "three stages fit the LDS");
+  extern __shared__ __attribute__((aligned(1024))) char smem[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  int blk = blockIdx.x;
+  const int G = gridDim.x;
+  if ((G & 7) == 0) blk = (blk & 7) * (G >> 3) + (blk >> 3);
+  // Tiles in bands of GT token tiles, token tile fastest (as k_gemm_f16w).
+  const int TBn = G / OB;
+  const int band = blk / (GT * OB), r = blk - band * GT * OB;
+  const int gt = min(GT, TBn - band * GT);
+  const int ob = r / gt, tb = band * GT + r % gt;
+  const int f0 = ob * BF, t0 = tb * kBT;
+  const int nk = N / kBK;
+
+  if (wave >= 4) {
+    // ================= producer waves 4 .. 7 =================
+    const int dw = wave - 4;
+    constexpr int kXI = kBT / 8 / NPW;
+    auto issue_x = [&](int s, int st) {
+      char* base = smem + st * XS;
+#pragma unroll
+      for (int p = 0; p < kXI; ++p) {
+        const int j = NPW * p + dw;
+        const int rr = 8 * j + (lane >> 3);
+        const int c = (lane & 7) ^ ((rr >> 1) & 7);
+        const int tt = t0 + rr < T ? t0 + rr : T - 1;
+        __builtin_amdgcn_global_load_lds((const void*)(x + (size_t)tt * ldx + s * kBK + 8 * c),
+                                         (__attribute__((address_space(3))) void*)(base + j * 1024), 16, 0, 0);
+      }
+    };
+    // The W kilobytes as in k_gemm_f16w; every wave issues WI instructions
+    // (repeating its last kilobyte where it has fewer) so a wait can count.
+    constexpr int WI = (BF / 8 + NPW - 1) / NPW;
+    auto issue_w = [&](int s, int st) {
+      char* base = smem + W0 + st * WS;
+#pragma unroll
+      for (int u = 0; u < WI; ++u) {
+        const int j0 = dw + NPW * u, j = j0 < BF / 8 ? j0 : j0 - NPW;
+        const int rp = 4 * j + (lane >> 4);
+        const int v = (lane & 15) ^ (2 * (rp & 7));
+        const int c = v >> 1, rr = 2 * rp + ((v & 1) ^ ((rp >> 1) & 1));
+        __builtin_amdgcn_global_load_lds((const void*)(W + (size_t)(f0 + rr) * N + s * kBK + 8 * c),
+                                         (__attribute__((address_space(3))) void*)(base + j * 1024), 16, 0, 0);
+      }
+    };
+    // The loads of step j + 2 go out after barrier j, into the stage that
+    // step j - 1 used: every MFMA wave finished reading it before barrier j.
+    issue_x(0, 0);
+    issue_w(0, 0);
+    if (nk > 1) {
+      issue_x(1, 1);
+      issue_w(1, 1);
+    }
+    for (int j = 0; j < nk; ++j) {
+      // Before barrier j: X(j) and W(j) landed (step j + 1's may be in flight).
+      if (j + 1 < nk) {
+        asm volatile("s_waitcnt vmcnt(%0)" :: "n"(kXI + WI) : "memory");
+      } else {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      }
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      if (j + 2 < nk) {
+        issue_x(j + 2, (j + 2) % NS);
+        issue_w(j + 2, (j + 2) % NS);
+      }
+    }
+    return;
+  }
+
+  // ================= MFMA waves 0-3 =================
+  const int wf = wave & 1, wt = wave >> 1;
+  const int i = lane & 15, kg = lane >> 4;
+  f32x4 acc[FA][TB];
+#pragma unroll
+  for (int xx = 0; xx < FA; ++xx)
+#pragma unroll
+    for (int q = 0; q < TB; ++q) acc[xx][q] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  f16x8 a0[FA], b0[TB], a1[FA], b1[TB];
+  // Rows 16 apart sit 2 KB apart in both layouts (the swizzles depend on
+  // the row mod 16 only): one lane offset per half-step, immediates after.
+  const int wl0 = W0 + g3::wpos(wf * FW + i, kg), wl1 = W0 + g3::wpos(wf * FW + i, 4 + kg);
+  const int xl0 = g3::xpos(wt * TW + i, kg), xl1 = g3::xpos(wt * TW + i, 4 + kg);
+  auto rd_a = [&](f16x8& v, int st, int ks, int xx) {
+    v = *(const f16x8*)(smem + st * WS + (ks ? wl1 : wl0) + 2048 * xx);
+  };
+  auto rd_b = [&](f16x8& v, int st, int ks, int q) {
+    v = *(const f16x8*)(smem + st * XS + (ks ? xl1 : xl0) + 2048 * q);
+  };
+  // The MFMAs of one half-step, token column by column; after column q the
+  // reads of the next half-step's column q (and A fragment q) go out, so
+  // each fragment's registers come free as the next one's load is issued,
+  // and the first MFMAs of a half-step wait on no read just issued.  The
+  // scheduling barriers keep that order (left alone, the scheduler gathers
+  // the reads after most of the MFMAs and then waits on them).
+  auto mm_rd = [&](const f16x8* a, const f16x8* b, f16x8* an, f16x8* bn, int st, int ks) {
+#pragma unroll
+    for (int q = 0; q < TB; ++q) {
+#pragma unroll
+      for (int xx = 0; xx < FA; ++xx)
+        acc[xx][q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[xx], b[q], acc[xx][q], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+      if (q < FA) rd_a(an[q], st, ks, q);
+      rd_b(bn[q], st, ks, q);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int xx = TB; xx < FA; ++xx) rd_a(an[xx], st, ks, xx);
+  };
+  __builtin_amdgcn_s_barrier();   // barrier 0: step 0 landed
+  asm volatile("" ::: "memory");
+#pragma unroll
+  for (int xx = 0; xx < FA; ++xx) rd_a(a0[xx], 0, 0, xx);
+#pragma unroll
+  for (int q = 0; q < TB; ++q) rd_b(b0[q], 0, 0, q);
+  for (int j = 0; j + 1 < nk; ++j) {
+    mm_rd(a0, b0, a1, b1, j % NS, 1);
+    // Every read of stage j % NS done before barrier j + 1: the producers
+    // refill it after that barrier.
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    mm_rd(a1, b1, a0, b0, (j + 1) % NS, 0);
+  }
+  mm_rd(a0, b0, a1, b1, (nk - 1) % NS, 1);
+#pragma unroll
+  for (int q = 0; q < TB; ++q)
+#pragma unroll
+    for (int xx = 0; xx < FA; ++xx)
+      acc[xx][q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1[xx], b1[q], acc[xx][q], 0, 0, 0);
+  // ---- y = acc + bias: lane (n, lg) holds 4 consecutive features of token n ----
+#pragma unroll
+  for (int xx = 0; xx < FA; ++xx) {
+    const int f = f0 + wf * FW + 16 * xx + 4 * kg;
+    f16x4 b4 = {};
+    if (bias) b4 = *(const f16x4*)(bias + f);
+#pragma unroll
+    for (int q = 0; q < TB; ++q) {
+      const int tt = t0 + wt * TW + 16 * q + i;
+      if (tt >= T) continue;
+      f16x4 o;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) o[v] = (f16)(acc[xx][q][v] + (float)b4[v]);
+      *(f16x4*)(y + (size_t)tt * ldy + f) = o;
+    }
+  }
+}
+
 // y[t][f] = fp16((Σ_p part[p][t][f]) · g[f] + bias[f]), the parts added in
 // order (deterministic); 8 features per thread.
 __global__ __launch_bounds__(256) void k_gemm_split_sum(LinearArgs a, int P, const float* __restrict__ part) {
@@ -1224,6 +1539,54 @@ int launch_gemm(const LinearArgs& a, hipStream_t s, void* work, long long work_b
     if (rc) return rc;
   }
   return 0;
+}
+
+// Returns 0 if launched, -1 if the shape is outside k_gemm_f16w: F a
+// multiple of 64, N of 64, x rows 16-byte aligned, y rows 8-byte aligned.
+int launch_gemm_f16w(const uint16_t* W, const uint16_t* x, const f16* bias, int F, int N, int T, int ldx,
+                     uint16_t* y, int ldy, hipStream_t s) {
+  if (T <= 0 || F % 64 != 0 || N % g3::kBK != 0 || ldx % 8 != 0 || ((uintptr_t)x & 15) != 0 || ldy % 4 != 0 ||
+      ((uintptr_t)y & 7) != 0 || ((uintptr_t)W & 15) != 0 || (bias && ((uintptr_t)bias & 7) != 0))
+    return -1;
+  // Tile: the one with the least time, rounds of the CUs x one tile's
+  // K-step time (measured 1.08 / 1.64 / 0.88 / 0.65 us at 64 columns for
+  // 160 / 256 / 128 / 64 features x 256 tokens: per unit of area the
+  // narrowest is ~1.5x the others), the earlier one on ties.  (A 288 x 128
+  // tile, three whole rounds for 13824 features at 2048 tokens, measured
+  // slower than 256 x 256 with its second round partly idle.)
+  struct Tile { int bf, bt, step; };
+  constexpr Tile tiles[4] = {{160, 256, 108}, {256, 256, 164}, {128, 256, 88}, {64, 256, 65}};
+  const long cus = dec::cu_count();
+  int k = -1;
+  long best = -1;
+  for (int c = 0; c < 4; ++c) {
+    if (F % tiles[c].bf != 0) continue;
+    const long n = (long)(F / tiles[c].bf) * ((T + tiles[c].bt - 1) / tiles[c].bt);
+    const long cost = (n + cus - 1) / cus * tiles[c].step;
+    if (k < 0 || cost < best) {
+      best = cost;
+      k = c;
+    }
+  }
+  const int OB = F / tiles[k].bf;
+  const long grid = (long)OB * ((T + tiles[k].bt - 1) / tiles[k].bt);
+  if (grid > 0x7fffffff) return -1;
+  auto run = [&](auto kern, int threads, int bytes, int v) {
+    static bool attr[4] = {false, false, false, false};
+    if (!attr[v]) attr[v] = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, bytes) == hipSuccess;
+    if (!attr[v]) return -1;
+    kern<<<(unsigned)grid, threads, bytes, s>>>(W, x, bias, N, T, ldx, y, ldy, OB);
+    return 0;
+  };
+  // Three stages where they fit the CU's 160 KB of LDS (all but 256 x 256).
+  // The 256 x 256 tile runs the two-stage kernel with 8-token-tile bands
+  // (measured 4% faster than 4 at 13824 features).
+  switch (k) {
+    case 0: return run(k_gemm_f16w4<160, 256>, 512, 3 * (256 + 160) * 128, 0);
+    case 1: return run(k_gemm_f16w<256, 4, 2, 8>, 768, 2 * (256 + 256) * 128, 1);
+    case 2: return run(k_gemm_f16w4<128, 256>, 512, 3 * (256 + 128) * 128, 2);
+    default: return run(k_gemm_f16w4<64, 256>, 512, 3 * (256 + 64) * 128, 3);
+  }
 }
 
 template int launch_gemm<KIND_E8D4>(const LinearArgs&, hipStream_t, void*, long long);

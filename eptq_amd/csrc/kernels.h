@@ -112,6 +112,10 @@ constexpr int kSplitCounters = 16384;
 constexpr size_t kSplitCounterBytes = (size_t)kSplitCounters * 4;
 constexpr size_t kSplitPartBytes = (16 * 64 + 16) * 4;
 constexpr int kSplitTileRows = 64;
+// Prefill GEMM over dequantized fp16 weights: y (T, F) = x (T, N) · Wᵀ + bias
+// for W (F, N) row-major; -1 when the shape is outside the kernel.
+int launch_gemm_f16w(const uint16_t* W, const uint16_t* x, const f16* bias, int F, int N, int T, int ldx,
+                     uint16_t* y, int ldy, hipStream_t s);
 // Workspace bytes that let the matrix-core decode split every launch it takes.
 long long decode_mfma_work_bytes();
 namespace dec { int mfma_min_batch_init(); }

@@ -230,6 +230,25 @@ def dequant(kind: str, Q, codes, g, h, O_vals, O_col, O_row_ptr, S_group=None,
     return W
 
 
+def f16_gemm(W: torch.Tensor, x: torch.Tensor, bias: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """y (T, F) = x (T, N) · Wᵀ + bias for fp16 W (F, N): the second pass of
+    the two-pass prefill (``eptq_f16_gemm``).  Raises EptqError (code 2)
+    where the kernel does not take the shape (F, N multiples of 64)."""
+    _require(W.dtype == torch.float16 and x.dtype == torch.float16 and W.is_contiguous() and x.is_contiguous()
+             and W.dim() == 2 and x.dim() == 2 and W.shape[1] == x.shape[1] and W.device == x.device,
+             "W (F, N) and x (T, N) must be contiguous fp16 on one device")
+    _require(bias is None or (bias.dtype == torch.float16 and bias.is_contiguous() and bias.numel() == W.shape[0]),
+             "bias must be a contiguous fp16 (F,) tensor")
+    F, N = int(W.shape[0]), int(W.shape[1])
+    T = int(x.shape[0])
+    y = torch.empty((T, F), dtype=torch.float16, device=x.device)
+    with torch.cuda.device(x.device):
+        rc = _lib.load().eptq_f16_gemm(_ptr(W), _ptr(x), _ptr(bias), F, N, T, _ptr(y), F,
+                                       torch.cuda.current_stream().cuda_stream)
+    _lib.check(rc, "eptq_f16_gemm")
+    return y
+
+
 # ---------------------------------------------------------------------------
 # torch.library registration (names and signatures of kernels/__init__.py:50-91)
 # ---------------------------------------------------------------------------

@@ -28,6 +28,7 @@ SIGNATURES = {
     "eptq_e8d4_forward_multi_noalloc": ([_I, _P, _P, _I, _P, _I, _I, _I, _P, _I, _P], _I),
     "eptq_e8d4_dequant": ([_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _P, _P], _I),
     "eptq_e8_dequant": ([_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _P, _P], _I),
+    "eptq_f16_gemm": ([_P, _P, _P, _I, _I, _I, _P, _I, _P], _I),
 }
 
 class EptqLayer(ctypes.Structure):

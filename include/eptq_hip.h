@@ -159,6 +159,21 @@ int eptq_e8d4_dequant(const void* Q, const void* codes_f32,
                       const void* S_group, int n_groups,
                       int M, int N, void* W, void* stream);
 
+/*
+ * Second pass of a two-pass prefill: y (T, ldy) fp16 = x (T, N) fp16 · Wᵀ +
+ * bias for fp16 W (F, N) row-major, e.g. from eptq_e8d4_dequant (F = 8M),
+ * bias NULL or (F) fp16.  The LDS-DMA GEMM of the fused prefill kernel with
+ * W streamed from memory instead of decoded per 256-token tile, so every
+ * weight is decoded once per call (by the dequantization) rather than once
+ * per token tile.  F and N multiples of 64, ldy >= F and a multiple of 4;
+ * W, x 16-byte aligned, y 8-byte aligned; EPTQ_EUNSUPPORTED otherwise.  No
+ * counterpart in the reference, whose module runs the fused kernel
+ * (csrc/eptq_kernels.cu:309-461) or a dense matmul; callers are prefills
+ * long enough that decoding W once pays for writing and reading it.
+ */
+int eptq_f16_gemm(const void* W, const void* x, const void* bias, int F, int N, int T,
+                  void* y, int ldy, void* stream);
+
 int eptq_e8_dequant(const void* Q, const void* codes_f32,
                     const void* g, const void* h,
                     const void* O_vals, const void* O_col, const void* O_row_ptr,
