@@ -1289,16 +1289,20 @@ __global__ __launch_bounds__(512, 2) void k_gemm_f16w4(
   for (int xx = 0; xx < FA; ++xx) rd_a(a0[xx], 0, 0, xx);
 #pragma unroll
   for (int q = 0; q < TB; ++q) rd_b(b0[q], 0, 0, q);
+  // The loop runs from barrier to barrier (the second half of step j, then
+  // the first half of step j + 1), so its first MFMAs follow the wait at the
+  // barrier and the reads issued just before the back edge are not waited
+  // for there.
+  mm_rd(a0, b0, a1, b1, 0, 1);
   for (int j = 0; j + 1 < nk; ++j) {
-    mm_rd(a0, b0, a1, b1, j % NS, 1);
     // Every read of stage j % NS done before barrier j + 1: the producers
     // refill it after that barrier.
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
     mm_rd(a1, b1, a0, b0, (j + 1) % NS, 0);
+    mm_rd(a0, b0, a1, b1, (j + 1) % NS, 1);
   }
-  mm_rd(a0, b0, a1, b1, (nk - 1) % NS, 1);
 #pragma unroll
   for (int q = 0; q < TB; ++q)
 #pragma unroll
