@@ -455,7 +455,10 @@ int eptq_f16_gemm(const void* W, const void* x, const void* bias, int F, int N, 
   if (F <= 0 || N <= 0 || T < 0 || ldy < F) return fail(EPTQ_EINVAL, "%s: F=%d N=%d T=%d ldy=%d", fn, F, N, T, ldy);
   if (T == 0) return EPTQ_OK;
   if (!W || !x || !y) return fail(EPTQ_EINVAL, "%s: null W/x/y", fn);
-  if (ranges_overlap(y, (size_t)T * ldy * 2, x, (size_t)T * N * 2) || ranges_overlap(y, (size_t)T * ldy * 2, W, (size_t)F * N * 2))
+  // y's extent ends at its last row's F columns: y may be a column slice of
+  // a wider output, allocated right before x or W.
+  const size_t y_bytes = ((size_t)(T - 1) * ldy + F) * 2;
+  if (ranges_overlap(y, y_bytes, x, (size_t)T * N * 2) || ranges_overlap(y, y_bytes, W, (size_t)F * N * 2))
     return fail(EPTQ_EINVAL, "%s: y overlaps x or W", fn);
   if (eptq::launch_gemm_f16w((const uint16_t*)W, (const uint16_t*)x, (const eptq::f16*)bias, F, N, T, N, (uint16_t*)y,
                              ldy, (hipStream_t)stream) != 0)

@@ -168,11 +168,46 @@ def _workspace_outside_graph_pools(device, stream) -> torch.Tensor:
     return box["w"]
 
 
+# Token count from which linear_forward_multi runs the two-pass prefill
+# (every weight decoded once into a transient fp16 W, then eptq_f16_gemm):
+# measured 1.09-1.36x the fused kernel at 2048 tokens on the six Llama-2-7B /
+# 13B projection shapes, mixed at 1024 (0.85-1.11x: the fused kernel splits K
+# over idle CUs there), slower at 512.
+TWO_PASS_MIN_TOKENS = 2048
+
+
+def _two_pass_into(lib, layers, codes, x, y) -> None:
+    """y[:, layer columns] = x · W_lᵀ + bias_l with each layer's W decoded once
+    (``eptq_e8d4_dequant`` into one transient buffer sized for the largest
+    layer, reused layer after layer on the stream) and multiplied by
+    ``eptq_f16_gemm``.  The table is the kernels' (fp16, widened to fp32):
+    the same table values the fused kernel multiplies."""
+    N = int(x.shape[1])
+    B, ldy = int(x.shape[0]), int(y.shape[1])
+    tab = codes if codes.dtype == torch.float32 else codes.float()
+    F_max = max(8 * int(L["Q"].shape[0]) for L in layers)
+    wbuf = torch.empty(F_max * N, dtype=torch.float16, device=x.device)
+    off = 0
+    with torch.cuda.device(x.device):
+        stream = torch.cuda.current_stream().cuda_stream
+        for L in layers:
+            M = int(L["Q"].shape[0])
+            rc = lib.eptq_e8d4_dequant(_ptr(L["Q"]), _ptr(tab), _ptr(L["g"]), _ptr(L["h"]), _ptr(L["O_vals"]),
+                                       _ptr(L["O_col"]), _ptr(L["O_row_ptr"]), None, 0, M, N, _ptr(wbuf), stream)
+            _lib.check(rc, "eptq_e8d4_dequant")
+            rc = lib.eptq_f16_gemm(_ptr(wbuf), _ptr(x), _ptr(L.get("bias")), 8 * M, N, B,
+                                   _ptr(y) + 2 * off, ldy, stream)
+            _lib.check(rc, "eptq_f16_gemm")
+            off += 8 * M
+
+
 def linear_forward_multi(layers, codes, x, work: Optional[torch.Tensor] = None) -> torch.Tensor:
     """E8-D4 layers sharing ``x`` (B, N) -> (B, Σ out) with the layers' outputs
     side by side, in one decode launch when the kernel takes them all.
     ``layers``: dicts with Q, g, h, O_vals, O_col, O_row_ptr and optional
-    bias, S_group (the EPTQLinear buffers).  ``work``: optional workspace from
+    bias, S_group (the EPTQLinear buffers).  From TWO_PASS_MIN_TOKENS fp16
+    tokens (layers without S_group, 64-multiple shapes) it runs the two-pass
+    prefill instead (``_two_pass_into``).  ``work``: optional workspace from
     ``decode_workspace`` (lets batches of 3..16 split the columns of layers
     with few row tiles over several workgroups); calls sharing one must not
     overlap in time."""
@@ -197,6 +232,10 @@ def linear_forward_multi(layers, codes, x, work: Optional[torch.Tensor] = None) 
     if B == 0:
         return y
     lib = _lib.load()
+    if (B >= TWO_PASS_MIN_TOKENS and x.dtype == torch.float16 and N % 64 == 0
+            and all(L.get("S_group") is None and (8 * int(L["Q"].shape[0])) % 64 == 0 for L in keep)):
+        _two_pass_into(lib, keep, codes, x, y)
+        return y
     with torch.cuda.device(x.device):
         stream = torch.cuda.current_stream().cuda_stream
         rc = lib.eptq_e8d4_forward_multi(len(layers), arr, _ptr(codes),

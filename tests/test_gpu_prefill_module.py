@@ -4,13 +4,17 @@
 library's own kernels — 16-row slices of the matrix-core decode up to 128
 rows, the prefill GEMMs that decode weight tiles into LDS or registers above
 (the reference's module does the same with its fused GEMM,
-``kernels/linear.py:199-210`` → ``csrc/eptq_kernels.cu:520-537``).  Checks:
+``kernels/linear.py:199-210`` → ``csrc/eptq_kernels.cu:520-537``), and from
+2048 fp16 tokens the two-pass prefill (``eptq_e8d4_dequant`` into a
+transient fp16 W, then ``eptq_f16_gemm``).  Checks:
 
 * within 1e-2 relative L2 of the fp32 reconstruct + matmul oracle (the
   north-star tolerance) at both sides of the 128-row switch;
 * no torch GEMM runs inside the forward (``F.linear`` / ``torch.matmul``
-  raise while the module is called), and no fp16 W is materialized (the
-  forward leaves only its output allocated);
+  raise while the module is called), and the forward leaves only its output
+  allocated (the two-pass prefill's W is freed on return);
+* at 2048+ tokens (two-pass) within 3e-3 of the fused prefill kernel on the
+  same layers;
 * multi-layer stacking (GQA q|k|v with a bias on one layer only), S_group,
   E8 layers, dense critical blocks, bf16 input.
 """
@@ -131,3 +135,28 @@ def test_module_prefill_edges(out, inp, T, dtype):
         assert y.shape == (0, out) and y.dtype == dtype
         return
     _check(mod, [qd], "e8_d4", 1.75, T, seed=T + 1, dtype=dtype)
+
+
+@pytest.mark.parametrize("T", [2048, 2100])
+def test_module_prefill_two_pass(T):
+    print(f"module prefill two-pass q|k|v 1280+256+256 x 1024, T={T}, bias on k only", flush=True)
+    from eptq_amd.kernels import TWO_PASS_MIN_TOKENS, _lib
+    assert T >= TWO_PASS_MIN_TOKENS
+    q = E8D4Quantizer(radius=1.75)
+    qds = [make_layer(o, 1024, seed=500 + k, percmask=0.002, bias=(k == 1))
+           for k, o in enumerate((1280, 256, 256))]
+    lins = [EPTQLinear.from_quantized_data(qd, q, "e8_d4").cuda() for qd in qds]
+    y = _check(EPTQMultiLinear(lins), qds, "e8_d4", 1.75, T, seed=13)
+    # The fused prefill kernel on the same layers (one C-ABI launch each).
+    x = make_x(T, 1024, seed=13).cuda()
+    outs = []
+    for lin in lins:
+        yl = torch.empty((T, lin.out_features), dtype=torch.float16, device="cuda")
+        _lib.forward_into("e8_d4", lin.Q, lin._codebook, lin.g, lin.h, x, lin.O_vals, lin.O_col,
+                          lin.O_row_ptr, lin.bias, None, yl, torch.cuda.current_stream().cuda_stream)
+        outs.append(yl)
+    fused = torch.cat(outs, dim=1)
+    torch.cuda.synchronize()
+    e = rel_l2(y.float().cpu().numpy(), fused.float().cpu().numpy())
+    print(f"  rel_l2 vs the fused kernel {e:.2e}", flush=True)
+    assert e <= 3e-3
