@@ -1019,7 +1019,7 @@ __global__ __launch_bounds__(64 * (8 + NPW), (8 + NPW) / 4) void k_gemm_lds_e8d4
 template <int BF, int NPW, int NS, int GT = 4>
 __global__ __launch_bounds__(64 * (8 + NPW), (8 + NPW) / 4) void k_gemm_f16w(
     const uint16_t* __restrict__ W, const uint16_t* __restrict__ x, const f16* __restrict__ bias, int N, int T,
-    int ldx, uint16_t* __restrict__ y, int ldy, int OB) {
+    int ldx, uint16_t* __restrict__ y, int ldy, int OB, int F) {
   constexpr int kBK = g3::kBK, kBT = g3::kBT;
   constexpr int XS = kBT * 128, WS = BF * 128, W0 = NS * XS;
   static_assert(NS == 2 || NS == 3, "stages");
@@ -1168,7 +1168,7 @@ __global__ __launch_bounds__(64 * (8 + NPW), (8 + NPW) / 4) void k_gemm_f16w(
 template <int BF, int BT, int GT = 4>
 __global__ __launch_bounds__(512, 2) void k_gemm_f16w4(
     const uint16_t* __restrict__ W, const uint16_t* __restrict__ x, const f16* __restrict__ bias, int N, int T,
-    int ldx, uint16_t* __restrict__ y, int ldy, int OB) {
+    int ldx, uint16_t* __restrict__ y, int ldy, int OB, int F) {
   constexpr int kBK = g3::kBK, kBT = BT, NS = 3, NPW = 4;
   constexpr int XS = kBT * 128, WS = BF * 128, W0 = NS * XS;
   constexpr int FW = BF / 2, FA = FW / 16, TW = kBT / 2, TB = TW / 16;
@@ -1215,7 +1215,8 @@ __global__ __launch_bounds__(512, 2) void k_gemm_f16w4(
         const int rp = 4 * j + (lane >> 4);
         const int v = (lane & 15) ^ (2 * (rp & 7));
         const int c = v >> 1, rr = 2 * rp + ((v & 1) ^ ((rp >> 1) & 1));
-        __builtin_amdgcn_global_load_lds((const void*)(W + (size_t)(f0 + rr) * N + s * kBK + 8 * c),
+        const int fr = f0 + rr < F ? f0 + rr : F - 1;   // a ragged last tile repeats row F - 1
+        __builtin_amdgcn_global_load_lds((const void*)(W + (size_t)fr * N + s * kBK + 8 * c),
                                          (__attribute__((address_space(3))) void*)(base + j * 1024), 16, 0, 0);
       }
     };
@@ -1312,6 +1313,7 @@ __global__ __launch_bounds__(512, 2) void k_gemm_f16w4(
 #pragma unroll
   for (int xx = 0; xx < FA; ++xx) {
     const int f = f0 + wf * FW + 16 * xx + 4 * kg;
+    if (f >= F) continue;   // past a ragged last tile (F is a multiple of 4)
     f16x4 b4 = {};
     if (bias) b4 = *(const f16x4*)(bias + f);
 #pragma unroll
@@ -1555,31 +1557,33 @@ int launch_gemm_f16w(const uint16_t* W, const uint16_t* x, const f16* bias, int 
   // Tile: the one with the least time, rounds of the CUs x one tile's
   // K-step time (measured 1.08 / 1.64 / 0.88 / 0.65 us at 64 columns for
   // 160 / 256 / 128 / 64 features x 256 tokens: per unit of area the
-  // narrowest is ~1.5x the others), the earlier one on ties.  (A 288 x 128
-  // tile, three whole rounds for 13824 features at 2048 tokens, measured
-  // slower than 256 x 256 with its second round partly idle.)
-  struct Tile { int bf, bt, step; };
-  constexpr Tile tiles[4] = {{160, 256, 108}, {256, 256, 164}, {128, 256, 88}, {64, 256, 65}};
+  // narrowest is ~1.5x the others), the earlier one on ties.  The
+  // three-stage kernel takes a ragged last feature tile (F a multiple of
+  // 64, not of the tile), the two-stage 256 x 256 one whole tiles only.  (A
+  // 288 x 128 tile, three whole rounds for 13824 features at 2048 tokens,
+  // measured slower than 256 x 256 with its second round partly idle.)
+  struct Tile { int bf, bt, step; bool ragged; };
+  constexpr Tile tiles[4] = {{160, 256, 108, true}, {256, 256, 164, false}, {128, 256, 88, true}, {64, 256, 65, true}};
   const long cus = dec::cu_count();
   int k = -1;
   long best = -1;
   for (int c = 0; c < 4; ++c) {
-    if (F % tiles[c].bf != 0) continue;
-    const long n = (long)(F / tiles[c].bf) * ((T + tiles[c].bt - 1) / tiles[c].bt);
+    if (F % tiles[c].bf != 0 && !tiles[c].ragged) continue;
+    const long n = (long)((F + tiles[c].bf - 1) / tiles[c].bf) * ((T + tiles[c].bt - 1) / tiles[c].bt);
     const long cost = (n + cus - 1) / cus * tiles[c].step;
     if (k < 0 || cost < best) {
       best = cost;
       k = c;
     }
   }
-  const int OB = F / tiles[k].bf;
+  const int OB = (F + tiles[k].bf - 1) / tiles[k].bf;
   const long grid = (long)OB * ((T + tiles[k].bt - 1) / tiles[k].bt);
   if (grid > 0x7fffffff) return -1;
   auto run = [&](auto kern, int threads, int bytes, int v) {
     static bool attr[4] = {false, false, false, false};
     if (!attr[v]) attr[v] = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, bytes) == hipSuccess;
     if (!attr[v]) return -1;
-    kern<<<(unsigned)grid, threads, bytes, s>>>(W, x, bias, N, T, ldx, y, ldy, OB);
+    kern<<<(unsigned)grid, threads, bytes, s>>>(W, x, bias, N, T, ldx, y, ldy, OB, F);
     return 0;
   };
   // Three stages where they fit the CU's 160 KB of LDS (all but 256 x 256).

@@ -4,8 +4,8 @@ bias over fp16 W streamed by LDS DMA into the fused kernel's tiles).
 * Against torch's fp32 matmul of the same fp16 operands: within 2e-3
   relative L2 (fp32 accumulation, fp16 output), for each tile the launcher
   picks on a 256-CU MI355X (160 x 256, 256 x 256, 128 x 256 and 64 x 256
-  features x tokens), token counts that leave a ragged last token tile, with
-  and without bias.
+  features x tokens), ragged last feature tiles (160 and 128), token counts
+  that leave a ragged last token tile, with and without bias.
 * The two passes together (``eptq_e8d4_dequant`` then the GEMM) within 1e-2
   of the oracle's reconstruct + matmul on a synthetic E8-D4 layer.
 * EPTQ_EUNSUPPORTED for F or N not a multiple of 64.
@@ -27,9 +27,10 @@ pytestmark = pytest.mark.gpu
 
 @pytest.mark.parametrize("F,N,T,bias", [
     (5120, 512, 2000, False),    # 160 x 256 tiles
-    (13824, 256, 2000, True),    # 256 x 256 (the two-stage kernel)
-    (13824, 128, 2100, False),   # 256 x 256, ragged last token tile
+    (13824, 256, 2000, True),    # 160 x 256, ragged last feature tile (64 of 160 rows)
+    (13824, 128, 2100, False),   # 256 x 256 (the two-stage kernel), ragged last token tile
     (4096, 256, 1900, True),     # 128 x 256
+    (5184, 256, 2048, True),     # 128 x 256, ragged last feature tile (64 of 128 rows)
     (1024, 2048, 257, True),     # 64 x 256 (few tiles: the narrowest)
     (64, 256, 17, False),        # 64 x 256, one token tile
 ])
