@@ -88,54 +88,64 @@ __global__ __launch_bounds__(256) void k_dequant(
         h8[c] = n0 + c < N ? h[n0 + c] : (f16)0.0f;
       }
     }
-    f16x8 out[8];
+    // out[k] word c/2: the fp16 pair (column c, column c + 1) of output row
+    // 8m + k, converted two at a time (one v_cvt_pk_f16_f32).
+    u32x4 out[8];
 #pragma unroll
-    for (int c = 0; c < 8; ++c) {
-      const int n = n0 + c;
-      const unsigned u = (unsigned)((int)q8[c] + 32768);
-      float v[8];
-      if (u == 65535u) {
-        const int i = csr_lower_bound(O_col, r0, r1, n);
-        const bool hit = (i < r1) && (O_col[i] == n);
+    for (int c = 0; c < 8; c += 2) {
+      float v[2][8];
 #pragma unroll
-        for (int k = 0; k < 8; ++k) v[k] = hit ? (float)O[(size_t)i * 8 + k] : 0.0f;
-      } else {
-        f32x4 a, b;
-        if (KIND == KIND_E8D4) {
-          a = tab[u >> 7];
-          b = tab[((u >> 14) << 7) | (u & 127u)];
+      for (int cc = 0; cc < 2; ++cc) {
+        const int n = n0 + c + cc;
+        const unsigned u = (unsigned)((int)q8[c + cc] + 32768);
+        if (u == 65535u) {
+          const int i = csr_lower_bound(O_col, r0, r1, n);
+          const bool hit = (i < r1) && (O_col[i] == n);
+#pragma unroll
+          for (int k = 0; k < 8; ++k) v[cc][k] = hit ? (float)O[(size_t)i * 8 + k] : 0.0f;
         } else {
-          const f32x4* p = (const f32x4*)(table + (size_t)u * 8);
-          a = p[0];
-          b = p[1];
-        }
-        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
-        v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
-        if (HAS_S) {
+          f32x4 a, b;
+          if (KIND == KIND_E8D4) {
+            a = tab[u >> 7];
+            b = tab[((u >> 14) << 7) | (u & 127u)];
+          } else {
+            const f32x4* p = (const f32x4*)(table + (size_t)u * 8);
+            a = p[0];
+            b = p[1];
+          }
+          v[cc][0] = a.x; v[cc][1] = a.y; v[cc][2] = a.z; v[cc][3] = a.w;
+          v[cc][4] = b.x; v[cc][5] = b.y; v[cc][6] = b.z; v[cc][7] = b.w;
+          if (HAS_S) {
 #pragma unroll
-          for (int k = 0; k < 8; ++k)
-            v[k] = n < N ? v[k] * (float)S[(size_t)((8 * m + k) / qb) * N + n] : v[k];
+            for (int k = 0; k < 8; ++k)
+              v[cc][k] = n < N ? v[cc][k] * (float)S[(size_t)((8 * m + k) / qb) * N + n] : v[cc][k];
+          }
         }
       }
-      const float hn = (float)h8[c];
+      const float h0 = (float)h8[c], h1 = (float)h8[c + 1];
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
-        const float t = v[k] * gk[k];
-        float w = t * hn;
+        float w0 = (v[0][k] * gk[k]) * h0;
+        float w1 = (v[1][k] * gk[k]) * h1;
         // The reference rounds twice: to fp32 at the multiply, then to fp16.
-        // Materialize the fp32 product so the compiler cannot fold multiply and
-        // conversion into one single-rounding mix instruction.
-        asm volatile("" : "+v"(w));
-        out[k][c] = (f16)w;
+        // Materialize the fp32 products so the compiler cannot fold multiply
+        // and conversion into one single-rounding mix instruction.
+        asm volatile("" : "+v"(w0), "+v"(w1));
+        out[k][c >> 1] = __builtin_bit_cast(uint32_t, (f16x2){(f16)w0, (f16)w1});
       }
     }
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
       f16* dst = W + (size_t)(8 * m + k) * N + n0;
       if (full) {
-        __builtin_nontemporal_store(out[k], (f16x8*)dst);   // streamed out, not re-read here
+        __builtin_nontemporal_store(out[k], (u32x4*)dst);   // streamed out, not re-read here
       } else {
-        for (int c = 0; c < 8 && n0 + c < N; ++c) dst[c] = out[k][c];
+        for (int c = 0; c < 8 && n0 + c < N; ++c) {
+          // Through a local: this compiler's __builtin_bit_cast of a vector
+          // element lvalue reads element 0.
+          const uint32_t wd = out[k][c >> 1];
+          dst[c] = __builtin_bit_cast(f16x2, wd)[c & 1];
+        }
       }
     }
   }
