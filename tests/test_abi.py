@@ -95,6 +95,26 @@ def test_dequant_rejects_invalid_arguments(lib, fn):
     assert rc == _lib.EPTQ_EUNSUPPORTED and "8-byte" in lib.eptq_last_error().decode()
 
 
+def test_f16_gemm_rejects_invalid_arguments(lib):
+    # (W, x, bias, F, N, T, y, ldy, stream); no argument here reaches a launch.
+    f = lib.eptq_f16_gemm
+    W, x, y = 1 << 20, 1 << 24, 1 << 28
+    assert f(W, x, None, 128, 64, 0, y, 128, None) == _lib.EPTQ_OK          # empty batch: no-op
+    assert f(None, x, None, 128, 64, 4, y, 128, None) == _lib.EPTQ_EINVAL
+    assert "null" in lib.eptq_last_error().decode()
+    assert f(W, x, None, 0, 64, 4, y, 128, None) == _lib.EPTQ_EINVAL
+    assert f(W, x, None, 128, 64, 4, y, 64, None) == _lib.EPTQ_EINVAL       # ldy < F
+    assert f(W, x, None, 128, 64, 4, x + 64, 128, None) == _lib.EPTQ_EINVAL  # y inside x
+    assert "overlaps" in lib.eptq_last_error().decode()
+    assert f(W, x, None, 100, 64, 4, y, 128, None) == _lib.EPTQ_EUNSUPPORTED  # F not a multiple of 64
+    assert "multiples" in lib.eptq_last_error().decode()
+    # y a column slice whose last row ends right where x starts: no overlap
+    # (F = 100 then stops it before any launch, with the shape error).
+    T, F, ldy = 4, 100, 256
+    assert f(W, y + ((T - 1) * ldy + F) * 2, None, F, 64, T, y, ldy, None) == _lib.EPTQ_EUNSUPPORTED
+    assert f(W, y + ((T - 1) * ldy + F) * 2 - 2, None, F, 64, T, y, ldy, None) == _lib.EPTQ_EINVAL
+
+
 def test_python_wrapper_raises_on_error_codes(lib):
     with pytest.raises(_lib.EptqError, match="eptq_e8d4_forward"):
         _lib.check(lib.eptq_e8d4_forward(*_fwd_args(Q=None)), "eptq_e8d4_forward")
