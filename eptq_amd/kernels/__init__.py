@@ -77,8 +77,11 @@ def _check_layer(kind, Q, codes, g, h, O_vals, O_col, O_row_ptr, S_group):
 
 
 def linear_forward(kind: str, Q, codes, g, h, x, O_vals, O_col, O_row_ptr, bias=None,
-                   S_group=None) -> torch.Tensor:
-    """Run the fused quantized Linear on ``x`` (B, N) -> (B, 8M), dtype of x."""
+                   S_group=None, two_pass: bool = False) -> torch.Tensor:
+    """Run the fused quantized Linear on ``x`` (B, N) -> (B, 8M), dtype of x.
+    ``two_pass`` (what the module's ops pass): from ``_two_pass_min`` fp16
+    tokens (2048 for E8-D4, 256 with S_group, 64 for E8) and 64-multiple
+    shapes, the two-pass prefill instead of the fused C-ABI kernel."""
     M, N, n_groups = _check_layer(kind, Q, codes, g, h, O_vals, O_col, O_row_ptr, S_group)
     _require(x.device == Q.device, "x must be on the layer's device")
     _require(x.dim() == 2 and x.shape[1] == N, f"x must be (B, {N})")
@@ -92,6 +95,10 @@ def linear_forward(kind: str, Q, codes, g, h, x, O_vals, O_col, O_row_ptr, bias=
     if B == 0:
         return y
     lib = _lib.load()
+    layer = dict(Q=Q, g=g, h=h, O_vals=O_vals, O_col=O_col, O_row_ptr=O_row_ptr, bias=bias, S_group=S_group)
+    if two_pass and B >= _two_pass_min(kind, [layer]) and _two_pass_ok([layer], x, N):
+        _two_pass_into(lib, [layer], codes, x, y, kind)
+        return y
     fn = lib.eptq_e8d4_forward if kind == "e8_d4" else lib.eptq_e8_forward
     with torch.cuda.device(x.device):
         stream = torch.cuda.current_stream().cuda_stream
@@ -168,46 +175,69 @@ def _workspace_outside_graph_pools(device, stream) -> torch.Tensor:
     return box["w"]
 
 
-# Token count from which linear_forward_multi runs the two-pass prefill
-# (every weight decoded once into a transient fp16 W, then eptq_f16_gemm):
-# measured 1.09-1.36x the fused kernel at 2048 tokens on the six Llama-2-7B /
-# 13B projection shapes, mixed at 1024 (0.85-1.11x: the fused kernel splits K
-# over idle CUs there), slower at 512.
+# Token counts from which the module's forwards run the two-pass prefill
+# (every weight decoded once into a transient fp16 W, then eptq_f16_gemm).
+# E8-D4: measured 1.09-1.36x the fused kernel at 2048 tokens on the six
+# Llama-2-7B / 13B projection shapes, mixed at 1024 (0.85-1.11x: the fused
+# kernel splits K over idle CUs there), slower at 512.  E8-D4 with S_group
+# (whose fused path is the older grouped GEMM): 1.2-1.8x from 256 tokens on
+# 4096x4096, 11008x4096 and 4096x11008.  E8 (whose fused GEMM gathers from a
+# 1 MB table): 2x from 64 tokens on 4096x4096, 1.3-2.5x at 256-2048 tokens on
+# 4096x4096 and 11008x4096, level on 3072x768.
 TWO_PASS_MIN_TOKENS = 2048
+TWO_PASS_MIN_TOKENS_GROUPED = 256
+TWO_PASS_MIN_TOKENS_E8 = 64
 
 
-def _two_pass_into(lib, layers, codes, x, y) -> None:
+def _two_pass_min(kind: str, layers) -> int:
+    if kind != "e8_d4":
+        return TWO_PASS_MIN_TOKENS_E8
+    return TWO_PASS_MIN_TOKENS_GROUPED if all(L.get("S_group") is not None for L in layers) else TWO_PASS_MIN_TOKENS
+
+
+def _two_pass_ok(layers, x, N) -> bool:
+    return (x.dtype == torch.float16 and N % 64 == 0
+            and all((8 * int(L["Q"].shape[0])) % 64 == 0 for L in layers))
+
+
+def _two_pass_into(lib, layers, codes, x, y, kind: str = "e8_d4") -> None:
     """y[:, layer columns] = x · W_lᵀ + bias_l with each layer's W decoded once
-    (``eptq_e8d4_dequant`` into one transient buffer sized for the largest
-    layer, reused layer after layer on the stream) and multiplied by
-    ``eptq_f16_gemm``.  The table is the kernels' (fp16, widened to fp32):
-    the same table values the fused kernel multiplies."""
+    (``eptq_e8d4_dequant`` / ``eptq_e8_dequant``, S_group included, into one
+    transient buffer sized for the largest layer, reused layer after layer on
+    the stream) and multiplied by ``eptq_f16_gemm``.  The table is the
+    kernels' (fp16, widened to fp32): the same table values the fused kernel
+    multiplies."""
     N = int(x.shape[1])
     B, ldy = int(x.shape[0]), int(y.shape[1])
     tab = codes if codes.dtype == torch.float32 else codes.float()
     F_max = max(8 * int(L["Q"].shape[0]) for L in layers)
     wbuf = torch.empty(F_max * N, dtype=torch.float16, device=x.device)
+    deq = lib.eptq_e8d4_dequant if kind == "e8_d4" else lib.eptq_e8_dequant
     off = 0
     with torch.cuda.device(x.device):
         stream = torch.cuda.current_stream().cuda_stream
         for L in layers:
             M = int(L["Q"].shape[0])
-            rc = lib.eptq_e8d4_dequant(_ptr(L["Q"]), _ptr(tab), _ptr(L["g"]), _ptr(L["h"]), _ptr(L["O_vals"]),
-                                       _ptr(L["O_col"]), _ptr(L["O_row_ptr"]), None, 0, M, N, _ptr(wbuf), stream)
-            _lib.check(rc, "eptq_e8d4_dequant")
+            S = L.get("S_group")
+            n_groups = 0 if S is None else int(S.shape[0])
+            rc = deq(_ptr(L["Q"]), _ptr(tab), _ptr(L["g"]), _ptr(L["h"]), _ptr(L["O_vals"]), _ptr(L["O_col"]),
+                     _ptr(L["O_row_ptr"]), _ptr(S), n_groups, M, N, _ptr(wbuf), stream)
+            _lib.check(rc, deq.__name__)
             rc = lib.eptq_f16_gemm(_ptr(wbuf), _ptr(x), _ptr(L.get("bias")), 8 * M, N, B,
                                    _ptr(y) + 2 * off, ldy, stream)
             _lib.check(rc, "eptq_f16_gemm")
             off += 8 * M
 
 
-def linear_forward_multi(layers, codes, x, work: Optional[torch.Tensor] = None) -> torch.Tensor:
+def linear_forward_multi(layers, codes, x, work: Optional[torch.Tensor] = None,
+                         two_pass: bool = False) -> torch.Tensor:
     """E8-D4 layers sharing ``x`` (B, N) -> (B, Σ out) with the layers' outputs
     side by side, in one decode launch when the kernel takes them all.
     ``layers``: dicts with Q, g, h, O_vals, O_col, O_row_ptr and optional
-    bias, S_group (the EPTQLinear buffers).  From TWO_PASS_MIN_TOKENS fp16
-    tokens (layers without S_group, 64-multiple shapes) it runs the two-pass
-    prefill instead (``_two_pass_into``).  ``work``: optional workspace from
+    bias, S_group (the EPTQLinear buffers).  ``two_pass`` (what the
+    module's op passes): from ``_two_pass_min`` fp16 tokens (64-multiple
+    shapes) the two-pass prefill (``_two_pass_into``) instead of the fused
+    C-ABI launch.  ``work``: optional workspace from
     ``decode_workspace`` (lets batches of 3..16 split the columns of layers
     with few row tiles over several workgroups); calls sharing one must not
     overlap in time."""
@@ -232,8 +262,7 @@ def linear_forward_multi(layers, codes, x, work: Optional[torch.Tensor] = None) 
     if B == 0:
         return y
     lib = _lib.load()
-    if (B >= TWO_PASS_MIN_TOKENS and x.dtype == torch.float16 and N % 64 == 0
-            and all(L.get("S_group") is None and (8 * int(L["Q"].shape[0])) % 64 == 0 for L in keep)):
+    if two_pass and B >= _two_pass_min("e8_d4", keep) and _two_pass_ok(keep, x, N):
         _two_pass_into(lib, keep, codes, x, y)
         return y
     with torch.cuda.device(x.device):
@@ -296,7 +325,7 @@ def f16_gemm(W: torch.Tensor, x: torch.Tensor, bias: Optional[torch.Tensor] = No
 def e8_forward(Q: torch.Tensor, codebook: torch.Tensor, g: torch.Tensor, h: torch.Tensor,
                x: torch.Tensor, O_vals: torch.Tensor, O_col: torch.Tensor,
                O_row_ptr: torch.Tensor, bias: torch.Tensor) -> torch.Tensor:
-    return linear_forward("e8_lattice", Q, codebook, g, h, x, O_vals, O_col, O_row_ptr, bias)
+    return linear_forward("e8_lattice", Q, codebook, g, h, x, O_vals, O_col, O_row_ptr, bias, two_pass=True)
 
 
 @e8_forward.register_fake
@@ -308,7 +337,7 @@ def _e8_forward_fake(Q, codebook, g, h, x, O_vals, O_col, O_row_ptr, bias):
 def e8d4_forward(Q: torch.Tensor, codes: torch.Tensor, g: torch.Tensor, h: torch.Tensor,
                  x: torch.Tensor, O_vals: torch.Tensor, O_col: torch.Tensor,
                  O_row_ptr: torch.Tensor, bias: torch.Tensor) -> torch.Tensor:
-    return linear_forward("e8_d4", Q, codes, g, h, x, O_vals, O_col, O_row_ptr, bias)
+    return linear_forward("e8_d4", Q, codes, g, h, x, O_vals, O_col, O_row_ptr, bias, two_pass=True)
 
 
 @e8d4_forward.register_fake
@@ -321,7 +350,8 @@ def e8_forward_grouped(Q: torch.Tensor, codebook: torch.Tensor, g: torch.Tensor,
                        x: torch.Tensor, O_vals: torch.Tensor, O_col: torch.Tensor,
                        O_row_ptr: torch.Tensor, bias: torch.Tensor,
                        S_group: torch.Tensor) -> torch.Tensor:
-    return linear_forward("e8_lattice", Q, codebook, g, h, x, O_vals, O_col, O_row_ptr, bias, S_group)
+    return linear_forward("e8_lattice", Q, codebook, g, h, x, O_vals, O_col, O_row_ptr, bias, S_group,
+                          two_pass=True)
 
 
 @e8_forward_grouped.register_fake
@@ -334,7 +364,7 @@ def e8d4_forward_grouped(Q: torch.Tensor, codes: torch.Tensor, g: torch.Tensor, 
                          x: torch.Tensor, O_vals: torch.Tensor, O_col: torch.Tensor,
                          O_row_ptr: torch.Tensor, bias: torch.Tensor,
                          S_group: torch.Tensor) -> torch.Tensor:
-    return linear_forward("e8_d4", Q, codes, g, h, x, O_vals, O_col, O_row_ptr, bias, S_group)
+    return linear_forward("e8_d4", Q, codes, g, h, x, O_vals, O_col, O_row_ptr, bias, S_group, two_pass=True)
 
 
 @e8d4_forward_grouped.register_fake
@@ -386,7 +416,7 @@ def e8d4_forward_multi(Q: List[torch.Tensor], codes: torch.Tensor, g: List[torch
                    bias=bias[i], S_group=S_group[i]) for i in range(len(Q))]
     if work is None and x.is_cuda:
         work = stream_workspace(x.device)
-    return linear_forward_multi(layers, codes, x, work=work)
+    return linear_forward_multi(layers, codes, x, work=work, two_pass=True)
 
 
 @e8d4_forward_multi.register_fake

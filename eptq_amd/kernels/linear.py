@@ -17,9 +17,10 @@ Differences, all towards the reference's own reconstruct semantics:
 * every batch size runs a hand-written HIP kernel of this library: the decode
   matvec for ≤16 rows, 16-row slices of the matrix-core decode up to 128 rows,
   the prefill GEMM that decodes weight tiles into LDS above (the reference's
-  ``csrc/eptq_kernels.cu:520-537`` route), and from 2048 fp16 tokens the
-  two-pass prefill: each weight decoded once into a transient fp16 W (freed
-  on return), then this library's W-streaming GEMM.  No library GEMM runs.  ``EPTQ_CUDA_DECODE`` / ``EPTQ_FORCE_TRITON`` are
+  ``csrc/eptq_kernels.cu:520-537`` route), and from 2048 fp16 tokens (256
+  for S_group layers, 64 for E8 layers) the two-pass prefill: each weight
+  decoded once into a transient fp16 W (freed on return), then this
+  library's W-streaming GEMM.  No library GEMM runs.  ``EPTQ_CUDA_DECODE`` / ``EPTQ_FORCE_TRITON`` are
   accepted and ignored.
 * ``dequantize()`` returns the bit-exact fp16 W of ``dequantize_layer`` from the
   GPU (needs the fp32 table, kept alongside the fp16 kernel table).

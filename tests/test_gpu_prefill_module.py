@@ -5,7 +5,8 @@ library's own kernels — 16-row slices of the matrix-core decode up to 128
 rows, the prefill GEMMs that decode weight tiles into LDS or registers above
 (the reference's module does the same with its fused GEMM,
 ``kernels/linear.py:199-210`` → ``csrc/eptq_kernels.cu:520-537``), and from
-2048 fp16 tokens the two-pass prefill (``eptq_e8d4_dequant`` into a
+2048 fp16 tokens (256 for E8-D4 layers with S_group, 64 for E8 layers) the
+two-pass prefill (``eptq_e8d4_dequant`` / ``eptq_e8_dequant`` into a
 transient fp16 W, then ``eptq_f16_gemm``).  Checks:
 
 * within 1e-2 relative L2 of the fp32 reconstruct + matmul oracle (the
@@ -81,9 +82,12 @@ def _check(mod, qds, kind, r, T, seed, dtype=torch.float16):
     ("e8_d4", 1.75, 1024, 2048, 64, 0.002, True, None),     # matrix-core decode slices
     ("e8_d4", 1.75, 1024, 2048, 128, 0.002, False, None),
     ("e8_d4", 1.75, 1280, 2048, 300, 0.002, True, None),    # LDS-decode GEMM, ragged token tile
-    ("e8_d4", 1.75, 2048, 1024, 300, 0.01, False, 128),     # S_group GEMM
-    ("e8_d4", 1.75, 256, 4096, 130, 0.05, True, 64),        # dense critical blocks
-    ("e8_lattice", 1.6, 3072, 768, 200, 0.002, True, None),
+    ("e8_d4", 1.75, 2048, 1024, 300, 0.01, False, 128),     # S_group: two-pass from 256 tokens
+    ("e8_d4", 1.75, 256, 4096, 130, 0.05, True, 64),        # dense critical blocks, S_group GEMM
+    ("e8_lattice", 1.6, 3072, 768, 40, 0.002, True, None),    # E8 GEMM
+    ("e8_lattice", 1.6, 3072, 768, 300, 0.002, True, None),   # E8 two-pass (from 64 tokens)
+    ("e8_lattice", 1.6, 1024, 512, 260, 0.002, False, 64),    # E8 two-pass with S_group
+    ("e8_d4", 1.75, 1024, 1024, 2048, 0.002, True, 128),      # E8-D4 two-pass with S_group and bias
 ])
 def test_module_prefill(kind, r, out, inp, T, p, bias, qb):
     print(f"module prefill {kind} {out}x{inp} T={T} p={p} bias={bias} qb={qb}", flush=True)
