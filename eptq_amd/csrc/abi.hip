@@ -449,20 +449,43 @@ int eptq_llama_linear(int n_layers, const eptq_layer* layers, const void* codes,
   return check_launch(fn);
 }
 
-int eptq_f16_gemm(const void* W, const void* x, const void* bias, int F, int N, int T, void* y, int ldy,
-                  void* stream) {
+int eptq_f16_gemm_rows(const void* W, const void* x, const void* bias, int F, int N, int T, const void* row_scale,
+                       void* y, int y_dtype, int ldy, void* stream) {
   const char* fn = "eptq_f16_gemm";
   if (F <= 0 || N <= 0 || T < 0 || ldy < F) return fail(EPTQ_EINVAL, "%s: F=%d N=%d T=%d ldy=%d", fn, F, N, T, ldy);
+  if (y_dtype != EPTQ_F16 && y_dtype != EPTQ_BF16) return fail(EPTQ_EINVAL, "%s: y_dtype=%d", fn, y_dtype);
   if (T == 0) return EPTQ_OK;
   if (!W || !x || !y) return fail(EPTQ_EINVAL, "%s: null W/x/y", fn);
+  if (row_scale && ((uintptr_t)row_scale & 3) != 0) return fail(EPTQ_EUNSUPPORTED, "%s: row_scale alignment", fn);
   // y's extent ends at its last row's F columns: y may be a column slice of
   // a wider output, allocated right before x or W.
   const size_t y_bytes = ((size_t)(T - 1) * ldy + F) * 2;
-  if (ranges_overlap(y, y_bytes, x, (size_t)T * N * 2) || ranges_overlap(y, y_bytes, W, (size_t)F * N * 2))
-    return fail(EPTQ_EINVAL, "%s: y overlaps x or W", fn);
+  if (ranges_overlap(y, y_bytes, x, (size_t)T * N * 2) || ranges_overlap(y, y_bytes, W, (size_t)F * N * 2) ||
+      ranges_overlap(y, y_bytes, row_scale, (size_t)T * 4))
+    return fail(EPTQ_EINVAL, "%s: y overlaps x, W or row_scale", fn);
   if (eptq::launch_gemm_f16w((const uint16_t*)W, (const uint16_t*)x, (const eptq::f16*)bias, F, N, T, N, (uint16_t*)y,
-                             ldy, (hipStream_t)stream) != 0)
+                             ldy, (hipStream_t)stream, (const float*)row_scale, y_dtype == EPTQ_BF16) != 0)
     return fail(EPTQ_EUNSUPPORTED, "%s: F=%d N=%d ldy=%d (multiples of 64, 64, 4) or alignment", fn, F, N, ldy);
+  return check_launch(fn);
+}
+
+int eptq_f16_gemm(const void* W, const void* x, const void* bias, int F, int N, int T, void* y, int ldy,
+                  void* stream) {
+  return eptq_f16_gemm_rows(W, x, bias, F, N, T, nullptr, y, EPTQ_F16, ldy, stream);
+}
+
+int eptq_bf16_rows_to_f16(const void* x, int N, int T, void* x16, void* row_scale, void* stream) {
+  const char* fn = "eptq_bf16_rows_to_f16";
+  if (N <= 0 || T < 0) return fail(EPTQ_EINVAL, "%s: N=%d T=%d", fn, N, T);
+  if (T == 0) return EPTQ_OK;
+  if (!x || !x16 || !row_scale) return fail(EPTQ_EINVAL, "%s: null x/x16/row_scale", fn);
+  if (ranges_overlap(x16, (size_t)T * N * 2, x, (size_t)T * N * 2) ||
+      ranges_overlap(row_scale, (size_t)T * 4, x, (size_t)T * N * 2) ||
+      ranges_overlap(row_scale, (size_t)T * 4, x16, (size_t)T * N * 2))
+    return fail(EPTQ_EINVAL, "%s: x, x16 and row_scale must not overlap", fn);
+  if (eptq::launch_bf16_rows_to_f16((const uint16_t*)x, N, T, (uint16_t*)x16, (float*)row_scale,
+                                    (hipStream_t)stream) != 0)
+    return fail(EPTQ_EUNSUPPORTED, "%s: N=%d (a multiple of 8 up to 16384) or alignment", fn, N);
   return check_launch(fn);
 }
 

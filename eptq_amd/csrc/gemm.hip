@@ -1007,6 +1007,20 @@ __global__ __launch_bounds__(64 * (8 + NPW), (8 + NPW) / 4) void k_gemm_lds_e8d4
   }
 }
 
+// Four outputs of one token: y = acc · sc + bias, rounded to fp16 or (ybf)
+// bf16; sc is the token's power-of-two activation scale (1 for fp16 x).
+__device__ __forceinline__ void store_out(uint16_t* p, const f32x4& acc, float sc, const f16x4& b4, int ybf) {
+  uint32_t w[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const float v0 = acc[2 * h] * sc + (float)b4[2 * h], v1 = acc[2 * h + 1] * sc + (float)b4[2 * h + 1];
+    const uint32_t lo = ybf ? Act<bf16>::from_f32(v0) : Act<f16>::from_f32(v0);
+    const uint32_t hi = ybf ? Act<bf16>::from_f32(v1) : Act<f16>::from_f32(v1);
+    w[h] = lo | (hi << 16);
+  }
+  *(u32x2*)p = (u32x2){w[0], w[1]};
+}
+
 // Prefill GEMM over weights already dequantized: y = x·Wᵀ + bias for fp16 W
 // (F × N, row-major, F = out_features) and x (T × N).  The tiles and MFMA
 // waves of k_gemm_lds_e8d4 (BF features × 256 tokens, 64-column K-steps, two
@@ -1019,7 +1033,7 @@ __global__ __launch_bounds__(64 * (8 + NPW), (8 + NPW) / 4) void k_gemm_lds_e8d4
 template <int BF, int NPW, int NS, int GT = 4>
 __global__ __launch_bounds__(64 * (8 + NPW), (8 + NPW) / 4) void k_gemm_f16w(
     const uint16_t* __restrict__ W, const uint16_t* __restrict__ x, const f16* __restrict__ bias, int N, int T,
-    int ldx, uint16_t* __restrict__ y, int ldy, int OB, int F) {
+    int ldx, uint16_t* __restrict__ y, int ldy, int OB, int F, const float* __restrict__ rs, int ybf) {
   constexpr int kBK = g3::kBK, kBT = g3::kBT;
   constexpr int XS = kBT * 128, WS = BF * 128, W0 = NS * XS;
   static_assert(NS == 2 || NS == 3, "stages");
@@ -1147,10 +1161,7 @@ __global__ __launch_bounds__(64 * (8 + NPW), (8 + NPW) / 4) void k_gemm_f16w(
     for (int q = 0; q < TB; ++q) {
       const int tt = t0 + wt * TW + 16 * q + i;
       if (tt >= T) continue;
-      f16x4 o;
-#pragma unroll
-      for (int v = 0; v < 4; ++v) o[v] = (f16)(acc[xx][q][v] + (float)b4[v]);
-      *(f16x4*)(y + (size_t)tt * ldy + f) = o;
+      store_out(y + (size_t)tt * ldy + f, acc[xx][q], rs ? rs[tt] : 1.0f, b4, ybf);
     }
   }
 }
@@ -1168,7 +1179,7 @@ __global__ __launch_bounds__(64 * (8 + NPW), (8 + NPW) / 4) void k_gemm_f16w(
 template <int BF, int BT, int GT = 4>
 __global__ __launch_bounds__(512, 2) void k_gemm_f16w4(
     const uint16_t* __restrict__ W, const uint16_t* __restrict__ x, const f16* __restrict__ bias, int N, int T,
-    int ldx, uint16_t* __restrict__ y, int ldy, int OB, int F) {
+    int ldx, uint16_t* __restrict__ y, int ldy, int OB, int F, const float* __restrict__ rs, int ybf) {
   constexpr int kBK = g3::kBK, kBT = BT, NS = 3, NPW = 4;
   constexpr int XS = kBT * 128, WS = BF * 128, W0 = NS * XS;
   constexpr int FW = BF / 2, FA = FW / 16, TW = kBT / 2, TB = TW / 16;
@@ -1320,10 +1331,7 @@ __global__ __launch_bounds__(512, 2) void k_gemm_f16w4(
     for (int q = 0; q < TB; ++q) {
       const int tt = t0 + wt * TW + 16 * q + i;
       if (tt >= T) continue;
-      f16x4 o;
-#pragma unroll
-      for (int v = 0; v < 4; ++v) o[v] = (f16)(acc[xx][q][v] + (float)b4[v]);
-      *(f16x4*)(y + (size_t)tt * ldy + f) = o;
+      store_out(y + (size_t)tt * ldy + f, acc[xx][q], rs ? rs[tt] : 1.0f, b4, ybf);
     }
   }
 }
@@ -1550,7 +1558,7 @@ int launch_gemm(const LinearArgs& a, hipStream_t s, void* work, long long work_b
 // Returns 0 if launched, -1 if the shape is outside k_gemm_f16w: F a
 // multiple of 64, N of 64, x rows 16-byte aligned, y rows 8-byte aligned.
 int launch_gemm_f16w(const uint16_t* W, const uint16_t* x, const f16* bias, int F, int N, int T, int ldx,
-                     uint16_t* y, int ldy, hipStream_t s) {
+                     uint16_t* y, int ldy, hipStream_t s, const float* rs, int ybf) {
   if (T <= 0 || F % 64 != 0 || N % g3::kBK != 0 || ldx % 8 != 0 || ((uintptr_t)x & 15) != 0 || ldy % 4 != 0 ||
       ((uintptr_t)y & 7) != 0 || ((uintptr_t)W & 15) != 0 || (bias && ((uintptr_t)bias & 7) != 0))
     return -1;
@@ -1583,7 +1591,7 @@ int launch_gemm_f16w(const uint16_t* W, const uint16_t* x, const f16* bias, int 
     static bool attr[4] = {false, false, false, false};
     if (!attr[v]) attr[v] = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, bytes) == hipSuccess;
     if (!attr[v]) return -1;
-    kern<<<(unsigned)grid, threads, bytes, s>>>(W, x, bias, N, T, ldx, y, ldy, OB, F);
+    kern<<<(unsigned)grid, threads, bytes, s>>>(W, x, bias, N, T, ldx, y, ldy, OB, F, rs, ybf);
     return 0;
   };
   // Three stages where they fit the CU's 160 KB of LDS (all but 256 x 256).
@@ -1595,6 +1603,70 @@ int launch_gemm_f16w(const uint16_t* W, const uint16_t* x, const f16* bias, int 
     case 2: return run(k_gemm_f16w4<128, 256>, 512, 3 * (256 + 128) * 128, 2);
     default: return run(k_gemm_f16w4<64, 256>, 512, 3 * (256 + 64) * 128, 3);
   }
+}
+
+// bf16 activations for the W-streaming GEMM: row t of x becomes
+// x16[t] = fp16(x[t] · 2^-e_t) with e_t = floor(log2 max_n |x[t][n]|) - 14,
+// so the row's largest magnitude lands in [2^14, 2^15): exact for every
+// element that stays in fp16's normal range (bf16 carries 8 significand
+// bits, fp16 11), i.e. all but those below 2^-28 of the row's maximum.
+// rs[t] = 2^e_t restores the scale at the GEMM's output.  One 256-thread
+// workgroup per row, the row in registers (N <= 256 · 8 · kRowChunks).
+constexpr int kRowChunks = 8;
+__global__ __launch_bounds__(256) void k_bf16_rows_to_f16(const uint16_t* __restrict__ x, int N,
+                                                          uint16_t* __restrict__ x16, float* __restrict__ rs) {
+  __shared__ float wm[4];
+  const int t = blockIdx.x, tid = threadIdx.x;
+  const int nch = N / 8;
+  const uint16_t* xr = x + (size_t)t * N;
+  u32x4 v[kRowChunks];
+  float mx = 0.0f;
+#pragma unroll
+  for (int k = 0; k < kRowChunks; ++k) {
+    const int c = tid + 256 * k;
+    v[k] = c < nch ? *(const u32x4*)(xr + 8 * c) : (u32x4){0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      mx = fmaxf(mx, fabsf(__builtin_bit_cast(float, v[k][d] << 16)));
+      mx = fmaxf(mx, fabsf(__builtin_bit_cast(float, v[k][d] & 0xffff0000u)));
+    }
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+  if ((tid & 63) == 0) wm[tid >> 6] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(wm[0], wm[1]), fmaxf(wm[2], wm[3]));
+  // floor(log2 mx) from the exponent bits (mx is a bf16 value widened, so
+  // normal or zero; a subnormal or zero row keeps e = -100, harmless).
+  int e = (int)((__builtin_bit_cast(uint32_t, mx) >> 23) & 0xff) - 127 - 14;
+  if (mx == 0.0f || e < -100) e = -100;
+  if (mx != mx || e > 100) e = 100;   // inf / NaN rows: their non-finite values stay non-finite
+  const float down = __builtin_ldexpf(1.0f, -e);
+  uint16_t* orow = x16 + (size_t)t * N;
+#pragma unroll
+  for (int k = 0; k < kRowChunks; ++k) {
+    const int c = tid + 256 * k;
+    if (c >= nch) continue;
+    u32x4 w;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      const float a = __builtin_bit_cast(float, v[k][d] << 16) * down;
+      const float b = __builtin_bit_cast(float, v[k][d] & 0xffff0000u) * down;
+      w[d] = __builtin_bit_cast(uint32_t, (f16x2){(f16)a, (f16)b});
+    }
+    *(u32x4*)(orow + 8 * c) = w;
+  }
+  if (tid == 0) rs[t] = __builtin_ldexpf(1.0f, e);
+}
+
+// Returns 0 if launched, -1 outside the kernel's range (N a multiple of 8 up
+// to 16384, 16-byte aligned rows).
+int launch_bf16_rows_to_f16(const uint16_t* x, int N, int T, uint16_t* x16, float* rs, hipStream_t s) {
+  if (T <= 0 || N <= 0 || N % 8 != 0 || N > 256 * 8 * kRowChunks || ((uintptr_t)x & 15) != 0 ||
+      ((uintptr_t)x16 & 15) != 0 || ((uintptr_t)rs & 3) != 0)
+    return -1;
+  k_bf16_rows_to_f16<<<(unsigned)T, 256, 0, s>>>(x, N, x16, rs);
+  return 0;
 }
 
 template int launch_gemm<KIND_E8D4>(const LinearArgs&, hipStream_t, void*, long long);

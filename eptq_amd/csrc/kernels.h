@@ -112,10 +112,13 @@ constexpr int kSplitCounters = 16384;
 constexpr size_t kSplitCounterBytes = (size_t)kSplitCounters * 4;
 constexpr size_t kSplitPartBytes = (16 * 64 + 16) * 4;
 constexpr int kSplitTileRows = 64;
-// Prefill GEMM over dequantized fp16 weights: y (T, F) = x (T, N) · Wᵀ + bias
-// for W (F, N) row-major; -1 when the shape is outside the kernel.
+// Prefill GEMM over dequantized fp16 weights: y (T, F) = rs[t] · (x (T, N) ·
+// Wᵀ) + bias for W (F, N) row-major, rs NULL for 1, y fp16 or (ybf) bf16;
+// -1 when the shape is outside the kernel.
 int launch_gemm_f16w(const uint16_t* W, const uint16_t* x, const f16* bias, int F, int N, int T, int ldx,
-                     uint16_t* y, int ldy, hipStream_t s);
+                     uint16_t* y, int ldy, hipStream_t s, const float* rs = nullptr, int ybf = 0);
+// bf16 rows to fp16 for it: x16[t] = fp16(x[t] · 2^-e_t), rs[t] = 2^e_t.
+int launch_bf16_rows_to_f16(const uint16_t* x, int N, int T, uint16_t* x16, float* rs, hipStream_t s);
 // Workspace bytes that let the matrix-core decode split every launch it takes.
 long long decode_mfma_work_bytes();
 namespace dec { int mfma_min_batch_init(); }

@@ -196,7 +196,8 @@ def _two_pass_min(kind: str, layers) -> int:
 
 
 def _two_pass_ok(layers, x, N) -> bool:
-    return (x.dtype == torch.float16 and N % 64 == 0
+    # bf16 x goes through eptq_bf16_rows_to_f16 (rows up to 16384 columns).
+    return ((x.dtype == torch.float16 or (x.dtype == torch.bfloat16 and N <= 16384)) and N % 64 == 0
             and all((8 * int(L["Q"].shape[0])) % 64 == 0 for L in layers))
 
 
@@ -204,9 +205,11 @@ def _two_pass_into(lib, layers, codes, x, y, kind: str = "e8_d4") -> None:
     """y[:, layer columns] = x · W_lᵀ + bias_l with each layer's W decoded once
     (``eptq_e8d4_dequant`` / ``eptq_e8_dequant``, S_group included, into one
     transient buffer sized for the largest layer, reused layer after layer on
-    the stream) and multiplied by ``eptq_f16_gemm``.  The table is the
+    the stream) and multiplied by ``eptq_f16_gemm_rows``.  The table is the
     kernels' (fp16, widened to fp32): the same table values the fused kernel
-    multiplies."""
+    multiplies.  bf16 x is first taken to fp16 row by row with a power-of-two
+    scale (``eptq_bf16_rows_to_f16``) that the GEMM restores at its bf16
+    output."""
     N = int(x.shape[1])
     B, ldy = int(x.shape[0]), int(y.shape[1])
     tab = codes if codes.dtype == torch.float32 else codes.float()
@@ -216,6 +219,12 @@ def _two_pass_into(lib, layers, codes, x, y, kind: str = "e8_d4") -> None:
     off = 0
     with torch.cuda.device(x.device):
         stream = torch.cuda.current_stream().cuda_stream
+        xg, rs = x, None
+        if x.dtype == torch.bfloat16:
+            xg = torch.empty((B, N), dtype=torch.float16, device=x.device)
+            rs = torch.empty(B, dtype=torch.float32, device=x.device)
+            _lib.check(lib.eptq_bf16_rows_to_f16(_ptr(x), N, B, _ptr(xg), _ptr(rs), stream), "eptq_bf16_rows_to_f16")
+        y_dtype = EPTQ_BF16 if y.dtype == torch.bfloat16 else EPTQ_F16
         for L in layers:
             M = int(L["Q"].shape[0])
             S = L.get("S_group")
@@ -223,9 +232,9 @@ def _two_pass_into(lib, layers, codes, x, y, kind: str = "e8_d4") -> None:
             rc = deq(_ptr(L["Q"]), _ptr(tab), _ptr(L["g"]), _ptr(L["h"]), _ptr(L["O_vals"]), _ptr(L["O_col"]),
                      _ptr(L["O_row_ptr"]), _ptr(S), n_groups, M, N, _ptr(wbuf), stream)
             _lib.check(rc, deq.__name__)
-            rc = lib.eptq_f16_gemm(_ptr(wbuf), _ptr(x), _ptr(L.get("bias")), 8 * M, N, B,
-                                   _ptr(y) + 2 * off, ldy, stream)
-            _lib.check(rc, "eptq_f16_gemm")
+            rc = lib.eptq_f16_gemm_rows(_ptr(wbuf), _ptr(xg), _ptr(L.get("bias")), 8 * M, N, B, _ptr(rs),
+                                        _ptr(y) + 2 * off, y_dtype, ldy, stream)
+            _lib.check(rc, "eptq_f16_gemm_rows")
             off += 8 * M
 
 

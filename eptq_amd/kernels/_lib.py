@@ -29,6 +29,8 @@ SIGNATURES = {
     "eptq_e8d4_dequant": ([_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _P, _P], _I),
     "eptq_e8_dequant": ([_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _P, _P], _I),
     "eptq_f16_gemm": ([_P, _P, _P, _I, _I, _I, _P, _I, _P], _I),
+    "eptq_f16_gemm_rows": ([_P, _P, _P, _I, _I, _I, _P, _P, _I, _I, _P], _I),
+    "eptq_bf16_rows_to_f16": ([_P, _I, _I, _P, _P, _P], _I),
 }
 
 class EptqLayer(ctypes.Structure):

@@ -174,6 +174,27 @@ int eptq_e8d4_dequant(const void* Q, const void* codes_f32,
 int eptq_f16_gemm(const void* W, const void* x, const void* bias, int F, int N, int T,
                   void* y, int ldy, void* stream);
 
+/*
+ * eptq_f16_gemm with a per-token scale and a choice of output type:
+ * y[t] = row_scale[t] · (x[t] · Wᵀ) + bias, rounded to fp16 (y_dtype
+ * EPTQ_F16) or bf16 (EPTQ_BF16); row_scale NULL (1) or T fp32 values, 4-byte
+ * aligned.  With eptq_bf16_rows_to_f16 below it is the two-pass prefill for
+ * bf16 activations.  No counterpart in the reference (as eptq_f16_gemm).
+ */
+int eptq_f16_gemm_rows(const void* W, const void* x, const void* bias, int F, int N, int T,
+                       const void* row_scale, void* y, int y_dtype, int ldy, void* stream);
+
+/*
+ * bf16 activations x (T, N) to the fp16 operand of eptq_f16_gemm_rows:
+ * x16[t] = fp16(x[t] · 2^-e_t), row_scale[t] = 2^e_t (fp32), e_t chosen so
+ * the row's largest magnitude lands in [2^14, 2^15) — exact for every element
+ * within 2^-28 of the row's maximum (bf16 has 8 significand bits, fp16 11).
+ * N a multiple of 8 up to 16384, x and x16 16-byte aligned, no overlap;
+ * EPTQ_EUNSUPPORTED / EPTQ_EINVAL otherwise.  No counterpart in the
+ * reference; the caller owns x16 (T·N·2 bytes) and row_scale (T·4 bytes).
+ */
+int eptq_bf16_rows_to_f16(const void* x, int N, int T, void* x16, void* row_scale, void* stream);
+
 int eptq_e8_dequant(const void* Q, const void* codes_f32,
                     const void* g, const void* h,
                     const void* O_vals, const void* O_col, const void* O_row_ptr,

@@ -115,6 +115,20 @@ def test_f16_gemm_rejects_invalid_arguments(lib):
     assert f(W, y + ((T - 1) * ldy + F) * 2 - 2, None, F, 64, T, y, ldy, None) == _lib.EPTQ_EINVAL
 
 
+def test_bf16_two_pass_entry_points_reject_invalid_arguments(lib):
+    g, r = lib.eptq_f16_gemm_rows, lib.eptq_bf16_rows_to_f16
+    W, x, y, rs = 1 << 20, 1 << 24, 1 << 28, 1 << 30
+    assert g(W, x, None, 128, 64, 4, rs, y, _lib.EPTQ_F32, 128, None) == _lib.EPTQ_EINVAL   # y fp16 or bf16 only
+    assert "y_dtype" in lib.eptq_last_error().decode()
+    assert g(W, x, None, 128, 64, 4, rs + 2, y, _lib.EPTQ_BF16, 128, None) == _lib.EPTQ_EUNSUPPORTED
+    assert g(W, x, None, 128, 64, 4, y + 64, y, _lib.EPTQ_BF16, 128, None) == _lib.EPTQ_EINVAL  # row_scale inside y
+    assert r(x, 4096, 0, y, rs, None) == _lib.EPTQ_OK                                            # no rows: no-op
+    assert r(None, 4096, 4, y, rs, None) == _lib.EPTQ_EINVAL
+    assert r(x, 4096, 4, x + 16, rs, None) == _lib.EPTQ_EINVAL                                   # x16 overlaps x
+    assert r(x, 4100, 4, y, rs, None) == _lib.EPTQ_EUNSUPPORTED                                  # N % 8
+    assert r(x, 16392, 4, y, rs, None) == _lib.EPTQ_EUNSUPPORTED                                 # N > 16384
+
+
 def test_python_wrapper_raises_on_error_codes(lib):
     with pytest.raises(_lib.EptqError, match="eptq_e8d4_forward"):
         _lib.check(lib.eptq_e8d4_forward(*_fwd_args(Q=None)), "eptq_e8d4_forward")

@@ -63,6 +63,58 @@ def test_two_pass_prefill_vs_oracle():
     assert np.isfinite(y).all() and e <= 1e-2
 
 
+def test_bf16_rows_to_f16_exact():
+    """Rows of very different magnitudes: x16 · row_scale gives back x exactly,
+    row_scale is a power of two, and each row's largest |x16| is in
+    [2^14, 2^15)."""
+    T, N = 9, 4096
+    gen = torch.Generator("cuda").manual_seed(3)
+    base = torch.randn((T, N), generator=gen, device="cuda")
+    mags = torch.tensor([2.0 ** k for k in (-60, -30, -10, -1, 0, 3, 12, 40, 90)], device="cuda")
+    x = (base * mags[:, None]).bfloat16()
+    x[4, 17] = 0.0
+    x16 = torch.empty((T, N), dtype=torch.float16, device="cuda")
+    rs = torch.empty(T, dtype=torch.float32, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+    _lib.check(_lib.load().eptq_bf16_rows_to_f16(x.data_ptr(), N, T, x16.data_ptr(), rs.data_ptr(), stream),
+               "eptq_bf16_rows_to_f16")
+    torch.cuda.synchronize()
+    back = x16.double() * rs.double()[:, None]
+    xd = x.double()
+    # Elements above 2^-28 of their row's maximum come back exactly.
+    keep = xd.abs() >= xd.abs().amax(dim=1, keepdim=True) * 2.0 ** -28
+    assert torch.equal(back[keep], xd[keep])
+    assert torch.all(torch.log2(rs.double()) == torch.round(torch.log2(rs.double())))
+    top = x16.double().abs().amax(dim=1)
+    assert torch.all(top >= 2.0 ** 14) and torch.all(top < 2.0 ** 15)
+
+
+@pytest.mark.parametrize("F,N,T", [(5120, 512, 2000), (1024, 2048, 300)])
+def test_f16_gemm_rows_bf16(F, N, T):
+    """bf16 x through the row conversion, then the row-scaled GEMM with bf16
+    output, against torch's fp32 matmul: within 5e-3 relative L2 (bf16
+    output rounding), rows of different magnitudes."""
+    print(f"eptq_f16_gemm_rows bf16 F={F} N={N} T={T}", flush=True)
+    gen = torch.Generator("cuda").manual_seed(F + T)
+    W = (torch.randn((F, N), generator=gen, device="cuda") * 0.05).half()
+    scale = 2.0 ** torch.randint(-20, 20, (T, 1), generator=gen, device="cuda").float()
+    x = (torch.randn((T, N), generator=gen, device="cuda") * scale).bfloat16()
+    b = torch.randn(F, generator=gen, device="cuda").half()
+    lib, stream = _lib.load(), torch.cuda.current_stream().cuda_stream
+    x16 = torch.empty((T, N), dtype=torch.float16, device="cuda")
+    rs = torch.empty(T, dtype=torch.float32, device="cuda")
+    _lib.check(lib.eptq_bf16_rows_to_f16(x.data_ptr(), N, T, x16.data_ptr(), rs.data_ptr(), stream),
+               "eptq_bf16_rows_to_f16")
+    y = torch.empty((T, F), dtype=torch.bfloat16, device="cuda")
+    _lib.check(lib.eptq_f16_gemm_rows(W.data_ptr(), x16.data_ptr(), b.data_ptr(), F, N, T, rs.data_ptr(),
+                                      y.data_ptr(), _lib.EPTQ_BF16, F, stream), "eptq_f16_gemm_rows")
+    want = x.float() @ W.float().t() + b.float()
+    # Per row (magnitudes differ by 2^40 across rows).
+    err = ((y.float() - want).norm(dim=1) / want.norm(dim=1)).max().item()
+    print(f"  max row rel_l2 {err:.2e}", flush=True)
+    assert torch.isfinite(y.float()).all() and err <= 5e-3
+
+
 def test_f16_gemm_unsupported():
     W = torch.zeros((100, 256), dtype=torch.float16, device="cuda")
     x = torch.zeros((8, 256), dtype=torch.float16, device="cuda")

@@ -125,6 +125,7 @@ def test_module_prefill_bf16_and_row_consistency():
     (1024, 2048, 129, torch.float16),     # first row past the 16-row slices
     (1280, 2048, 257, torch.float16),     # a 256-token tile plus one row
     (1024, 2048, 100, torch.bfloat16),    # bf16 at mid counts (no matrix-core slices)
+    (1024, 2048, 2048, torch.bfloat16),   # bf16 two-pass (rows to fp16 with a power-of-two scale)
     (1024, 2080, 200, torch.float16),     # in_features an odd multiple of 32
     (512, 1000, 150, torch.float16),      # in_features not a multiple of 32
     (1024, 2048, 0, torch.float16),       # empty batch
