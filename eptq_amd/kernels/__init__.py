@@ -79,8 +79,8 @@ def _check_layer(kind, Q, codes, g, h, O_vals, O_col, O_row_ptr, S_group):
 def linear_forward(kind: str, Q, codes, g, h, x, O_vals, O_col, O_row_ptr, bias=None,
                    S_group=None, two_pass: bool = False) -> torch.Tensor:
     """Run the fused quantized Linear on ``x`` (B, N) -> (B, 8M), dtype of x.
-    ``two_pass`` (what the module's ops pass): from ``_two_pass_min`` fp16
-    tokens (2048 for E8-D4, 256 with S_group, 64 for E8) and 64-multiple
+    ``two_pass`` (what the module's ops pass): from ``_two_pass_min`` tokens
+    (2048 for E8-D4, 256 with S_group or bf16 x, 64 for E8) and 64-multiple
     shapes, the two-pass prefill instead of the fused C-ABI kernel."""
     M, N, n_groups = _check_layer(kind, Q, codes, g, h, O_vals, O_col, O_row_ptr, S_group)
     _require(x.device == Q.device, "x must be on the layer's device")
@@ -96,7 +96,7 @@ def linear_forward(kind: str, Q, codes, g, h, x, O_vals, O_col, O_row_ptr, bias=
         return y
     lib = _lib.load()
     layer = dict(Q=Q, g=g, h=h, O_vals=O_vals, O_col=O_col, O_row_ptr=O_row_ptr, bias=bias, S_group=S_group)
-    if two_pass and B >= _two_pass_min(kind, [layer]) and _two_pass_ok([layer], x, N):
+    if two_pass and B >= _two_pass_min(kind, [layer], x) and _two_pass_ok([layer], x, N):
         _two_pass_into(lib, [layer], codes, x, y, kind)
         return y
     fn = lib.eptq_e8d4_forward if kind == "e8_d4" else lib.eptq_e8_forward
@@ -183,15 +183,20 @@ def _workspace_outside_graph_pools(device, stream) -> torch.Tensor:
 # (whose fused path is the older grouped GEMM): 1.2-1.8x from 256 tokens on
 # 4096x4096, 11008x4096 and 4096x11008.  E8 (whose fused GEMM gathers from a
 # 1 MB table): 2x from 64 tokens on 4096x4096, 1.3-2.5x at 256-2048 tokens on
-# 4096x4096 and 11008x4096, level on 3072x768.
+# 4096x4096 and 11008x4096, level on 3072x768.  E8-D4 with bf16 x (whose
+# fused path decodes into registers): 1.2-2.1x from 256 tokens on 4096x4096,
+# 11008x4096, 4096x11008 and 14336x4096.
 TWO_PASS_MIN_TOKENS = 2048
 TWO_PASS_MIN_TOKENS_GROUPED = 256
+TWO_PASS_MIN_TOKENS_BF16 = 256
 TWO_PASS_MIN_TOKENS_E8 = 64
 
 
-def _two_pass_min(kind: str, layers) -> int:
+def _two_pass_min(kind: str, layers, x) -> int:
     if kind != "e8_d4":
         return TWO_PASS_MIN_TOKENS_E8
+    if x.dtype == torch.bfloat16:
+        return TWO_PASS_MIN_TOKENS_BF16
     return TWO_PASS_MIN_TOKENS_GROUPED if all(L.get("S_group") is not None for L in layers) else TWO_PASS_MIN_TOKENS
 
 
@@ -271,7 +276,7 @@ def linear_forward_multi(layers, codes, x, work: Optional[torch.Tensor] = None,
     if B == 0:
         return y
     lib = _lib.load()
-    if two_pass and B >= _two_pass_min("e8_d4", keep) and _two_pass_ok(keep, x, N):
+    if two_pass and B >= _two_pass_min("e8_d4", keep, x) and _two_pass_ok(keep, x, N):
         _two_pass_into(lib, keep, codes, x, y)
         return y
     with torch.cuda.device(x.device):

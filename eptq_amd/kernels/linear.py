@@ -18,7 +18,7 @@ Differences, all towards the reference's own reconstruct semantics:
   matvec for ≤16 rows, 16-row slices of the matrix-core decode up to 128 rows,
   the prefill GEMM that decodes weight tiles into LDS above (the reference's
   ``csrc/eptq_kernels.cu:520-537`` route), and from 2048 fp16 tokens (256
-  for S_group layers, 64 for E8 layers) the two-pass prefill: each weight
+  for S_group layers or bf16 x, 64 for E8 layers) the two-pass prefill: each weight
   decoded once into a transient fp16 W (freed on return), then this
   library's W-streaming GEMM.  No library GEMM runs.  ``EPTQ_CUDA_DECODE`` / ``EPTQ_FORCE_TRITON`` are
   accepted and ignored.

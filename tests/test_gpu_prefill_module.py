@@ -5,8 +5,8 @@ library's own kernels — 16-row slices of the matrix-core decode up to 128
 rows, the prefill GEMMs that decode weight tiles into LDS or registers above
 (the reference's module does the same with its fused GEMM,
 ``kernels/linear.py:199-210`` → ``csrc/eptq_kernels.cu:520-537``), and from
-2048 fp16 tokens (256 for E8-D4 layers with S_group, 64 for E8 layers) the
-two-pass prefill (``eptq_e8d4_dequant`` / ``eptq_e8_dequant`` into a
+2048 fp16 tokens (256 for E8-D4 layers with S_group or bf16 x, 64 for E8
+layers) the two-pass prefill (``eptq_e8d4_dequant`` / ``eptq_e8_dequant`` into a
 transient fp16 W, then ``eptq_f16_gemm``).  Checks:
 
 * within 1e-2 relative L2 of the fp32 reconstruct + matmul oracle (the
