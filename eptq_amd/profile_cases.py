@@ -8,6 +8,8 @@ dozen dispatches each, no graph capture.
     python -m eptq_amd.profile_cases decode --shape 4096x4096 --batch 1 --copies 8
     python -m eptq_amd.profile_cases prefill --shape 5120x5120 --tokens 2048
     python -m eptq_amd.profile_cases prefill --shape 4096x11008 --tokens 512 --work
+    python -m eptq_amd.profile_cases prefill --shape 4096x4096 --tokens 2048 --bf16 --two-pass
+    python -m eptq_amd.profile_cases e8 --shape 4096x4096 --batch 2048 --two-pass
     python -m eptq_amd.profile_cases e8 --shape 3072x768 --copies 8
     python -m eptq_amd.profile_cases step --layers 4
     python -m eptq_amd.profile_cases module --tokens 2048
@@ -42,6 +44,8 @@ def main(argv=None) -> None:
     ap.add_argument("--bf16", action="store_true", help="bf16 activations (cases decode, prefill)")
     ap.add_argument("--work", action="store_true",
                     help="through the multi-layer entry point with a decode workspace (split K; cases decode, prefill)")
+    ap.add_argument("--two-pass", action="store_true",
+                    help="the module's route (two passes from its token thresholds; cases prefill, e8)")
     args = ap.parse_args(argv)
 
     import torch
@@ -68,7 +72,7 @@ def main(argv=None) -> None:
                     linear_forward_multi([L], codes, x, work=work)
                 else:
                     linear_forward("e8_d4", L["Q"], codes, L["g"], L["h"], x, L["O_vals"], L["O_col"],
-                                   L["O_row_ptr"], None, L["S_group"])
+                                   L["O_row_ptr"], None, L["S_group"], two_pass=args.two_pass)
     elif args.case == "e8":
         codes = E8LatticeQuantizer(radius=1.6).flat_table().half().to(dev)
         layers = [_layer(torch, out, inp, 7100 + c, 0.002, dev, bias=True) for c in range(args.copies)]
@@ -77,7 +81,7 @@ def main(argv=None) -> None:
         for _ in range(args.reps):
             for L in layers:
                 linear_forward("e8_lattice", L["Q"], codes, L["g"], L["h"], x, L["O_vals"], L["O_col"],
-                               L["O_row_ptr"], L["bias"], None)
+                               L["O_row_ptr"], L["bias"], None, two_pass=args.two_pass)
     elif args.case == "module":
         # One Llama-2-13B decoder layer's Linears through the drop-in modules
         # (EPTQMultiLinear q|k|v and gate|up, EPTQLinear o and down) at
