@@ -1167,15 +1167,17 @@ __global__ __launch_bounds__(64 * (8 + NPW), (8 + NPW) / 4) void k_gemm_f16w(
 }
 
 // k_gemm_f16w with BF x BT tiles and four matrix-core waves, one per SIMD,
-// each holding a (BF/2) x (BT/2) block of the tile, and their LDS reads a half-step ahead of
-// their MFMAs: the reads for the second half of step j (k 32..63) go out
-// before the MFMAs of the first half, the barrier of step j + 1 sits between
-// the two halves, and the reads of step j + 1's first half go out before the
-// MFMAs of step j's second half.  So the MFMAs never wait for LDS, and the
-// barrier no longer lines every wave's reads up into one burst.  Four
-// producer waves (one per SIMD) bring x and W in by LDS DMA, three stages
-// deep.  Eight waves in all: 256 registers per wave for up to 160 fp32
-// accumulators and two sets of fragments.
+// each holding a (BF/2) x (BT/2) block of the tile, and their LDS reads a
+// half-step ahead of their MFMAs: the reads for the second half of step j
+// (k 32..63) go out column by column among the MFMAs of its first half, the
+// barrier of step j + 1 sits between the two halves, and the reads of step
+// j + 1's first half go out among the MFMAs of step j's second half.  So the
+// MFMAs never wait for LDS, and the barrier no longer lines every wave's
+// reads up into one burst.  Four producer waves (one per SIMD) bring x and W
+// in by LDS DMA, three stages deep.  Eight waves in all: 256 registers per
+// wave for up to 160 fp32 accumulators and two sets of fragments.  The last
+// feature tile may be ragged (rows past F read row F - 1, stores stop at F);
+// the output is rs[t] · acc + bias in fp16 or (ybf) bf16.
 template <int BF, int BT, int GT = 4>
 __global__ __launch_bounds__(512, 2) void k_gemm_f16w4(
     const uint16_t* __restrict__ W, const uint16_t* __restrict__ x, const f16* __restrict__ bias, int N, int T,
