@@ -1023,13 +1023,15 @@ __device__ __forceinline__ void store_out(uint16_t* p, const f32x4& acc, float s
 
 // Prefill GEMM over weights already dequantized: y = x·Wᵀ + bias for fp16 W
 // (F × N, row-major, F = out_features) and x (T × N).  The tiles and MFMA
-// waves of k_gemm_lds_e8d4 (BF features × 256 tokens, 64-column K-steps, two
+// waves of k_gemm_lds_e8d4 (BF features × 256 tokens, 64-column K-steps, NS
 // stages, one barrier per step); the producer waves bring both the x tile and
 // the W tile in by LDS DMA, W in the swizzled layout the decode writes (the
 // swizzle is in the source addresses: LDS DMA writes each lane's 16 bytes at
 // 16·lane of the instruction's kilobyte).  With W from k_dequant this is the
 // two-pass prefill: every weight decoded once, rather than once per 256-token
-// tile as in the fused kernel.
+// tile as in the fused kernel.  The launcher runs it for 256 × 256 tiles
+// only (two stages: three do not fit the LDS), k_gemm_f16w4 below for the
+// rest; F is a multiple of BF here, rs and ybf as in k_gemm_f16w4.
 template <int BF, int NPW, int NS, int GT = 4>
 __global__ __launch_bounds__(64 * (8 + NPW), (8 + NPW) / 4) void k_gemm_f16w(
     const uint16_t* __restrict__ W, const uint16_t* __restrict__ x, const f16* __restrict__ bias, int N, int T,
