@@ -13,6 +13,7 @@ dozen dispatches each, no graph capture.
     python -m eptq_amd.profile_cases e8 --shape 3072x768 --copies 8
     python -m eptq_amd.profile_cases step --layers 4
     python -m eptq_amd.profile_cases module --tokens 2048
+    python -m eptq_amd.profile_cases gemm16 --shape 5120x13824 --tokens 2048
 """
 
 from __future__ import annotations
@@ -33,7 +34,7 @@ def _layer(torch, out, inp, seed, p, dev, qb=None, bias=False):
 
 def main(argv=None) -> None:
     ap = argparse.ArgumentParser()
-    ap.add_argument("case", choices=["decode", "prefill", "e8", "step", "module"])
+    ap.add_argument("case", choices=["decode", "prefill", "e8", "step", "module", "gemm16"])
     ap.add_argument("--shape", default="4096x4096", help="out x in")
     ap.add_argument("--batch", type=int, default=1)
     ap.add_argument("--tokens", type=int, default=2048)
@@ -82,6 +83,16 @@ def main(argv=None) -> None:
             for L in layers:
                 linear_forward("e8_lattice", L["Q"], codes, L["g"], L["h"], x, L["O_vals"], L["O_col"],
                                L["O_row_ptr"], L["bias"], None, two_pass=args.two_pass)
+    elif args.case == "gemm16":
+        # The two-pass prefill's second pass alone (eptq_f16_gemm) on a seeded
+        # fp16 W (out x in) and x (--tokens x in), --reps launches.
+        from eptq_amd.kernels import f16_gemm
+        gen = torch.Generator(device=dev).manual_seed(5)
+        W = (torch.randn((out, inp), generator=gen, device=dev) * 0.05).half()
+        x = torch.randn((args.tokens, inp), generator=gen, device=dev).half()
+        torch.cuda.synchronize()
+        for _ in range(args.reps):
+            f16_gemm(W, x)
     elif args.case == "module":
         # One Llama-2-13B decoder layer's Linears through the drop-in modules
         # (EPTQMultiLinear q|k|v and gate|up, EPTQLinear o and down) at
