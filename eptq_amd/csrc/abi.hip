@@ -410,10 +410,10 @@ int eptq_llama_norm_swiglu(const eptq_layer* gate_up, const void* codes, const v
                       8 * gate_up[0].M, stream, true);
 }
 
-int eptq_llama_linear(int n_layers, const eptq_layer* layers, const void* codes, const void* x, int N, int B,
-                      const void* norm_w, float eps, const void* resid, void* y, int ldy, void* work,
-                      long long work_bytes, void* stream) {
-  const char* fn = "eptq_llama_linear";
+// eptq_llama_linear, and with act (B, 8M of the first layer) its SwiGLU form.
+static int llama_linear(const char* fn, int n_layers, const eptq_layer* layers, const void* codes, const void* x,
+                        int N, int B, const void* norm_w, float eps, const void* resid, void* y, int ldy,
+                        void* work, long long work_bytes, void* stream, void* act) {
   const int n = n_layers;
   if (n < 1 || n > eptq::kMaxLayers || !layers) return fail(EPTQ_EINVAL, "%s: n_layers=%d (1..%d)", fn, n, eptq::kMaxLayers);
   if (B < 0 || B > 16) return fail(B < 0 ? EPTQ_EINVAL : EPTQ_EUNSUPPORTED, "%s: B=%d (0..16)", fn, B);
@@ -443,10 +443,37 @@ int eptq_llama_linear(int n_layers, const eptq_layer* layers, const void* codes,
     a[l].res = resid ? (const uint16_t*)resid + L.y_offset : nullptr;
   }
   if (B == 0) return EPTQ_OK;
-  if (eptq::launch_decode_mfma_multi(a, n, (hipStream_t)stream, work, work ? work_bytes : 0) != 0)
+  if (eptq::launch_decode_mfma_multi(a, n, (hipStream_t)stream, work, work ? work_bytes : 0, (uint16_t*)act) != 0)
     return fail(EPTQ_EUNSUPPORTED, "%s: the matrix-core decode kernel does not take N=%d B=%d%s", fn, N, B,
                 norm_w ? " with the norm" : "");
   return check_launch(fn);
+}
+
+int eptq_llama_linear(int n_layers, const eptq_layer* layers, const void* codes, const void* x, int N, int B,
+                      const void* norm_w, float eps, const void* resid, void* y, int ldy, void* work,
+                      long long work_bytes, void* stream) {
+  return llama_linear("eptq_llama_linear", n_layers, layers, codes, x, N, B, norm_w, eps, resid, y, ldy, work,
+                      work_bytes, stream, nullptr);
+}
+
+int eptq_llama_linear_swiglu(const eptq_layer* gate_up, const void* codes, const void* x, int N, int B,
+                             const void* norm_w, float eps, void* gu, void* out, void* work, long long work_bytes,
+                             void* stream) {
+  const char* fn = "eptq_llama_linear_swiglu";
+  if (!gate_up) return fail(EPTQ_EINVAL, "%s: null layers", fn);
+  if (gate_up[0].M != gate_up[1].M || gate_up[0].M <= 0)
+    return fail(EPTQ_EINVAL, "%s: gate and up need equal M > 0 (%d, %d)", fn, gate_up[0].M, gate_up[1].M);
+  if (!work) return fail(EPTQ_EINVAL, "%s: the SwiGLU form needs a workspace", fn);
+  if (B > 0 && (!gu || !out)) return fail(EPTQ_EINVAL, "%s: null gu/out", fn);
+  if (out && ((uintptr_t)out & 3) != 0) return fail(EPTQ_EUNSUPPORTED, "%s: out must be 4-byte aligned", fn);
+  const int F = 8 * gate_up[0].M;
+  const size_t out_bytes = (size_t)(B > 0 ? B : 0) * F * 2;
+  if (ranges_overlap(out, out_bytes, gu, 2 * out_bytes) || ranges_overlap(out, out_bytes, x, (size_t)(B > 0 ? B : 0) * N * 2))
+    return fail(EPTQ_EINVAL, "%s: out overlaps gu or x", fn);
+  eptq_layer l2[2] = {gate_up[0], gate_up[1]};
+  l2[0].y_offset = 0;
+  l2[1].y_offset = F;
+  return llama_linear(fn, 2, l2, codes, x, N, B, norm_w, eps, nullptr, gu, 2 * F, work, work_bytes, stream, out);
 }
 
 int eptq_f16_gemm_rows(const void* W, const void* x, const void* bias, int F, int N, int T, const void* row_scale,

@@ -137,6 +137,7 @@ int launch_one(const LinearArgs* layers, int n, hipStream_t s, int per_cu, size_
   if (total > cap) total = cap;
   MultiArgs ma;
   ma.n = n;
+  ma.act = nullptr;
   ma.start[0] = 0;
   for (int l = 0; l < kMaxLayers; ++l) {
     if (l < n) {
@@ -228,6 +229,7 @@ int launch_pair_k(const LinearArgs* l, hipStream_t s) {
   const int RG = (l[0].M + L::R - 1) / L::R;
   MultiArgs ma;
   ma.n = 2;
+  ma.act = nullptr;
   ma.l[0] = l[0];
   ma.l[1] = l[1];
   ma.l[2] = ma.l[3] = l[0];

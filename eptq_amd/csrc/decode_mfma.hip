@@ -578,6 +578,7 @@ __global__ __launch_bounds__((S + 1) * 64, 3) void k_decode_mfma(MultiArgs ma, i
     if (tid < 8) sinv[tid] = rsqrtf(ssl / (float)N + a.eps);
     __syncthreads();
   }
+  uint32_t pks[kItems];
   if (fin) {
     const h2 gg = __builtin_bit_cast(h2, gpair), bb = __builtin_bit_cast(h2, bpair);
     const h2 rr = __builtin_bit_cast(h2, rpair);
@@ -594,7 +595,49 @@ __global__ __launch_bounds__((S + 1) * 64, 3) void k_decode_mfma(MultiArgs ma, i
         pk = (uint32_t)Act<XT>::from_f32((float)rr[0] + (float)o[0]) |
              ((uint32_t)Act<XT>::from_f32((float)rr[1] + (float)o[1]) << 16);
       }
-      *gp((uint32_t*)(a.y + (size_t)b * a.ldy + orow)) = pk;
+      uint32_t* yp = (uint32_t*)(a.y + (size_t)b * a.ldy + orow);
+      if (ma.act) __hip_atomic_store(yp, pk, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      else *gp(yp) = pk;
+      pks[it] = pk;
+    }
+  }
+  // SwiGLU (ma.act: layer 0 gate, layer 1 up, up's columns right after
+  // gate's in y): the two workgroups that finish row tile `tile` of the two
+  // layers meet at a counter past the split counters; the second to arrive
+  // reads the other's outputs and writes act = silu(gate) ⊙ up.  Publication
+  // as for the split sums above: agent-scope atomic stores of y, vmcnt(0)
+  // before the barrier that precedes the count, agent-scope atomic loads.
+  if (ma.act && fin) {   // uniform over the workgroup
+    __shared__ int pair_last;
+    __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
+    __syncthreads();
+    if (tid == 0) {
+      int* pc = wcnt + ma.start[2] + tile;
+      const int old = __hip_atomic_fetch_add(pc, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      pair_last = old == 1;
+      if (old == 1) __hip_atomic_store(pc, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (pair_last) {
+      const int F = 8 * M;
+#pragma unroll
+      for (int it = 0; it < kItems; ++it) {
+        if (!ok[it]) continue;
+        const int b = ((tid + NT * it) >> 5) & 15;
+        const uint32_t other = __hip_atomic_load((const uint32_t*)(a.y + (size_t)b * a.ldy + orow + (li == 0 ? F : -F)),
+                                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const h2 gv = __builtin_bit_cast(h2, li == 0 ? pks[it] : other);
+        const h2 uv = __builtin_bit_cast(h2, li == 0 ? other : pks[it]);
+        const float g0 = (float)gv[0], g1 = (float)gv[1];
+        float o0 = g0 / (1.0f + __expf(-g0)) * (float)uv[0];
+        float o1 = g1 / (1.0f + __expf(-g1)) * (float)uv[1];
+        // The fp32 rounding of the product before the fp16 one, as the
+        // separate SwiGLU kernel computes it (the compiler would otherwise
+        // fuse the multiply and the conversion).
+        asm volatile("" : "+v"(o0), "+v"(o1));
+        *gp((uint32_t*)(ma.act + (size_t)b * F + orow)) =
+            (uint32_t)Act<f16>::from_f32(o0) | ((uint32_t)Act<f16>::from_f32(o1) << 16);
+      }
     }
   }
 }
@@ -611,9 +654,11 @@ inline int parts_for(int split, int tiles, void* work, long long work_bytes) {
 }
 
 template <int S, bool HAS_S, typename XT, bool XH, bool NORM = false>
-int launch_t(const LinearArgs* l, int n, hipStream_t s, void* work, long long work_bytes) {
+int launch_t(const LinearArgs* l, int n, hipStream_t s, void* work, long long work_bytes, uint16_t* act) {
   int tiles = 0;
   for (int k = 0; k < n; ++k) tiles += (l[k].M + kTile - 1) / kTile;
+  // SwiGLU pairs: one counter per row tile of a layer, after the tiles' own.
+  if (act && (!work || work_bytes < (long long)kCntBytes || tiles + tiles / 2 > kMaxCounters)) return -1;
   // One workgroup per CU.  Up to one round of tiles: each tile's columns
   // split P ways.  More tiles than CUs: the first round takes whole tiles,
   // and the tiles left for the second round are split so that it is shorter.
@@ -623,6 +668,7 @@ int launch_t(const LinearArgs* l, int n, hipStream_t s, void* work, long long wo
   if (P == 1) T1 = 0;
   MultiArgs ma;
   ma.n = n;
+  ma.act = act;
   ma.start[0] = 0;
   for (int k = 0; k < kMaxLayers; ++k) {
     ma.l[k] = l[k < n ? k : 0];
@@ -637,7 +683,7 @@ int launch_t(const LinearArgs* l, int n, hipStream_t s, void* work, long long wo
       return -1;
     attr = dyn;
   }
-  int* cnt = P > 1 ? (int*)work : nullptr;
+  int* cnt = P > 1 || act ? (int*)work : nullptr;
   float* part = P > 1 ? (float*)((char*)work + kCntBytes) : nullptr;
   kern<<<grid, (S + 1) * 64, dyn, s>>>(ma, P, T1, cnt, part);
   return 0;
@@ -647,9 +693,15 @@ int launch_t(const LinearArgs* l, int n, hipStream_t s, void* work, long long wo
 
 // Returns 0 if launched, -1 if the layers are outside this kernel's range
 // (then the vector decode kernel or the generic matvec takes them).
-int launch_decode_mfma_multi(const LinearArgs* l, int n, hipStream_t s, void* work, long long work_bytes) {
+int launch_decode_mfma_multi(const LinearArgs* l, int n, hipStream_t s, void* work, long long work_bytes,
+                             uint16_t* act) {
   if (n < 1 || n > kMaxLayers) return -1;
   const LinearArgs& a = l[0];
+  // SwiGLU: gate and up of equal M, up's outputs right after gate's, fp16,
+  // 4-byte aligned act, no residual.
+  if (act && (n != 2 || l[1].M != a.M || l[1].y != a.y + 8 * (size_t)a.M || l[1].ldy != a.ldy || a.x_bf16 ||
+              a.res || l[1].res || ((uintptr_t)act & 3) != 0))
+    return -1;
   if (a.B < 1 || a.B > 16 || a.codes_f32 || (a.N & 7) != 0) return -1;
   // prep 1 (the norm at the output; no residual add before it, no xsum) and
   // the residual: fp16 x, B <= 8, whole 64-column blocks (so Σx² sees no
@@ -678,18 +730,18 @@ int launch_decode_mfma_multi(const LinearArgs* l, int n, hipStream_t s, void* wo
   // workgroups: gate|up 11008x4096 at B=8 24.6 us against 22.2 us.)
   using namespace dmf;
   const bool xh = a.B <= 8;
-  if (norm) return a.S ? launch_t<kS, true, f16, true, true>(l, n, s, work, work_bytes)
-                       : launch_t<kS, false, f16, true, true>(l, n, s, work, work_bytes);
+  if (norm) return a.S ? launch_t<kS, true, f16, true, true>(l, n, s, work, work_bytes, act)
+                       : launch_t<kS, false, f16, true, true>(l, n, s, work, work_bytes, act);
   if (a.x_bf16) {
-    if (a.S) return xh ? launch_t<kS, true, bf16, true>(l, n, s, work, work_bytes)
-                       : launch_t<kS, true, bf16, false>(l, n, s, work, work_bytes);
-    return xh ? launch_t<kS, false, bf16, true>(l, n, s, work, work_bytes)
-              : launch_t<kS, false, bf16, false>(l, n, s, work, work_bytes);
+    if (a.S) return xh ? launch_t<kS, true, bf16, true>(l, n, s, work, work_bytes, act)
+                       : launch_t<kS, true, bf16, false>(l, n, s, work, work_bytes, act);
+    return xh ? launch_t<kS, false, bf16, true>(l, n, s, work, work_bytes, act)
+              : launch_t<kS, false, bf16, false>(l, n, s, work, work_bytes, act);
   }
-  if (a.S) return xh ? launch_t<kS, true, f16, true>(l, n, s, work, work_bytes)
-                     : launch_t<kS, true, f16, false>(l, n, s, work, work_bytes);
-  return xh ? launch_t<kS, false, f16, true>(l, n, s, work, work_bytes)
-            : launch_t<kS, false, f16, false>(l, n, s, work, work_bytes);
+  if (a.S) return xh ? launch_t<kS, true, f16, true>(l, n, s, work, work_bytes, act)
+                     : launch_t<kS, true, f16, false>(l, n, s, work, work_bytes, act);
+  return xh ? launch_t<kS, false, f16, true>(l, n, s, work, work_bytes, act)
+            : launch_t<kS, false, f16, false>(l, n, s, work, work_bytes, act);
 }
 
 long long decode_mfma_work_bytes() {

@@ -69,6 +69,11 @@ struct MultiArgs {
   LinearArgs l[kMaxLayers];
   int start[kMaxLayers + 1];
   int n;
+  // Matrix-core kernel only (null elsewhere): with two layers gate and up of
+  // equal M whose outputs sit side by side in y, also act (B, 8M) =
+  // silu(gate) ⊙ up, written by whichever of a row tile's two workgroups
+  // finishes last.
+  uint16_t* act;
 };
 
 template <int KIND> int launch_dequant(const DequantArgs& a, hipStream_t s);
@@ -101,9 +106,11 @@ int launch_decode_e8d4_pair(const LinearArgs* layers, hipStream_t s);
 
 // Matrix-core E8-D4 decode (B <= 16, fp16 or bf16 x, fp16 table; prep 1 and a
 // residual for fp16 x, B <= 8, N a multiple of 64);
-// -1 when the layers are outside its range.
+// -1 when the layers are outside its range.  act (fp16 x, n = 2, equal M,
+// layers[1].y = layers[0].y + 8M, a workspace): also act (B, 8M) =
+// silu(gate) ⊙ up with the roundings of the separate SwiGLU kernel.
 int launch_decode_mfma_multi(const LinearArgs* layers, int n, hipStream_t s, void* work = nullptr,
-                             long long work_bytes = 0);
+                             long long work_bytes = 0, uint16_t* act = nullptr);
 // Split-K workspace of the matrix-core decode kernel: kSplitCounters int
 // arrival counters (one per 64-row tile of a launch), then fp32 partial sums,
 // kSplitPartBytes per (split tile, part): [16 batch rows][64 outputs], then

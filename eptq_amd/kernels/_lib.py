@@ -49,6 +49,7 @@ LLAMA_SIGNATURES = {
     "eptq_llama_norm_linear": ([_I, _P, _P, _P, _P, _P, _F, _P, _I, _I, _P, _I, _P], _I),
     "eptq_llama_norm_swiglu": ([_P, _P, _P, _P, _P, _F, _P, _I, _I, _P, _P], _I),
     "eptq_llama_linear": ([_I, _P, _P, _P, _I, _I, _P, _F, _P, _P, _I, _P, ctypes.c_longlong, _P], _I),
+    "eptq_llama_linear_swiglu": ([_P, _P, _P, _I, _I, _P, _F, _P, _P, _P, ctypes.c_longlong, _P], _I),
     "eptq_llama_lm_head_work_bytes": ([_I], ctypes.c_longlong),
     "eptq_llama_lm_head_argmax": ([_P, _P, _P, _F, _P, _I, _I, _I, _P, _P, _P, _P, _P], _I),
 }

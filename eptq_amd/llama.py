@@ -7,10 +7,11 @@ every decoder Linear (q/k/v/o, gate/up/down) a synthetic E8-D4
 ``QuantizedLayerData`` and the embedding, norms and ``lm_head`` random fp16
 (the reference keeps ``lm_head`` unquantized, ``quantize.py:86-90``).
 
-Decode step (one token per sequence), 6 launches per layer: q|k|v with the
-residual add and RMSNorm formed inside the launch (one multi-layer decode
-launch) -> rotary + cache write + attention (one kernel) -> o -> gate|up with
-the residual add and RMSNorm inside -> SiLU·up -> down.  Shapes are
+Decode step (one token per sequence), 5 launches per layer: q|k|v with the
+RMSNorm formed inside the launch (one multi-layer decode launch) -> rotary +
+cache write + attention (one kernel) -> o -> gate|up with the RMSNorm inside
+and silu(gate)·up at its output -> down, the residual adds inside the o and
+down launches (B <= 2: inside the q|k|v and gate|up launches).  Shapes are
 static (preallocated cache, position in a device tensor), so the step is
 captured once in a HIP graph and replayed.
 Prefill (many tokens) runs the same Linears (MFMA GEMM) and PyTorch attention.
@@ -307,6 +308,25 @@ class QuantLlama(nn.Module):
         _lib.check(rc, "eptq_llama_linear")
         return y
 
+    def _llin_swiglu(self, mod, x, norm_w):
+        """silu(gate(t)) * up(t), t = RMSNorm(x) with weight norm_w, on the
+        matrix-core decode kernel with the product formed in the same launch
+        (``eptq_llama_linear_swiglu``, which needs the step's workspace);
+        without a workspace the gate|up launch and the SiLU kernel."""
+        work = getattr(self, "lin_work", None)
+        if work is None:
+            return silu_mul(self._llin(mod, x, norm_w=norm_w))
+        arr, width = _cached_array(mod)
+        B, N = x.shape
+        gu = torch.empty((B, width), dtype=x.dtype, device=x.device)
+        act = torch.empty((B, width // 2), dtype=x.dtype, device=x.device)
+        rc = _lib.load().eptq_llama_linear_swiglu(
+            arr, _parts(mod)[0]._codebook.data_ptr(), x.data_ptr(), N, B,
+            None if norm_w is None else norm_w.data_ptr(), self.cfg.eps, gu.data_ptr(), act.data_ptr(),
+            work.data_ptr(), work.numel(), _stream(x))
+        _lib.check(rc, "eptq_llama_linear_swiglu")
+        return act
+
     def _norm_into(self, mod, x, delta, w):
         """mod(RMSNorm(x + delta)) and the residual x + delta (a new tensor when
         fused; x itself, updated in place, on the separate-launch path)."""
@@ -347,8 +367,8 @@ class QuantLlama(nn.Module):
 
     def _matrix_core_step(self, B):
         """Whether a decode step of B rows runs its Linears on the matrix-core
-        kernel with the norms and residual adds folded in (6 launches per
-        layer): 3 <= B <= 8, fp16, hidden a multiple of 64."""
+        kernel with the norms, residual adds and SwiGLU product folded in (5
+        launches per layer): 3 <= B <= 8, fp16, hidden a multiple of 64."""
         return (self.fused_ops and 3 <= B <= 8 and self.cfg.hidden % 64 == 0
                 and self.embed_tokens.weight.dtype == torch.float16)
 
@@ -378,7 +398,7 @@ class QuantLlama(nn.Module):
             _lib.check(rc, "eptq_llama_rope_attn")
             if mc:
                 self._llin(layer.o_proj, att, resid=x)                 # x += o(att)
-                act = silu_mul(self._llin(layer.gate_up_proj, x, norm_w=ln2))
+                act = self._llin_swiglu(layer.gate_up_proj, x, ln2)
                 self._llin(layer.down_proj, act, resid=x)              # x += down(act)
                 continue
             o = self._lin(layer.o_proj, att)

@@ -92,6 +92,22 @@ int eptq_llama_linear(int n_layers, const eptq_layer* layers, const void* codes,
                       const void* norm_w, float eps, const void* resid, void* y, int ldy, void* work,
                       long long work_bytes, void* stream);
 
+/* eptq_llama_linear for the feed-forward gate and up layers with the SwiGLU
+ * product in the same launch: gu (B, 2F) fp16 = [gate(t) | up(t)] as
+ * eptq_llama_linear writes them (F = 8·M, the layers' y_offset fields are
+ * not used), and out (B, F) = silu(gate) ⊙ up, bit-identical to
+ * eptq_llama_linear followed by eptq_llama_silu_mul.  Whichever of a row
+ * tile's two workgroups finishes second forms the product, meeting the
+ * other at a counter in work, which is required (as in eptq_llama_linear;
+ * the counters return to zero).  out 4-byte aligned, not overlapping gu or
+ * x.  EPTQ_EUNSUPPORTED where eptq_llama_linear is, for a work buffer
+ * smaller than its counter area, or for tile counts past it.  No
+ * counterpart in the reference, whose decode step runs the gate and up
+ * Linears and the SiLU product as separate operators (bench_decode.py). */
+int eptq_llama_linear_swiglu(const eptq_layer* gate_up, const void* codes, const void* x, int N, int B,
+                             const void* norm_w, float eps, void* gu, void* out, void* work, long long work_bytes,
+                             void* stream);
+
 /* Bytes of the eptq_llama_lm_head_argmax workspace for B batch rows
  * (zero-filled before its first use; every call leaves it zeroed). */
 long long eptq_llama_lm_head_work_bytes(int B);

@@ -190,6 +190,16 @@ def test_fused_llama_linears_validate_arguments(lib):
     pair[1].M = 8
     assert g(pair, 16, 16, None, 16, 1e-5, None, 64, 1, 16, None) == _lib.EPTQ_EINVAL             # M differ
     assert "differ" in lib.eptq_last_error().decode()
+    pair[1].M = 4
+    sw = lib.eptq_llama_linear_swiglu   # gate_up, codes, x, N, B, norm_w, eps, gu, out, work, work_bytes, stream
+    assert sw(None, 16, 16, 64, 1, 16, 1e-5, 4096, 8192, 16, 1 << 20, None) == _lib.EPTQ_EINVAL   # no layers
+    assert sw(pair, 16, 16, 64, 1, 16, 1e-5, 4096, 8192, None, 0, None) == _lib.EPTQ_EINVAL      # no work
+    assert "workspace" in lib.eptq_last_error().decode()
+    assert sw(pair, 16, 16, 64, 1, 16, 1e-5, 4096, 4096, 16, 1 << 20, None) == _lib.EPTQ_EINVAL  # out == gu
+    assert sw(pair, 16, 16, 64, 1, 16, 1e-5, 4096, 8194, 16, 1 << 20, None) == _lib.EPTQ_EUNSUPPORTED  # out align
+    assert sw(pair, 16, 16, 64, 0, 16, 1e-5, 4096, 8192, 16, 1 << 20, None) == _lib.EPTQ_OK      # B = 0
+    pair[1].M = 8
+    assert sw(pair, 16, 16, 64, 1, 16, 1e-5, 4096, 8192, 16, 1 << 20, None) == _lib.EPTQ_EINVAL  # M differ
     h = lib.eptq_llama_lm_head_argmax
     assert lib.eptq_llama_lm_head_work_bytes(2) >= 24
     assert h(None, None, 16, 1e-5, 16, 100, 4096, 1, 16, 16, None, 16, None) == 1          # null x

@@ -138,3 +138,44 @@ def test_llama_linear_norm_unsupported():
     x2 = make_x(4, 1000, seed=3).cuda()
     rc, _ = _call(lins2, x2, norm_w=_norm_w(1000, seed=2).cuda())
     assert rc == _lib.EPTQ_EUNSUPPORTED
+
+
+def _swiglu(lins, x, norm_w, work):
+    arr, width = _layer_array(lins)
+    B, N = x.shape
+    gu = torch.empty((B, width), dtype=torch.float16, device="cuda")
+    act = torch.empty((B, width // 2), dtype=torch.float16, device="cuda")
+    rc = _lib.load().eptq_llama_linear_swiglu(
+        arr, lins[0]._codebook.data_ptr(), x.data_ptr(), N, B, None if norm_w is None else norm_w.data_ptr(), EPS,
+        gu.data_ptr(), act.data_ptr(), work.data_ptr(), work.numel(), torch.cuda.current_stream().cuda_stream)
+    _lib.check(rc, "eptq_llama_linear_swiglu")
+    return gu, act
+
+
+@pytest.mark.parametrize("F,N,Bs,norm", [
+    (11008, 4096, (8, 5), True),    # Llama-2-7B gate|up: 344 tiles, whole then split over parts
+    (1024, 1024, (3, 2), False),    # 32 tiles, every tile split
+    (2048, 2048, (16, 9), False),   # B = 16
+    (512, 1024, (4, 3), True),
+])
+def test_llama_linear_swiglu(F, N, Bs, norm):
+    """The SwiGLU form: gu bit-identical to eptq_llama_linear, the product
+    bit-identical to eptq_llama_silu_mul of it, on two calls in a row (the
+    second smaller: the pair counters return to zero)."""
+    from eptq_amd.llama import silu_mul
+    _, lins = _lins([(F, N), (F, N)], seed=F + N)
+    w = _norm_w(N, seed=N + 1).cuda() if norm else None
+    work = decode_workspace("cuda")
+    for B in Bs:
+        print(f"eptq_llama_linear_swiglu F={F} N={N} B={B} norm={norm}", flush=True)
+        x = (make_x(B, N, seed=B + 3) * 2).cuda()
+        gu, act = _swiglu(lins, x, w, work)
+        rc, want_gu = _call(lins, x, norm_w=w, work=work)
+        _lib.check(rc, "eptq_llama_linear")
+        want_act = silu_mul(want_gu)
+        torch.cuda.synchronize()
+        assert torch.equal(gu, want_gu)
+        assert torch.equal(act, want_act)
+        assert torch.isfinite(act.float()).all() and act.float().abs().max() > 0
+    tiles = 2 * ((F // 8 + 7) // 8)
+    assert int(work[: 4 * (tiles + tiles // 2)].view(torch.int32).abs().sum()) == 0

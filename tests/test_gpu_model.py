@@ -206,18 +206,21 @@ def test_fused_norm_matches_separate_launches():
     gate|up launches against the same step with the norms as launches of
     their own (the fused entry points must really run: no fallback; gate|up
     takes the SwiGLU launch for B <= 2; for 3 <= B <= 8 every Linear runs on
-    eptq_llama_linear, the norms folded into q|k|v and gate|up and the
-    residual adds into o and down)."""
+    the matrix-core kernel, the norms folded into q|k|v and gate|up, the
+    SwiGLU product into gate|up (eptq_llama_linear_swiglu) and the residual
+    adds into o and down)."""
     from eptq_amd.llama import LlamaConfig, build_synthetic
     import eptq_amd.llama as LL
     print("synthetic llama: fused norm vs separate launches", flush=True)
     calls, swiglu, mc = [], [], []
     real, real_sw, real_llin = LL.norm_linear, LL.norm_swiglu, LL.QuantLlama._llin
+    real_llsw = LL.QuantLlama._llin_swiglu
     LL.norm_linear = lambda *a, **k: (calls.append(1), real(*a, **k))[1]
     LL.norm_swiglu = lambda *a, **k: (swiglu.append(1), real_sw(*a, **k))[1]
     LL.QuantLlama._llin = lambda self, mod, x, norm_w=None, resid=None: (
         mc.append("norm" if norm_w is not None else "resid" if resid is not None else "plain"),
         real_llin(self, mod, x, norm_w=norm_w, resid=resid))[1]
+    LL.QuantLlama._llin_swiglu = lambda self, mod, x, norm_w: (mc.append("swiglu"), real_llsw(self, mod, x, norm_w))[1]
     for kv, B in ((4, 1), (2, 3), (4, 8)):
         cfg = LlamaConfig(hidden=512, ffn=1024, layers=2, heads=4, kv_heads=kv, vocab=256)
         model = build_synthetic(cfg, device="cuda", seed=13 + B)
@@ -244,11 +247,13 @@ def test_fused_norm_matches_separate_launches():
             assert len(swiglu) == cfg.layers and len(calls) == cfg.layers and not mc, "fused path for every norm"
         else:
             assert not swiglu and not calls, B
-            assert mc.count("norm") == 2 * cfg.layers and mc.count("resid") == 2 * cfg.layers, mc
+            assert mc.count("norm") == cfg.layers and mc.count("swiglu") == cfg.layers, mc
+            assert mc.count("resid") == 2 * cfg.layers, mc
         calls.clear()
         swiglu.clear()
         mc.clear()
     LL.norm_linear, LL.norm_swiglu, LL.QuantLlama._llin = real, real_sw, real_llin
+    LL.QuantLlama._llin_swiglu = real_llsw
 
 
 def test_split_attention_matches_single_workgroup():
