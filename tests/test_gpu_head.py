@@ -42,7 +42,8 @@ def _work(B):
 
 @pytest.mark.parametrize("B,H,V,delta", [(1, 4096, 32000, True), (2, 4096, 1000, True), (1, 8192, 777, False),
                                          (2, 6144, 64, True), (3, 4096, 2000, True), (8, 4096, 32000, True),
-                                         (5, 8192, 513, False), (8, 6144, 100, True)])
+                                         (5, 8192, 513, False), (8, 6144, 100, True),
+                                         (8, 4096, 1537, False), (4, 4096, 5001, True)])
 def test_head_matches_fp32_reference(B, H, V, delta):
     print(f"lm_head+argmax B={B} H={H} V={V} delta={delta}", flush=True)
     x, d, w, W = _setup(B, H, V, seed=B + H + V, delta=delta)
