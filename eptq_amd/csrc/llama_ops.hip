@@ -405,7 +405,6 @@ __global__ __launch_bounds__(kT) void k_silu_mul(const f16* __restrict__ gu, f16
 // atomic count) writes tok[b], adds 1 to *pos (if given) and clears the keys
 // and the count for the next call.  The next row is requested before the
 // current one is summed (two rows in flight per wave).
-constexpr int kHeadPerCu = 2;   // workgroups per CU
 
 __device__ __forceinline__ unsigned long long head_key(f16 v, int idx) {
   const uint32_t b = __builtin_bit_cast(uint16_t, v);
@@ -561,7 +560,11 @@ int launch_head(const f16* x, const f16* delta, const f16* w, float eps, const f
                 int64_t* tok, int64_t* pos, unsigned long long* keys, int* cnt, hipStream_t s) {
   int dev = 0, cus = 256;
   if (hipGetDevice(&dev) == hipSuccess) (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-  int G = cus * kHeadPerCu;
+  // Workgroups per CU: one for B <= 2 (t in registers; every extra workgroup
+  // repeats the norm prologue: 46 us against 53 with two, 86 with four, for
+  // the Llama-2-7B lm_head at B = 1), two above (t read from LDS: 77.5 us
+  // against 109 with one at B = 8).
+  int G = cus * (B <= 2 ? 1 : 2);
   const int rows_per_wg = kT / 64;
   if (G * rows_per_wg > V) G = (V + rows_per_wg - 1) / rows_per_wg;
   auto kern = k_lm_head_argmax<B, CH>;
